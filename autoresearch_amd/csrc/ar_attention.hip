@@ -1,0 +1,623 @@
+// ar_attention.hip -- flash attention forward and backward on the gfx950
+// matrix cores, for the reference's flash_attn_fwd (ops.mojo:244-323),
+// flash_attn_bwd_dq (ops.mojo:349-411) and flash_attn_bwd_dkv
+// (ops.mojo:414-480).
+//
+// Layout: q, k, v, O, dO are [B, T, H, hd] (token-major, heads interleaved:
+// row stride H*hd), LSE and D are [B, T, H].  Key kp is visible from query qp
+// iff kp <= qp and (window <= 0 or kp >= qp - window).
+//
+// Work decomposition (all three kernels): a workgroup of 4 wave64s owns 128
+// rows of one (b, h) -- queries for fwd / dQ, keys for dK/dV -- 32 per wave,
+// and streams 64-row tiles of the other side through LDS, skipping tiles that
+// the causal / sliding-window mask removes entirely.
+//
+// MFMA mapping.  Products are formed transposed so the 32 rows a wave owns
+// are the MFMA *columns*: e.g. the forward computes S^T = K Q^T, where lane l
+// holds query l%32 and 16 keys.  Softmax statistics are then per-lane values
+// (two lanes, l and l^32, share a query).  The P (or dS) tile is fed straight
+// back as the B operand of the next product (O^T += V^T P^T) without leaving
+// registers: the MFMA accumulator layout hands each lane a permuted subset of
+// keys, and the A operand (V^T, K^T, dO^T, Q^T) is read from LDS in that same
+// permuted key order.  bf16 compute (v_mfma_f32_32x32x16_bf16) reads the
+// permuted operand from a transposed [d][row] LDS copy; fp32 compute
+// (v_mfma_f32_32x32x2_f32) reads it straight from the [row][d] tile.
+//
+// dK/dV are accumulated by key-block ownership and dQ by query-block
+// ownership (two kernels, no atomics: deterministic).  Softmax runs in the
+// exp2 domain with the 1/sqrt(hd) scale and log2(e) folded into one multiply.
+#include "ar_internal.hpp"
+
+using namespace ar;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kOwn = 128;  // rows owned by a workgroup (4 waves x 32)
+constexpr int kTile = 64;  // rows per streamed LDS tile
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ int acc_row(int v, int lane) { return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); }
+
+template <bool BF16> struct AT;
+
+template <> struct AT<true> {
+    using LT = bf16;
+    using Frag = bf16x8;
+    static constexpr int KS = 16, CW = 8, PADN = 8, LDT = kTile + 8, STEPS32 = 2;
+    static constexpr bool TRANS = true;
+    __device__ static f32x16 mma(Frag a, Frag b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    // Operand fragment of a row stored d-contiguous: k-step ks.
+    __device__ static Frag rowfrag(const LT* row, int ks, int lane) {
+        return *reinterpret_cast<const bf16x8*>(row + ks * KS + (lane >> 5) * 8);
+    }
+    // A operand in permuted row order for k-step s of 32-row block kb:
+    // rows {32kb + 16s + 4g + 0..3, 32kb + 16s + 8 + 4g + 0..3}, g = lane/32.
+    // `tr` is the transposed LDS tile, [d][row] with row stride LDT.
+    __device__ static Frag permfrag(const LT* natural, int ldn, const LT* tr, int d, int kb, int s, int lane) {
+        (void)natural;
+        (void)ldn;
+        const int g = lane >> 5;
+        const LT* p = tr + d * LDT + kb * 32 + 16 * s + 4 * g;
+        bf16x4 lo = *reinterpret_cast<const bf16x4*>(p);
+        bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + 8);
+        Frag f;
+        f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
+        f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
+        return f;
+    }
+    // B operand from the lane's own accumulator values, k-step s.
+    __device__ static Frag accfrag(const f32x16& a, int s) {
+        Frag f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = (bf16)a[8 * s + e];
+        return f;
+    }
+};
+
+template <> struct AT<false> {
+    using LT = float;
+    using Frag = float;
+    static constexpr int KS = 2, CW = 4, PADN = 4, LDT = 4, STEPS32 = 16;
+    static constexpr bool TRANS = false;
+    __device__ static f32x16 mma(Frag a, Frag b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+    }
+    __device__ static Frag rowfrag(const LT* row, int ks, int lane) { return row[ks * KS + (lane >> 5)]; }
+    // row {32kb + 8(s/4) + 4g + s%4}, read from the natural [row][d] tile.
+    __device__ static Frag permfrag(const LT* natural, int ldn, const LT* tr, int d, int kb, int s, int lane) {
+        (void)tr;
+        const int r = kb * 32 + (s >> 2) * 8 + (lane >> 5) * 4 + (s & 3);
+        return natural[r * ldn + d];
+    }
+    __device__ static Frag accfrag(const f32x16& a, int s) { return a[s]; }
+};
+
+// Load rows [row0, row0 + 64) of a [T, rs]-strided operand (columns [0, HD))
+// into LDS: natural [row][HD + PADN] and, for bf16, transposed [HD][LDT].
+// Rows at or beyond T are zero.
+template <bool BF16, int HD, typename TIN>
+__device__ __forceinline__ void load_tile(typename AT<BF16>::LT* nat, typename AT<BF16>::LT* tr, const TIN* base,
+                                          int64_t rs, int row0, int T, bool want_tr) {
+    using A = AT<BF16>;
+    using LT = typename A::LT;
+    constexpr int CW = A::CW, LDN = HD + A::PADN;
+    constexpr int ITEMS = (kTile / 4) * (HD / CW);  // 4 rows x CW columns per item
+    for (int it = threadIdx.x; it < ITEMS; it += kThreads) {
+        const int r4 = it % (kTile / 4), dc = (it / (kTile / 4)) * CW;
+        LT vals[4][CW];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = r4 * 4 + i;
+            if (row0 + r < T) {
+                const TIN* src = base + (int64_t)(row0 + r) * rs + dc;
+                if constexpr (sizeof(TIN) == 4) {
+                    float tmp[CW];
+#pragma unroll
+                    for (int j = 0; j < CW; j += 4) *reinterpret_cast<float4*>(tmp + j) =
+                        *reinterpret_cast<const float4*>(src + j);
+#pragma unroll
+                    for (int j = 0; j < CW; ++j) vals[i][j] = (LT)tmp[j];
+                } else {
+                    static_assert(BF16, "bf16 storage needs bf16 compute");
+                    *reinterpret_cast<uint4*>(vals[i]) = *reinterpret_cast<const uint4*>(src);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < CW; ++j) vals[i][j] = (LT)0.0f;
+            }
+            if (nat)
+                *reinterpret_cast<uint4*>(nat + (r4 * 4 + i) * LDN + dc) = *reinterpret_cast<const uint4*>(vals[i]);
+        }
+        if constexpr (A::TRANS) {
+            if (want_tr) {
+#pragma unroll
+                for (int j = 0; j < CW; ++j) {
+                    bf16x4 col;
+                    col[0] = vals[0][j]; col[1] = vals[1][j]; col[2] = vals[2][j]; col[3] = vals[3][j];
+                    *reinterpret_cast<bf16x4*>(tr + (dc + j) * A::LDT + r4 * 4) = col;
+                }
+            }
+        }
+    }
+}
+
+// Load the 32 rows [r0, r0+32) of an operand as B fragments (lane row r0 + l%32).
+template <bool BF16, int HD, typename TIN>
+__device__ __forceinline__ void load_bfrags(typename AT<BF16>::Frag (&f)[HD / AT<BF16>::KS], const TIN* base,
+                                            int64_t rs, int row, int T, int lane) {
+    using A = AT<BF16>;
+#pragma unroll
+    for (int ks = 0; ks < HD / A::KS; ++ks) {
+        if constexpr (BF16) {
+            typename A::Frag fr;
+            if (row < T) {
+                const TIN* src = base + (int64_t)row * rs + ks * A::KS + (lane >> 5) * 8;
+                if constexpr (sizeof(TIN) == 4) {
+                    float4 a = *reinterpret_cast<const float4*>(src);
+                    float4 b = *reinterpret_cast<const float4*>(src + 4);
+                    fr[0] = (bf16)a.x; fr[1] = (bf16)a.y; fr[2] = (bf16)a.z; fr[3] = (bf16)a.w;
+                    fr[4] = (bf16)b.x; fr[5] = (bf16)b.y; fr[6] = (bf16)b.z; fr[7] = (bf16)b.w;
+                } else {
+                    fr = *reinterpret_cast<const bf16x8*>(src);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) fr[e] = (bf16)0.0f;
+            }
+            f[ks] = fr;
+        } else {
+            f[ks] = row < T ? (float)base[(int64_t)row * rs + ks * A::KS + (lane >> 5)] : 0.0f;
+        }
+    }
+}
+
+// Write a wave's transposed accumulator tiles (rows d, columns = the wave's 32
+// rows) as [row][d] output rows, scaled, through a wave-private LDS scratch.
+template <int HD, typename TOUT>
+__device__ __forceinline__ void store_rows_T(TOUT* out, int64_t rs, int row_base, int T, const f32x16 (&acc)[HD / 32],
+                                             float scale, float* scratch, int lane) {
+    // scratch: 32 x 36 floats per wave
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) scratch[(lane & 31) * 36 + acc_row(v, lane)] = acc[dt][v] * scale;
+        __syncthreads();
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass) {
+            const int r = pass * 8 + lane / 8, c4 = (lane % 8) * 4;
+            const int row = row_base + r;
+            if (row < T) {
+                float4 x = *reinterpret_cast<const float4*>(scratch + r * 36 + c4);
+                TOUT* dst = out + (int64_t)row * rs + dt * 32 + c4;
+                if constexpr (sizeof(TOUT) == 4) {
+                    *reinterpret_cast<float4*>(dst) = x;
+                } else {
+                    dst[0] = (TOUT)x.x; dst[1] = (TOUT)x.y; dst[2] = (TOUT)x.z; dst[3] = (TOUT)x.w;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <bool BF16, int HD>
+constexpr int lds_tile_elems() {
+    using A = AT<BF16>;
+    return kTile * (HD + A::PADN) + (A::TRANS ? HD * A::LDT : 0);
+}
+
+// ============================ forward ============================
+template <bool BF16, int HD, typename TIN>
+__global__ __launch_bounds__(kThreads) void fa_fwd_k(float* out, float* lse, const TIN* q, const TIN* k, const TIN* v,
+                                                     int B, int T, int H, int window, float scale_log2) {
+    using A = AT<BF16>;
+    using LT = typename A::LT;
+    constexpr int LDN = HD + A::PADN;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    LT* sK = reinterpret_cast<LT*>(smem_raw);
+    LT* sV = sK + kTile * LDN;                                  // natural V (fp32 path)
+    LT* sVT = sK + kTile * LDN;                                 // transposed V (bf16 path)
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int bh = blockIdx.y, b = bh / H, h = bh % H;
+    const int q0 = blockIdx.x * kOwn, qw = q0 + wave * 32, my_q = qw + (lane & 31);
+    const int64_t rs = (int64_t)H * HD;
+    const int64_t boff = (int64_t)b * T * rs + (int64_t)h * HD;
+
+    typename A::Frag qf[HD / A::KS];
+    load_bfrags<BF16, HD>(qf, q + boff, rs, my_q, T, lane);
+
+    f32x16 o[HD / 32];
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+    float m = -INFINITY, l = 0.f;
+
+    int kstart = 0;
+    if (window > 0) kstart = q0 - window > 0 ? q0 - window : 0;
+    kstart = (kstart / kTile) * kTile;
+    const int kend = (q0 + kOwn < T) ? q0 + kOwn : T;
+    for (int kv0 = kstart; kv0 < kend; kv0 += kTile) {
+        load_tile<BF16, HD>(sK, nullptr, k + boff, rs, kv0, T, false);
+        load_tile<BF16, HD>(A::TRANS ? nullptr : sV, A::TRANS ? sVT : nullptr, v + boff, rs, kv0, T, true);
+        __syncthreads();
+        const bool skip = kv0 > qw + 31 || (window > 0 && kv0 + kTile - 1 < qw - window) || qw >= T;
+        if (!skip) {
+            f32x16 s[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
+                const LT* krow = sK + (kb * 32 + (lane & 31)) * LDN;
+#pragma unroll
+                for (int ks = 0; ks < HD / A::KS; ++ks) s[kb] = A::mma(A::rowfrag(krow, ks, lane), qf[ks], s[kb]);
+            }
+            float mt = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int key = kv0 + kb * 32 + acc_row(e, lane);
+                    const bool ok = key <= my_q && key < T && (window <= 0 || key >= my_q - window);
+                    const float x = ok ? s[kb][e] * scale_log2 : -INFINITY;
+                    s[kb][e] = x;
+                    mt = fmaxf(mt, x);
+                }
+            mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+            const float m_new = fmaxf(m, mt);
+            const float m_use = m_new == -INFINITY ? 0.f : m_new;
+            const float alpha = exp2f(m - m_use);
+            float rsum = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float p = exp2f(s[kb][e] - m_use);
+                    s[kb][e] = p;
+                    rsum += p;
+                }
+            rsum += __shfl_xor(rsum, 32, kWave);
+            l = l * alpha + rsum;
+            m = m_new;
+#pragma unroll
+            for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int st = 0; st < A::STEPS32; ++st) {
+                    const typename A::Frag pb = A::accfrag(s[kb], st);
+#pragma unroll
+                    for (int dt = 0; dt < HD / 32; ++dt) {
+                        const int d = dt * 32 + (lane & 31);
+                        o[dt] = A::mma(A::permfrag(sV, LDN, sVT, d, kb, st, lane), pb, o[dt]);
+                    }
+                }
+        }
+        __syncthreads();
+    }
+    const float inv_l = l > 0.f ? 1.0f / l : 0.f;
+    if (lane < 32 && my_q < T)
+        lse[((int64_t)b * T + my_q) * H + h] = l > 0.f ? (m + log2f(l)) * kLn2 : -INFINITY;
+    float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 36;
+    // Output scale is per query (per lane); fold it before staging.
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[dt][e] *= inv_l;
+    store_rows_T<HD>(out + boff, rs, qw, T, o, 1.0f, scratch, lane);
+}
+
+// ============================ backward: dQ ============================
+template <bool BF16, int HD, typename TIN>
+__global__ __launch_bounds__(kThreads) void fa_bwd_dq_k(float* dq, const TIN* q, const TIN* k, const TIN* v,
+                                                        const TIN* dout, const float* lse, const float* dbuf, int B,
+                                                        int T, int H, int window, float scale_log2, float scale) {
+    using A = AT<BF16>;
+    using LT = typename A::LT;
+    constexpr int LDN = HD + A::PADN;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    LT* sK = reinterpret_cast<LT*>(smem_raw);
+    LT* sKT = sK + kTile * LDN;
+    LT* sV = sKT + (A::TRANS ? HD * A::LDT : 0);
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int bh = blockIdx.y, b = bh / H, h = bh % H;
+    const int q0 = blockIdx.x * kOwn, qw = q0 + wave * 32, my_q = qw + (lane & 31);
+    const int64_t rs = (int64_t)H * HD;
+    const int64_t boff = (int64_t)b * T * rs + (int64_t)h * HD;
+
+    typename A::Frag qf[HD / A::KS], df[HD / A::KS];
+    load_bfrags<BF16, HD>(qf, q + boff, rs, my_q, T, lane);
+    load_bfrags<BF16, HD>(df, dout + boff, rs, my_q, T, lane);
+    const int64_t bth = ((int64_t)b * T + (my_q < T ? my_q : 0)) * H + h;
+    const float my_lse2 = lse[bth] * kLog2e;
+    const float my_D = dbuf[bth];
+
+    f32x16 acc[HD / 32];
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[dt][e] = 0.f;
+
+    int kstart = 0;
+    if (window > 0) kstart = q0 - window > 0 ? q0 - window : 0;
+    kstart = (kstart / kTile) * kTile;
+    const int kend = (q0 + kOwn < T) ? q0 + kOwn : T;
+    for (int kv0 = kstart; kv0 < kend; kv0 += kTile) {
+        load_tile<BF16, HD>(sK, sKT, k + boff, rs, kv0, T, true);
+        load_tile<BF16, HD>(sV, nullptr, v + boff, rs, kv0, T, false);
+        __syncthreads();
+        const bool skip = kv0 > qw + 31 || (window > 0 && kv0 + kTile - 1 < qw - window) || qw >= T;
+        if (!skip) {
+            f32x16 s[2], dp[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) s[kb][e] = dp[kb][e] = 0.f;
+                const LT* krow = sK + (kb * 32 + (lane & 31)) * LDN;
+                const LT* vrow = sV + (kb * 32 + (lane & 31)) * LDN;
+#pragma unroll
+                for (int ks = 0; ks < HD / A::KS; ++ks) {
+                    s[kb] = A::mma(A::rowfrag(krow, ks, lane), qf[ks], s[kb]);
+                    dp[kb] = A::mma(A::rowfrag(vrow, ks, lane), df[ks], dp[kb]);
+                }
+            }
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int key = kv0 + kb * 32 + acc_row(e, lane);
+                    const bool ok = key <= my_q && key < T && my_q < T && (window <= 0 || key >= my_q - window);
+                    const float p = ok ? exp2f(s[kb][e] * scale_log2 - my_lse2) : 0.f;
+                    s[kb][e] = p * (dp[kb][e] - my_D);
+                }
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int st = 0; st < A::STEPS32; ++st) {
+                    const typename A::Frag db = A::accfrag(s[kb], st);
+#pragma unroll
+                    for (int dt = 0; dt < HD / 32; ++dt) {
+                        const int d = dt * 32 + (lane & 31);
+                        acc[dt] = A::mma(A::permfrag(sK, LDN, sKT, d, kb, st, lane), db, acc[dt]);
+                    }
+                }
+        }
+        __syncthreads();
+    }
+    float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 36;
+    store_rows_T<HD>(dq + boff, rs, qw, T, acc, scale, scratch, lane);
+}
+
+// ============================ backward: dK, dV ============================
+template <bool BF16, int HD, typename TIN>
+__global__ __launch_bounds__(kThreads) void fa_bwd_dkv_k(float* dk, float* dv, const TIN* q, const TIN* k,
+                                                         const TIN* v, const TIN* dout, const float* lse,
+                                                         const float* dbuf, int B, int T, int H, int window,
+                                                         float scale_log2, float scale) {
+    using A = AT<BF16>;
+    using LT = typename A::LT;
+    constexpr int LDN = HD + A::PADN;
+    constexpr int TE = lds_tile_elems<BF16, HD>();
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    LT* sQ = reinterpret_cast<LT*>(smem_raw);
+    LT* sQT = sQ + kTile * LDN;
+    LT* sD = sQ + TE;
+    LT* sDT = sD + kTile * LDN;
+    float* sL = reinterpret_cast<float*>(sQ + 2 * TE);
+    float* sDl = sL + kTile;
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int bh = blockIdx.y, b = bh / H, h = bh % H;
+    const int k0 = blockIdx.x * kOwn, kw = k0 + wave * 32, my_k = kw + (lane & 31);
+    const int64_t rs = (int64_t)H * HD;
+    const int64_t boff = (int64_t)b * T * rs + (int64_t)h * HD;
+
+    typename A::Frag kf[HD / A::KS], vf[HD / A::KS];
+    load_bfrags<BF16, HD>(kf, k + boff, rs, my_k, T, lane);
+    load_bfrags<BF16, HD>(vf, v + boff, rs, my_k, T, lane);
+
+    f32x16 dka[HD / 32], dva[HD / 32];
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) dka[dt][e] = dva[dt][e] = 0.f;
+
+    const int qstart = (k0 / kTile) * kTile;
+    int qend = T;
+    if (window > 0 && k0 + kOwn - 1 + window + 1 < T) qend = k0 + kOwn - 1 + window + 1;
+    for (int qt0 = qstart; qt0 < qend; qt0 += kTile) {
+        load_tile<BF16, HD>(sQ, sQT, q + boff, rs, qt0, T, true);
+        load_tile<BF16, HD>(sD, sDT, dout + boff, rs, qt0, T, true);
+        if (threadIdx.x < kTile) {
+            const int qq = qt0 + threadIdx.x;
+            const int64_t bth = ((int64_t)b * T + (qq < T ? qq : 0)) * H + h;
+            sL[threadIdx.x] = lse[bth] * kLog2e;
+            sDl[threadIdx.x] = dbuf[bth];
+        }
+        __syncthreads();
+        const bool skip = qt0 + kTile - 1 < kw || (window > 0 && qt0 > kw + 31 + window) || kw >= T;
+        if (!skip) {
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                f32x16 s, dp;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.f;
+                const LT* qrow = sQ + (qb * 32 + (lane & 31)) * LDN;
+                const LT* drow = sD + (qb * 32 + (lane & 31)) * LDN;
+#pragma unroll
+                for (int ks = 0; ks < HD / A::KS; ++ks) {
+                    s = A::mma(A::rowfrag(qrow, ks, lane), kf[ks], s);
+                    dp = A::mma(A::rowfrag(drow, ks, lane), vf[ks], dp);
+                }
+                // s, dp: lane holds key my_k, queries qt0 + 32qb + acc_row(e)
+                f32x16 p, ds;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int qr = qb * 32 + acc_row(e, lane);
+                    const int qq = qt0 + qr;
+                    const bool ok = my_k <= qq && qq < T && my_k < T && (window <= 0 || my_k >= qq - window);
+                    const float pv = ok ? exp2f(s[e] * scale_log2 - sL[qr]) : 0.f;
+                    p[e] = pv;
+                    ds[e] = pv * (dp[e] - sDl[qr]);
+                }
+#pragma unroll
+                for (int st = 0; st < A::STEPS32; ++st) {
+                    const typename A::Frag pb = A::accfrag(p, st);
+                    const typename A::Frag db = A::accfrag(ds, st);
+#pragma unroll
+                    for (int dt = 0; dt < HD / 32; ++dt) {
+                        const int d = dt * 32 + (lane & 31);
+                        dva[dt] = A::mma(A::permfrag(sD, LDN, sDT, d, qb, st, lane), pb, dva[dt]);
+                        dka[dt] = A::mma(A::permfrag(sQ, LDN, sQT, d, qb, st, lane), db, dka[dt]);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 36;
+    store_rows_T<HD>(dk + boff, rs, kw, T, dka, scale, scratch, lane);
+    store_rows_T<HD>(dv + boff, rs, kw, T, dva, 1.0f, scratch, lane);
+}
+
+template <bool BF16, int HD>
+size_t fwd_lds() {
+    using A = AT<BF16>;
+    size_t tiles = (size_t)(kTile * (HD + A::PADN) + (A::TRANS ? HD * A::LDT : kTile * (HD + A::PADN))) *
+                   sizeof(typename A::LT);
+    size_t stage = 4 * 32 * 36 * sizeof(float);
+    return tiles > stage ? tiles : stage;
+}
+template <bool BF16, int HD>
+size_t dq_lds() {
+    using A = AT<BF16>;
+    size_t tiles = (size_t)(2 * kTile * (HD + A::PADN) + (A::TRANS ? HD * A::LDT : 0)) * sizeof(typename A::LT);
+    size_t stage = 4 * 32 * 36 * sizeof(float);
+    return tiles > stage ? tiles : stage;
+}
+template <bool BF16, int HD>
+size_t dkv_lds() {
+    size_t tiles = (size_t)2 * lds_tile_elems<BF16, HD>() * sizeof(typename AT<BF16>::LT) + 2 * kTile * sizeof(float);
+    size_t stage = 4 * 32 * 36 * sizeof(float);
+    return tiles > stage ? tiles : stage;
+}
+
+}  // namespace
+
+namespace ar {
+
+template <bool BF16, int HD, typename TIN>
+static int32_t attn_dispatch_hd(hipStream_t st, AttnOp op, float* o1, float* o2, const TIN* q, const TIN* k,
+                                const TIN* v, const TIN* dout, const float* lse, const float* dbuf, int B, int T, int H,
+                                int window) {
+    const float scale = 1.0f / sqrtf((float)HD);
+    const float scale_log2 = scale * kLog2e;
+    dim3 grid((unsigned)((T + kOwn - 1) / kOwn), (unsigned)(B * H));
+    if (op == AttnOp::FWD) {
+        const size_t lds = fwd_lds<BF16, HD>();
+        fa_fwd_k<BF16, HD, TIN><<<grid, kThreads, lds, st>>>(o1, o2, q, k, v, B, T, H, window, scale_log2);
+        return check_launch("flash_attn_fwd");
+    }
+    if (op == AttnOp::DQ) {
+        const size_t lds = dq_lds<BF16, HD>();
+        fa_bwd_dq_k<BF16, HD, TIN><<<grid, kThreads, lds, st>>>(o1, q, k, v, dout, lse, dbuf, B, T, H, window,
+                                                                scale_log2, scale);
+        return check_launch("flash_attn_bwd_dq");
+    }
+    const size_t lds = dkv_lds<BF16, HD>();
+    fa_bwd_dkv_k<BF16, HD, TIN><<<grid, kThreads, lds, st>>>(o1, o2, q, k, v, dout, lse, dbuf, B, T, H, window,
+                                                             scale_log2, scale);
+    return check_launch("flash_attn_bwd_dkv");
+}
+
+template <bool BF16, typename TIN>
+int32_t attn_dispatch(hipStream_t st, AttnOp op, float* o1, float* o2, const TIN* q, const TIN* k, const TIN* v,
+                      const TIN* dout, const float* lse, const float* dbuf, int64_t B, int64_t T, int64_t H,
+                      int64_t HD, int64_t window) {
+    if (HD > 128) return set_error(AR_EUNSUPPORTED, "flash attention: head_dim %lld > 128", (long long)HD);
+    if (B <= 0 || T <= 0 || H <= 0) return B == 0 || T == 0 ? AR_OK : set_error(AR_EINVAL, "flash attention: bad shape");
+    if (B * H > 65535 || T > (1 << 30)) return set_error(AR_EINVAL, "flash attention: shape too large");
+    const int w = window > (int64_t)T ? (int)T : (int)window;  // a window >= T is full causal
+    switch (HD) {
+        case 32: return attn_dispatch_hd<BF16, 32, TIN>(st, op, o1, o2, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
+        case 64: return attn_dispatch_hd<BF16, 64, TIN>(st, op, o1, o2, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
+        case 128: return attn_dispatch_hd<BF16, 128, TIN>(st, op, o1, o2, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
+        default: return set_error(AR_EUNSUPPORTED, "flash attention: head_dim %lld not in {32, 64, 128}", (long long)HD);
+    }
+}
+
+}  // namespace ar
+
+static __host__ __device__ inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+#define AR_ATTN_PTRS(...)                                                                   \
+    do {                                                                                    \
+        const void* ps[] = {__VA_ARGS__};                                                   \
+        for (const void* p : ps)                                                            \
+            if (!p || !al16(p)) return ar::set_error(AR_EINVAL, "%s: null or unaligned pointer", __func__); \
+    } while (0)
+
+extern "C" int32_t ar_flash_attn_fwd(ar_stream_t stream, float* output, float* lse_out, const float* q, const float* k,
+                                     const float* v, int64_t B, int64_t T, int64_t num_heads, int64_t head_dim,
+                                     int64_t window_size) {
+    AR_ATTN_PTRS(output, q, k, v);
+    AR_CHECK_ARG(lse_out != nullptr, "flash_attn_fwd: null lse");
+    return ar::attn_dispatch<false, float>(S(stream), ar::AttnOp::FWD, output, lse_out, q, k, v, nullptr, nullptr,
+                                           nullptr, B, T, num_heads, head_dim, window_size);
+}
+extern "C" int32_t ar_flash_attn_fwd_bf16(ar_stream_t stream, float* output, float* lse_out, const float* q,
+                                          const float* k, const float* v, int64_t B, int64_t T, int64_t num_heads,
+                                          int64_t head_dim, int64_t window_size) {
+    AR_ATTN_PTRS(output, q, k, v);
+    AR_CHECK_ARG(lse_out != nullptr, "flash_attn_fwd_bf16: null lse");
+    return ar::attn_dispatch<true, float>(S(stream), ar::AttnOp::FWD, output, lse_out, q, k, v, nullptr, nullptr,
+                                          nullptr, B, T, num_heads, head_dim, window_size);
+}
+extern "C" int32_t ar_flash_attn_bwd_dq(ar_stream_t stream, float* grad_q, const float* q, const float* k,
+                                        const float* v, const float* grad_output, const float* lse, const float* d_buf,
+                                        int64_t B, int64_t T, int64_t num_heads, int64_t head_dim,
+                                        int64_t window_size) {
+    AR_ATTN_PTRS(grad_q, q, k, v, grad_output);
+    AR_CHECK_ARG(lse && d_buf, "flash_attn_bwd_dq: null lse / d_buf");
+    return ar::attn_dispatch<false, float>(S(stream), ar::AttnOp::DQ, grad_q, nullptr, q, k, v, grad_output, lse,
+                                           d_buf, B, T, num_heads, head_dim, window_size);
+}
+extern "C" int32_t ar_flash_attn_bwd_dq_bf16(ar_stream_t stream, float* grad_q, const float* q, const float* k,
+                                             const float* v, const float* grad_output, const float* lse,
+                                             const float* d_buf, int64_t B, int64_t T, int64_t num_heads,
+                                             int64_t head_dim, int64_t window_size) {
+    AR_ATTN_PTRS(grad_q, q, k, v, grad_output);
+    AR_CHECK_ARG(lse && d_buf, "flash_attn_bwd_dq_bf16: null lse / d_buf");
+    return ar::attn_dispatch<true, float>(S(stream), ar::AttnOp::DQ, grad_q, nullptr, q, k, v, grad_output, lse,
+                                          d_buf, B, T, num_heads, head_dim, window_size);
+}
+extern "C" int32_t ar_flash_attn_bwd_dkv(ar_stream_t stream, float* grad_k, float* grad_v, const float* q,
+                                         const float* k, const float* v, const float* grad_output, const float* lse,
+                                         const float* d_buf, int64_t B, int64_t T, int64_t num_heads,
+                                         int64_t head_dim, int64_t window_size) {
+    AR_ATTN_PTRS(grad_k, grad_v, q, k, v, grad_output);
+    AR_CHECK_ARG(lse && d_buf, "flash_attn_bwd_dkv: null lse / d_buf");
+    return ar::attn_dispatch<false, float>(S(stream), ar::AttnOp::DKV, grad_k, grad_v, q, k, v, grad_output, lse,
+                                           d_buf, B, T, num_heads, head_dim, window_size);
+}
+extern "C" int32_t ar_flash_attn_bwd_dkv_bf16(ar_stream_t stream, float* grad_k, float* grad_v, const float* q,
+                                              const float* k, const float* v, const float* grad_output,
+                                              const float* lse, const float* d_buf, int64_t B, int64_t T,
+                                              int64_t num_heads, int64_t head_dim, int64_t window_size) {
+    AR_ATTN_PTRS(grad_k, grad_v, q, k, v, grad_output);
+    AR_CHECK_ARG(lse && d_buf, "flash_attn_bwd_dkv_bf16: null lse / d_buf");
+    return ar::attn_dispatch<true, float>(S(stream), ar::AttnOp::DKV, grad_k, grad_v, q, k, v, grad_output, lse,
+                                          d_buf, B, T, num_heads, head_dim, window_size);
+}
+
+template int32_t ar::attn_dispatch<false, float>(hipStream_t, ar::AttnOp, float*, float*, const float*, const float*,
+                                                 const float*, const float*, const float*, const float*, int64_t,
+                                                 int64_t, int64_t, int64_t, int64_t);
+template int32_t ar::attn_dispatch<true, float>(hipStream_t, ar::AttnOp, float*, float*, const float*, const float*,
+                                                const float*, const float*, const float*, const float*, int64_t,
+                                                int64_t, int64_t, int64_t, int64_t);

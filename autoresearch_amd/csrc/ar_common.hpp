@@ -1,0 +1,95 @@
+// ar_common.hpp -- shared helpers for the gfx950 (CDNA4) kernel library.
+//
+// Conventions for every kernel source in this directory:
+//   * wave64 everywhere; reductions use DPP/ds_swizzle-backed __shfl_xor.
+//   * fp32 arithmetic in element kernels; bf16 only as a storage / MFMA
+//     operand type, always with fp32 accumulation.
+//   * entry points return AR_OK or a negative ar_status and never throw.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ar_ops.h"
+
+namespace ar {
+
+using bf16 = __bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// ---- error plumbing (ar_errors.cpp) ----
+int32_t set_error(int32_t code, const char* fmt, ...);
+int32_t check_launch(const char* what);
+inline hipStream_t S(ar_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Library-owned device workspace, grown on demand (ar_errors.cpp).  Kernels
+// queued earlier on any stream may still read the old buffer, so growth
+// synchronises the device before freeing it.
+void* workspace(size_t bytes, int32_t* status);
+
+// ---- device helpers ----
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// Block-wide sum for blockDim.x a multiple of 64 (<= 1024).  `red` must hold
+// blockDim.x/64 floats.  Every thread receives the total.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x / kWave, l = threadIdx.x % kWave, nw = blockDim.x / kWave;
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    return t;
+}
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    const int w = threadIdx.x / kWave, l = threadIdx.x % kWave, nw = blockDim.x / kWave;
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    float t = -INFINITY;
+    for (int i = 0; i < nw; ++i) t = fmaxf(t, red[i]);
+    return t;
+}
+
+template <typename T> __device__ __forceinline__ float to_f32(T v);
+template <> __device__ __forceinline__ float to_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ float to_f32<bf16>(bf16 v) { return (float)v; }
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf16)v; }
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Grid for a flat element-wise kernel: grid-stride loops, capped so a launch
+// never exceeds what 256 CUs can keep resident many times over.
+inline unsigned flat_grid(int64_t n, int per_block_items) {
+    int64_t g = cdiv(n, per_block_items);
+    if (g < 1) g = 1;
+    if (g > 65536) g = 65536;
+    return (unsigned)g;
+}
+
+}  // namespace ar
+
+#define AR_CHECK_ARG(cond, ...)                                   \
+    do {                                                          \
+        if (!(cond)) return ar::set_error(AR_EINVAL, __VA_ARGS__); \
+    } while (0)
+
+#define AR_LAUNCH_CHECK(what) ar::check_launch(what)

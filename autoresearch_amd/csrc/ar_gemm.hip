@@ -1,0 +1,472 @@
+// ar_gemm.hip -- MFMA GEMMs for gfx950: the reference's three linear kernels
+// linear_fwd (NT, ops.mojo:110-203), linear_bwd_dx (NN, ops.mojo:870-950) and
+// linear_bwd_dw (TN, ops.mojo:953-1033), and the Muon Polar-Express products
+// that reuse them (optimizer.mojo:288-336).
+//
+// One kernel template covers all three layouts.  In GEMM terms it computes
+//   C[mo, no] (=, +=) sum_r A(mo, r) * B(no, r)
+// where each operand is stored either "K-major" (r contiguous: X[M,K] of NT)
+// or "MN-major" (mo/no contiguous: W[N,K] read as B of NN, dY and X of TN).
+//   NT: A = X  [M,K] K-major,  B = W  [N,K] K-major
+//   NN: A = dY [M,N] K-major,  B = W  [N,K] MN-major  (reduction over N)
+//   TN: A = dY [M,N] MN-major, B = X  [M,K] MN-major  (reduction over M)
+//
+// Design (CDNA4):
+//   * 256 threads = 4 wave64s, block tile 128x128, each wave a 64x64 quadrant
+//     computed as 2x2 MFMA 32x32 tiles (v_mfma_f32_32x32x16_bf16 for bf16
+//     compute, v_mfma_f32_32x32x2_f32 for exact fp32 compute).
+//   * Operands are staged through LDS in [row][k] layout (k contiguous,
+//     16-byte padded rows) so every MFMA fragment is one ds_read_b128 (bf16)
+//     or ds_read_b32 (fp32).  MN-major operands are transposed on the way in:
+//     a thread loads a (k x 4-row) block with 4-wide vector loads and writes
+//     it as 4 k-contiguous 16-byte LDS chunks.
+//   * Two LDS stages; the next k-tile's global loads are issued before the
+//     current tile's MFMAs, one barrier per k-tile.
+//   * 1-D grid, remapped so each XCD (8 per MI355X, workgroups dispatched
+//     round-robin) owns a contiguous run of row-major tiles: the A row-panel
+//     a tile reads stays in that XCD's L2.
+//   * TN reduces over M = B*T (65536 at the benchmark size) into a small
+//     output, so it is split over the reduction: each split writes an fp32
+//     partial and a second kernel adds the partials in split order
+//     (deterministic; the reference's single-block loop over M is serial).
+#include "ar_internal.hpp"
+
+using namespace ar;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int BM = 128, BN = 128;
+
+enum Epi { EPI_STORE = 0, EPI_ACCUM = 1, EPI_PARTIAL = 2 };
+
+template <bool BF16> struct Mfma;
+
+template <> struct Mfma<true> {
+    using LT = bf16;
+    static constexpr int BK = 64, KS = 16, LDK = BK + 8, CW = 8;
+    using Frag = bf16x8;
+    __device__ static Frag frag(const LT* p) { return *reinterpret_cast<const bf16x8*>(p); }
+    __device__ static f32x16 mma(Frag a, Frag b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    __device__ static int lane_k(int lane) { return (lane >> 5) * 8; }
+};
+
+template <> struct Mfma<false> {
+    using LT = float;
+    static constexpr int BK = 32, KS = 2, LDK = BK + 4, CW = 4;
+    using Frag = float;
+    __device__ static Frag frag(const LT* p) { return *p; }
+    __device__ static f32x16 mma(Frag a, Frag b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+    }
+    __device__ static int lane_k(int lane) { return lane >> 5; }
+};
+
+// Row of accumulator element v (0..15) of a 32x32 MFMA tile held by `lane`;
+// its column is lane % 32.
+__device__ __forceinline__ int acc_row(int v, int lane) { return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); }
+
+template <typename T, int N>
+__device__ __forceinline__ void vload(T (&dst)[N], const T* src) {
+    constexpr int BYTES = N * (int)sizeof(T);
+    static_assert(BYTES == 8 || BYTES == 16 || BYTES == 32, "vector width");
+    if constexpr (BYTES == 8) {
+        *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(src);
+    } else if constexpr (BYTES == 16) {
+        *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+    } else {
+        reinterpret_cast<uint4*>(dst)[0] = reinterpret_cast<const uint4*>(src)[0];
+        reinterpret_cast<uint4*>(dst)[1] = reinterpret_cast<const uint4*>(src)[1];
+    }
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void vzero(T (&dst)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) dst[i] = T(0.0f);
+}
+
+// Global -> register -> LDS tile loader for one operand (ROWS x BK tile).
+template <typename TG, typename LT, bool KMAJ, int ROWS, int BK, int CW>
+struct TileLoader {
+    static constexpr int MW = 4;  // rows per MN-major item
+    static constexpr int NPASS = KMAJ ? (ROWS * BK / CW) / kThreads : ((BK / CW) * (ROWS / MW)) / kThreads;
+    static_assert(NPASS >= 1, "tile too small for the block");
+    static constexpr int PER = KMAJ ? CW : CW * MW;  // TG values per pass
+    TG v[NPASS][PER];
+
+    // g: operand base; ld: row stride of the stored matrix; rows: extent of
+    // the output dimension; K: reduction extent.
+    __device__ __forceinline__ void load(const TG* g, int64_t ld, int64_t row0, int64_t rows, int64_t k0,
+                                         int64_t kend) {
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int p = 0; p < NPASS; ++p) {
+            if constexpr (KMAJ) {
+                const int c = p * kThreads + tid;
+                const int r = c / (BK / CW), kc = (c % (BK / CW)) * CW;
+                const int64_t gr = row0 + r, gk = k0 + kc;
+                if (gr < rows && gk < kend) {
+                    TG tmp[CW];
+                    vload(tmp, g + gr * ld + gk);
+#pragma unroll
+                    for (int i = 0; i < CW; ++i) v[p][i] = tmp[i];
+                } else {
+                    vzero(v[p]);
+                }
+            } else {
+                const int item = p * kThreads + tid;
+                const int mg = item % (ROWS / MW), kg = item / (ROWS / MW);
+                const int64_t gr = row0 + mg * MW;
+#pragma unroll
+                for (int j = 0; j < CW; ++j) {
+                    const int64_t gk = k0 + kg * CW + j;
+                    TG tmp[MW];
+                    if (gr < rows && gk < kend) vload(tmp, g + gk * ld + gr);
+                    else vzero(tmp);
+#pragma unroll
+                    for (int i = 0; i < MW; ++i) v[p][j * MW + i] = tmp[i];
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(LT* lds, int ldk) const {
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int p = 0; p < NPASS; ++p) {
+            if constexpr (KMAJ) {
+                const int c = p * kThreads + tid;
+                const int r = c / (BK / CW), kc = (c % (BK / CW)) * CW;
+                LT out[CW];
+#pragma unroll
+                for (int i = 0; i < CW; ++i) out[i] = (LT)to_f32(v[p][i]);
+                *reinterpret_cast<uint4*>(lds + r * ldk + kc) = *reinterpret_cast<const uint4*>(out);
+            } else {
+                const int item = p * kThreads + tid;
+                const int mg = item % (ROWS / MW), kg = item / (ROWS / MW);
+#pragma unroll
+                for (int i = 0; i < MW; ++i) {
+                    LT out[CW];
+#pragma unroll
+                    for (int j = 0; j < CW; ++j) out[j] = (LT)to_f32(v[p][j * MW + i]);
+                    *reinterpret_cast<uint4*>(lds + (mg * MW + i) * ldk + kg * CW) =
+                        *reinterpret_cast<const uint4*>(out);
+                }
+            }
+        }
+    }
+};
+
+// Linear block id -> (tile_m, tile_n, split) with an XCD-contiguous order.
+__device__ __forceinline__ void tile_coords(int64_t tiles_n, int64_t tiles_mn, int64_t total, int64_t& tm,
+                                            int64_t& tn, int64_t& z) {
+    int64_t id = blockIdx.x;
+    if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
+    z = id / tiles_mn;
+    const int64_t r = id % tiles_mn;
+    tm = r / tiles_n;
+    tn = r % tiles_n;
+}
+
+template <typename TA, typename TB, typename TC, bool AK, bool BKM, bool BF16, int EPI>
+__global__ __launch_bounds__(kThreads) void gemm_k(TC* C, const TA* A, const TB* B, int64_t M, int64_t N,
+                                                      int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                                                      int64_t k_per_split, float* partial) {
+    using MM = Mfma<BF16>;
+    using LT = typename MM::LT;
+    constexpr int BK = MM::BK, LDK = MM::LDK, CW = MM::CW;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    LT* lds = reinterpret_cast<LT*>(smem_raw);
+    LT* lA[2] = {lds, lds + (BM + BN) * LDK};
+    LT* lB[2] = {lds + BM * LDK, lds + (BM + BN) * LDK + BM * LDK};
+
+    const int64_t tiles_n = (N + BN - 1) / BN, tiles_m = (M + BM - 1) / BM;
+    const int64_t tiles_mn = tiles_m * tiles_n;
+    const int64_t splits = (K + k_per_split - 1) / k_per_split;
+    int64_t tm, tn, z;
+    tile_coords(tiles_n, tiles_mn, tiles_mn * splits, tm, tn, z);
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+    const int64_t kbeg = z * k_per_split;
+    const int64_t kend = (kbeg + k_per_split < K) ? kbeg + k_per_split : K;
+
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int wm = wave / 2, wn = wave % 2;
+
+    TileLoader<TA, LT, AK, BM, BK, CW> la;
+    TileLoader<TB, LT, BKM, BN, BK, CW> lb;
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+    const int64_t nk = (kend - kbeg + BK - 1) / BK;
+    if (nk > 0) {
+        la.load(A, lda, m0, M, kbeg, kend);
+        lb.load(B, ldb, n0, N, kbeg, kend);
+        la.store(lA[0], LDK);
+        lb.store(lB[0], LDK);
+    }
+    __syncthreads();
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            la.load(A, lda, m0, M, kbeg + (kt + 1) * BK, kend);
+            lb.load(B, ldb, n0, N, kbeg + (kt + 1) * BK, kend);
+        }
+        const LT* a_base = lA[cur] + (wm * 64 + (lane & 31)) * LDK + MM::lane_k(lane);
+        const LT* b_base = lB[cur] + (wn * 64 + (lane & 31)) * LDK + MM::lane_k(lane);
+#pragma unroll
+        for (int ks = 0; ks < BK / MM::KS; ++ks) {
+            typename MM::Frag fa[2], fb[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) fa[i] = MM::frag(a_base + i * 32 * LDK + ks * MM::KS);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) fb[j] = MM::frag(b_base + j * 32 * LDK + ks * MM::KS);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = MM::mma(fa[i], fb[j], acc[i][j]);
+        }
+        if (more) {
+            la.store(lA[cur ^ 1], LDK);
+            lb.store(lB[cur ^ 1], LDK);
+        }
+        __syncthreads();
+    }
+
+    // Epilogue.
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+            if (col >= N) continue;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t row = m0 + wm * 64 + i * 32 + acc_row(v, lane);
+                if (row >= M) continue;
+                const float x = acc[i][j][v];
+                if constexpr (EPI == EPI_STORE) {
+                    C[row * ldc + col] = from_f32<TC>(x);
+                } else if constexpr (EPI == EPI_ACCUM) {
+                    C[row * ldc + col] = from_f32<TC>(to_f32(C[row * ldc + col]) + x);
+                } else {
+                    partial[(z * M + row) * N + col] = x;
+                }
+            }
+        }
+}
+
+// C[i] (+)= sum_z partial[z][i], z in order (row stride ldc for C).
+template <typename TC>
+__global__ void splitk_reduce_k(TC* C, const float* partial, int64_t M, int64_t N, int64_t ldc, int64_t splits,
+                                int accumulate) {
+    const int64_t total = M * N;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / N, c = i % N;
+        float s = accumulate ? to_f32(C[r * ldc + c]) : 0.f;
+        for (int64_t z = 0; z < splits; ++z) s += partial[z * total + i];
+        C[r * ldc + c] = from_f32<TC>(s);
+    }
+}
+
+template <bool BF16>
+constexpr size_t lds_bytes() {
+    using MM = Mfma<BF16>;
+    return (size_t)2 * (BM + BN) * MM::LDK * sizeof(typename MM::LT);
+}
+
+}  // namespace
+
+namespace ar {
+
+template <bool BF16>
+static int64_t choose_splits(int64_t tiles, int64_t K, int64_t splits_req, int64_t& kps) {
+    constexpr int BKt = Mfma<BF16>::BK;
+    int64_t splits = splits_req;
+    if (splits < 1) {
+        // Aim for >= 512 workgroups (2 per CU) when the reduction is long.
+        splits = 1;
+        while (tiles * splits < 512 && K / (splits * 2) >= 4 * BKt) splits *= 2;
+    }
+    kps = ((K + splits - 1) / splits + BKt - 1) / BKt * BKt;
+    if (kps < BKt) kps = BKt;
+    splits = (K + kps - 1) / kps;
+    return splits < 1 ? 1 : splits;
+}
+
+// Launches one GEMM in GEMM space: C[mo, no] (+)= sum_r A(mo, r) B(no, r).
+template <typename TA, typename TB, typename TC, bool AK, bool BKM, bool BF16>
+static int32_t gemm_launch(hipStream_t st, TC* C, const TA* A, const TB* B, int64_t M, int64_t N, int64_t K,
+                           int64_t lda, int64_t ldb, int64_t ldc, bool accumulate, int64_t splits_req,
+                           float* partial, const char* nm) {
+    const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    int64_t kps = 0;
+    const int64_t splits = choose_splits<BF16>(tiles, K, splits_req, kps);
+    const size_t lds = lds_bytes<BF16>();
+    if (splits == 1) {
+        const unsigned grid = (unsigned)tiles;
+        if (accumulate)
+            gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_ACCUM><<<grid, kThreads, lds, st>>>(C, A, B, M, N, K, lda, ldb, ldc,
+                                                                                    kps, nullptr);
+        else
+            gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_STORE><<<grid, kThreads, lds, st>>>(C, A, B, M, N, K, lda, ldb, ldc,
+                                                                                    kps, nullptr);
+        return check_launch(nm);
+    }
+    if (!partial) return set_error(AR_EINVAL, "%s: split-K scratch missing", nm);
+    const unsigned grid = (unsigned)(tiles * splits);
+    gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_PARTIAL><<<grid, kThreads, lds, st>>>(C, A, B, M, N, K, lda, ldb, ldc, kps,
+                                                                              partial);
+    splitk_reduce_k<TC><<<flat_grid(M * N, 256 * 4), 256, 0, st>>>(C, partial, M, N, ldc, splits, accumulate ? 1 : 0);
+    return check_launch(nm);
+}
+
+// GEMM-space sizes of a reference-layout call.
+static void gemm_space(int layout, int64_t M, int64_t N, int64_t K, int64_t& gm, int64_t& gn, int64_t& gk) {
+    if (layout == 0) { gm = M; gn = N; gk = K; }
+    else if (layout == 1) { gm = M; gn = K; gk = N; }
+    else { gm = N; gn = K; gk = M; }
+}
+
+int64_t gemm_auto_splits(int layout, bool bf16, int64_t M, int64_t N, int64_t K) {
+    if (layout != 2) return 1;
+    int64_t gm, gn, gk, kps;
+    gemm_space(layout, M, N, K, gm, gn, gk);
+    const int64_t tiles = ((gm + BM - 1) / BM) * ((gn + BN - 1) / BN);
+    return bf16 ? choose_splits<true>(tiles, gk, 0, kps) : choose_splits<false>(tiles, gk, 0, kps);
+}
+
+int64_t gemm_partial_elems(int layout, int64_t M, int64_t N, int64_t K, int64_t splits) {
+    int64_t gm, gn, gk;
+    gemm_space(layout, M, N, K, gm, gn, gk);
+    return splits > 1 ? splits * gm * gn : 0;
+}
+
+int32_t gemm_f32(hipStream_t st, int layout, bool bf, float* C, const float* X, const float* W, int64_t M, int64_t N,
+                 int64_t K, bool accumulate, int64_t splits, float* partial) {
+    if (layout == 0) {
+        if (bf)
+            return gemm_launch<float, float, float, true, true, true>(st, C, X, W, M, N, K, K, K, N, accumulate, 1,
+                                                                      nullptr, "linear_fwd");
+        return gemm_launch<float, float, float, true, true, false>(st, C, X, W, M, N, K, K, K, N, accumulate, 1,
+                                                                   nullptr, "linear_fwd");
+    }
+    if (layout == 1) {
+        // GEMM (mo=M, no=K, r=N): A = dY [M][N] K-major, B(no=k, r=n) = W[n][k] MN-major.
+        if (bf)
+            return gemm_launch<float, float, float, true, false, true>(st, C, X, W, M, K, N, N, K, K, accumulate, 1,
+                                                                       nullptr, "linear_bwd_dx");
+        return gemm_launch<float, float, float, true, false, false>(st, C, X, W, M, K, N, N, K, K, accumulate, 1,
+                                                                    nullptr, "linear_bwd_dx");
+    }
+    // TN: GEMM (mo=N, no=K, r=M): A(mo=n, r=m) = dY[m][n] MN-major, B(no=k, r=m) = X[m][k] MN-major.
+    if (splits < 1) splits = gemm_auto_splits(2, bf, M, N, K);
+    if (bf)
+        return gemm_launch<float, float, float, false, false, true>(st, C, X, W, N, K, M, N, K, K, accumulate,
+                                                                    splits, partial, "linear_bwd_dw");
+    return gemm_launch<float, float, float, false, false, false>(st, C, X, W, N, K, M, N, K, K, accumulate, splits,
+                                                                 partial, "linear_bwd_dw");
+}
+
+}  // namespace ar
+
+// =====================================================================
+// C ABI
+// =====================================================================
+
+static int32_t check_gemm_args(const void* C, const void* A, const void* B, int64_t M, int64_t N, int64_t K,
+                               const char* nm) {
+    if (!C || !A || !B) return set_error(AR_EINVAL, "%s: null pointer", nm);
+    if (M < 0 || N < 0 || K < 0) return set_error(AR_EINVAL, "%s: negative dimension", nm);
+    if ((M | N | K) & 7)
+        return set_error(AR_EINVAL, "%s: M, N, K must be multiples of 8 (got %lld, %lld, %lld)", nm, (long long)M,
+                         (long long)N, (long long)K);
+    if ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C)) & 15)
+        return set_error(AR_EINVAL, "%s: operands must be 16-byte aligned", nm);
+    return AR_OK;
+}
+
+static inline bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
+    const char *pa = (const char*)a, *pb = (const char*)b;
+    return pa < pb + bbytes && pb < pa + abytes;
+}
+
+static int32_t linear_fwd_impl(ar_stream_t s, float* out, const float* in, const float* w, int64_t M, int64_t N,
+                               int64_t K, bool bf) {
+    int32_t st = check_gemm_args(out, in, w, M, N, K, "linear_fwd");
+    if (st) return st;
+    if (M == 0 || N == 0) return AR_OK;
+    if (overlaps(out, M * N * 4, in, M * K * 4) || overlaps(out, M * N * 4, w, N * K * 4))
+        return set_error(AR_EINVAL, "linear_fwd: output overlaps an input");
+    if (K == 0) return ar_zero_buffer(s, out, M * N);
+    return ar::gemm_f32(S(s), 0, bf, out, in, w, M, N, K, false, 1, nullptr);
+}
+
+static int32_t linear_bwd_dx_impl(ar_stream_t s, float* dx, const float* dy, const float* w, int64_t M, int64_t N,
+                                  int64_t K, bool bf) {
+    int32_t st = check_gemm_args(dx, dy, w, M, N, K, "linear_bwd_dx");
+    if (st) return st;
+    if (M == 0 || K == 0) return AR_OK;
+    if (overlaps(dx, M * K * 4, w, N * K * 4)) return set_error(AR_EINVAL, "linear_bwd_dx: grad_input overlaps weight");
+    if (N == 0) return ar_zero_buffer(s, dx, M * K);
+    const float* src = dy;
+    if (overlaps(dx, M * K * 4, dy, M * N * 4)) {
+        // model.mojo:906 calls this in place; read all of dY first (copy).
+        float* tmp = (float*)ar::workspace((size_t)M * N * sizeof(float), &st);
+        if (!tmp) return st;
+        if (hipMemcpyAsync(tmp, dy, (size_t)M * N * sizeof(float), hipMemcpyDeviceToDevice, S(s)) != hipSuccess)
+            return set_error(AR_EHIP, "linear_bwd_dx: alias copy failed");
+        src = tmp;
+    }
+    return ar::gemm_f32(S(s), 1, bf, dx, src, w, M, N, K, false, 1, nullptr);
+}
+
+static int32_t linear_bwd_dw_impl(ar_stream_t s, float* dw, const float* dy, const float* x, int64_t M, int64_t N,
+                                  int64_t K, bool bf) {
+    int32_t st = check_gemm_args(dw, dy, x, M, N, K, "linear_bwd_dw");
+    if (st) return st;
+    if (N == 0 || K == 0 || M == 0) return AR_OK;
+    if (overlaps(dw, N * K * 4, dy, M * N * 4) || overlaps(dw, N * K * 4, x, M * K * 4))
+        return set_error(AR_EINVAL, "linear_bwd_dw: grad_weight overlaps an input");
+    const int64_t splits = ar::gemm_auto_splits(2, bf, M, N, K);
+    float* partial = nullptr;
+    if (splits > 1) {
+        partial = (float*)ar::workspace((size_t)ar::gemm_partial_elems(2, M, N, K, splits) * sizeof(float), &st);
+        if (!partial) return st;
+    }
+    return ar::gemm_f32(S(s), 2, bf, dw, dy, x, M, N, K, true, splits, partial);
+}
+
+extern "C" int32_t ar_linear_fwd(ar_stream_t stream, float* output, const float* input, const float* weight,
+                                 int64_t M, int64_t N, int64_t K) {
+    return linear_fwd_impl(stream, output, input, weight, M, N, K, false);
+}
+extern "C" int32_t ar_linear_fwd_bf16(ar_stream_t stream, float* output, const float* input, const float* weight,
+                                      int64_t M, int64_t N, int64_t K) {
+    return linear_fwd_impl(stream, output, input, weight, M, N, K, true);
+}
+extern "C" int32_t ar_linear_bwd_dx(ar_stream_t stream, float* grad_input, const float* grad_output,
+                                    const float* weight, int64_t M, int64_t N, int64_t K) {
+    return linear_bwd_dx_impl(stream, grad_input, grad_output, weight, M, N, K, false);
+}
+extern "C" int32_t ar_linear_bwd_dx_bf16(ar_stream_t stream, float* grad_input, const float* grad_output,
+                                         const float* weight, int64_t M, int64_t N, int64_t K) {
+    return linear_bwd_dx_impl(stream, grad_input, grad_output, weight, M, N, K, true);
+}
+extern "C" int32_t ar_linear_bwd_dw(ar_stream_t stream, float* grad_weight, const float* grad_output,
+                                    const float* input, int64_t M, int64_t N, int64_t K) {
+    return linear_bwd_dw_impl(stream, grad_weight, grad_output, input, M, N, K, false);
+}
+extern "C" int32_t ar_linear_bwd_dw_bf16(ar_stream_t stream, float* grad_weight, const float* grad_output,
+                                         const float* input, int64_t M, int64_t N, int64_t K) {
+    return linear_bwd_dw_impl(stream, grad_weight, grad_output, input, M, N, K, true);
+}

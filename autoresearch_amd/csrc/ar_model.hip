@@ -1,0 +1,590 @@
+// ar_model.hip -- the whole training step: a C++ restatement of the Mojo
+// host code (model.mojo ModelWeights / ForwardBuffers / forward / backward /
+// zero_grads, optimizer.mojo AdamWState / MuonState, train.mojo's step body)
+// sequencing the gfx950 kernels of this library.
+//
+// Differences from the reference's host code, none of which change results:
+//   * activations are produced directly into their per-layer saved buffers,
+//     so the reference's device-to-device "save" copies disappear
+//     (model.mojo:618, 632, 640, 659-660, 689-691, 700-701, 717, 721, 727,
+//     738, 743, 873, 903);
+//   * c_proj dX is written to its own buffer instead of in place
+//     (model.mojo:906), which is the read-all-then-write semantics;
+//   * the token-id sort used by the deterministic embedding scatter is done
+//     once per backward and shared by the wte and value-embedding scatters;
+//   * all reductions are deterministic (fixed order, no float atomics).
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "ar_internal.hpp"
+
+using namespace ar;
+
+namespace {
+
+constexpr int64_t kGateChannels = 32;  // config.mojo:64
+constexpr int64_t kMlpExpansion = 4;   // config.mojo:63
+constexpr float kSoftcap = 15.0f;      // config.mojo:86
+
+struct Tensor {
+    int64_t offset, size, rows, cols;
+    std::string name;
+};
+
+struct LayerBufs {
+    float *x, *xn_attn, *q, *k, *v, *lse, *attn_out, *xn_mlp, *mlp_hidden, *mlp_act, *rms_attn, *rms_mlp, *ve, *gate;
+};
+
+}  // namespace
+
+struct ar_gpt {
+    ar_gpt_config c;
+    int64_t B, T, BT, period;
+    bool bf16;
+    hipStream_t st;
+    std::vector<Tensor> t;
+    int64_t nparams = 0;
+    float *params = nullptr, *grads = nullptr, *adam_m = nullptr, *adam_v = nullptr, *muon_buf = nullptr;
+    int64_t i_wte, i_lm, i_res, i_x0;
+    std::vector<int64_t> i_q, i_k, i_v, i_proj, i_fc, i_mlpp, i_ve, i_gate;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    int64_t rope_rows = 0;
+    // activations
+    float *x0, *x, *rms_qk, *proj_out, *mlp_out, *logits, *loss, *mean_loss, *x_final, *rms_final, *d_buf;
+    std::vector<LayerBufs> L;
+    // gradients of activations
+    float *grad_x, *grad_x0, *grad_logits, *grad_attn_out, *grad_q, *grad_k, *grad_v, *grad_x_norm, *grad_tmp,
+        *grad_mlp, *grad_ve, *grad_gate;
+    // scratch (sequential users on one stream)
+    float* scratch = nullptr;
+    int64_t scratch_elems = 0;
+    uint32_t* sorted_ids = nullptr;
+    int32_t* sorted_tok = nullptr;
+    void* sort_scratch = nullptr;
+    size_t sort_bytes = 0;
+    int32_t sort_bits = 32;
+    int64_t adam_step = 0;
+    std::vector<void*> allocs;
+    // profiling (ar_gpt_profile)
+    bool prof = false;
+    std::vector<hipEvent_t> ev;
+    struct Rec { int cls; double flops; int e0, e1; };
+    std::vector<Rec> recs;
+    size_t ev_used = 0;
+};
+
+namespace {
+
+bool has_ve(const ar_gpt_config& c, int64_t i) { return (i % 2) == ((c.n_layer - 1) % 2); }  // config.mojo:45-47
+int64_t window_size(const ar_gpt_config& c, int64_t i) {                                      // config.mojo:49-55
+    if (i == c.n_layer - 1) return c.sequence_len;
+    if (i % 4 < 3) return c.sequence_len / 2;
+    return c.sequence_len;
+}
+
+int32_t dalloc(ar_gpt* m, void** p, size_t bytes) {
+    if (bytes == 0) bytes = 256;
+    if (hipMalloc(p, bytes) != hipSuccess) return set_error(AR_ENOMEM, "gpt: hipMalloc(%zu) failed", bytes);
+    m->allocs.push_back(*p);
+    return AR_OK;
+}
+#define AR_TRY(expr)                      \
+    do {                                  \
+        int32_t _r = (expr);              \
+        if (_r != AR_OK) return _r;       \
+    } while (0)
+#define FALLOC(ptr, n) AR_TRY(dalloc(m, (void**)&(ptr), (size_t)(n) * sizeof(float)))
+
+int64_t add_tensor(ar_gpt* m, int64_t rows, int64_t cols, const std::string& nm) {
+    Tensor t{m->nparams, rows * cols, rows, cols, nm};
+    m->t.push_back(t);
+    m->nparams += (rows * cols + 63) & ~int64_t(63);  // 256-byte aligned tensors
+    return (int64_t)m->t.size() - 1;
+}
+
+inline float* P(ar_gpt* m, int64_t i) { return m->params + m->t[i].offset; }
+inline float* G(ar_gpt* m, int64_t i) { return m->grads + m->t[i].offset; }
+
+inline ar_stream_t AS(ar_gpt* m) { return reinterpret_cast<ar_stream_t>(m->st); }
+
+// Profiling brackets (no-ops unless ar_gpt_profile enabled them).
+int prof_begin(ar_gpt* m) {
+    if (!m->prof) return -1;
+    if (m->ev_used + 2 > m->ev.size()) {
+        for (int i = 0; i < 1024; ++i) {
+            hipEvent_t e;
+            if (hipEventCreate(&e) != hipSuccess) return -1;
+            m->ev.push_back(e);
+        }
+    }
+    const int e0 = (int)m->ev_used;
+    m->ev_used += 2;
+    hipEventRecord(m->ev[e0], m->st);
+    return e0;
+}
+void prof_end(ar_gpt* m, int e0, int cls, double flops) {
+    if (e0 < 0) return;
+    hipEventRecord(m->ev[e0 + 1], m->st);
+    m->recs.push_back({cls, flops, e0, e0 + 1});
+}
+
+int32_t linear(ar_gpt* m, float* out, const float* in, const float* w, int64_t M, int64_t N, int64_t K) {
+    const int e = prof_begin(m);
+    const int32_t r = gemm_f32(m->st, 0, m->bf16, out, in, w, M, N, K, false, 1, nullptr);
+    prof_end(m, e, 0, 2.0 * M * N * K);
+    return r;
+}
+int32_t linear_dx(ar_gpt* m, float* dx, const float* dy, const float* w, int64_t M, int64_t N, int64_t K) {
+    const int e = prof_begin(m);
+    const int32_t r = gemm_f32(m->st, 1, m->bf16, dx, dy, w, M, N, K, false, 1, nullptr);
+    prof_end(m, e, 1, 2.0 * M * N * K);
+    return r;
+}
+int32_t linear_dw(ar_gpt* m, float* dw, const float* dy, const float* x, int64_t M, int64_t N, int64_t K) {
+    const int e = prof_begin(m);
+    const int32_t r = gemm_f32(m->st, 2, m->bf16, dw, dy, x, M, N, K, true, 0, m->scratch);
+    prof_end(m, e, 2, 2.0 * M * N * K);
+    return r;
+}
+// Algorithmic attention FLOPs of one call: forward 4*B*H*hd*sum_q keys(q),
+// dQ 3x that (S, dP, dQ products), dK/dV 4x (S, dP, dV, dK).
+double attn_keys(const ar_gpt* m, int64_t ws) {
+    const int64_t T = m->T;
+    double keys = 0;
+    for (int64_t q = 0; q < T; ++q) {
+        const int64_t k0 = (ws > 0 && q - ws > 0) ? q - ws : 0;
+        keys += (double)(q - k0 + 1);
+    }
+    return keys;
+}
+int32_t attention(ar_gpt* m, AttnOp op, float* o1, float* o2, const float* q, const float* k, const float* v,
+                  const float* dout, const float* lse, const float* dbuf, int64_t ws) {
+    const ar_gpt_config& c = m->c;
+    const int e = prof_begin(m);
+    int32_t r;
+    if (m->bf16)
+        r = attn_dispatch<true, float>(m->st, op, o1, o2, q, k, v, dout, lse, dbuf, m->B, m->T, c.n_head, c.head_dim,
+                                       ws);
+    else
+        r = attn_dispatch<false, float>(m->st, op, o1, o2, q, k, v, dout, lse, dbuf, m->B, m->T, c.n_head,
+                                        c.head_dim, ws);
+    if (e >= 0) {
+        const double unit = 2.0 * m->B * c.n_head * c.head_dim * attn_keys(m, ws);
+        const int cls = op == AttnOp::FWD ? 3 : (op == AttnOp::DQ ? 4 : 5);
+        prof_end(m, e, cls, unit * (op == AttnOp::FWD ? 2.0 : (op == AttnOp::DQ ? 3.0 : 4.0)));
+    }
+    return r;
+}
+int32_t rope_model(ar_gpt* m, float* x, bool inverse) {
+    return rope(m->st, x, x, m->rope_cos, m->rope_sin, m->BT, m->c.n_head, m->c.head_dim, m->period, inverse);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------
+// creation (model.mojo:263-335, 495-571; optimizer.mojo:86-101, 242-253)
+// ------------------------------------------------------------------------
+
+static int32_t gpt_build(ar_gpt* m) {
+    const ar_gpt_config& c = m->c;
+    const int64_t C = c.n_embd, V = c.vocab_size, Lr = c.n_layer, kv = c.kv_dim, F = kMlpExpansion * C;
+    const int64_t BT = m->BT, H = c.n_head, hd = c.head_dim;
+    // Tensor order = train.mojo's optimizer registration order.
+    m->i_wte = add_tensor(m, V, C, "wte");
+    m->i_lm = add_tensor(m, V, C, "lm_head");
+    m->i_res = add_tensor(m, 1, Lr, "resid_lambdas");
+    m->i_x0 = add_tensor(m, 1, Lr, "x0_lambdas");
+    for (int64_t i = 0; i < Lr; ++i) {
+        const std::string p = "h" + std::to_string(i) + ".";
+        m->i_q.push_back(add_tensor(m, C, C, p + "c_q"));
+        m->i_k.push_back(add_tensor(m, kv, C, p + "c_k"));
+        m->i_v.push_back(add_tensor(m, kv, C, p + "c_v"));
+        m->i_proj.push_back(add_tensor(m, C, C, p + "c_proj"));
+        m->i_fc.push_back(add_tensor(m, F, C, p + "c_fc"));
+        m->i_mlpp.push_back(add_tensor(m, C, F, p + "mlp_proj"));
+        if (has_ve(c, i)) {
+            m->i_ve.push_back(add_tensor(m, V, kv, p + "value_embeds"));
+            m->i_gate.push_back(add_tensor(m, c.n_kv_head, kGateChannels, p + "ve_gate"));
+        } else {
+            m->i_ve.push_back(-1);
+            m->i_gate.push_back(-1);
+        }
+    }
+    FALLOC(m->params, m->nparams);
+    FALLOC(m->grads, m->nparams);
+    FALLOC(m->adam_m, m->nparams);
+    FALLOC(m->adam_v, m->nparams);
+    FALLOC(m->muon_buf, m->nparams);
+    AR_TRY(ar_zero_buffer(AS(m), m->adam_m, m->nparams));
+    AR_TRY(ar_zero_buffer(AS(m), m->adam_v, m->nparams));
+    AR_TRY(ar_zero_buffer(AS(m), m->muon_buf, m->nparams));
+    AR_TRY(ar_zero_buffer(AS(m), m->params, m->nparams));
+    AR_TRY(ar_zero_buffer(AS(m), m->grads, m->nparams));
+
+    const int64_t half = hd / 2;
+    m->rope_rows = m->period > 2048 ? m->period : 2048;  // MAX_SEQ_LEN rows (model.mojo:307)
+    FALLOC(m->rope_cos, m->rope_rows * half);
+    FALLOC(m->rope_sin, m->rope_rows * half);
+
+    FALLOC(m->x0, BT * C);
+    FALLOC(m->x, BT * C);
+    FALLOC(m->rms_qk, BT * H);
+    FALLOC(m->proj_out, BT * C);
+    FALLOC(m->mlp_out, BT * C);
+    FALLOC(m->logits, BT * V);
+    FALLOC(m->loss, BT);
+    FALLOC(m->mean_loss, 64);
+    FALLOC(m->x_final, BT * C);
+    FALLOC(m->rms_final, BT);
+    FALLOC(m->d_buf, BT * H);
+    m->L.resize(Lr);
+    for (int64_t i = 0; i < Lr; ++i) {
+        LayerBufs& b = m->L[i];
+        FALLOC(b.x, BT * C);
+        FALLOC(b.xn_attn, BT * C);
+        FALLOC(b.q, BT * C);
+        FALLOC(b.k, BT * kv);
+        FALLOC(b.v, BT * kv);
+        FALLOC(b.lse, BT * H);
+        FALLOC(b.attn_out, BT * C);
+        FALLOC(b.xn_mlp, BT * C);
+        FALLOC(b.mlp_hidden, BT * F);
+        FALLOC(b.mlp_act, BT * F);
+        FALLOC(b.rms_attn, BT);
+        FALLOC(b.rms_mlp, BT);
+        if (has_ve(c, i)) {
+            FALLOC(b.ve, BT * kv);
+            FALLOC(b.gate, BT * H);
+        } else {
+            b.ve = b.gate = nullptr;
+        }
+    }
+    FALLOC(m->grad_x, BT * C);
+    FALLOC(m->grad_x0, BT * C);
+    FALLOC(m->grad_logits, BT * V);
+    FALLOC(m->grad_attn_out, BT * C);
+    FALLOC(m->grad_q, BT * C);
+    FALLOC(m->grad_k, BT * kv);
+    FALLOC(m->grad_v, BT * kv);
+    FALLOC(m->grad_x_norm, BT * C);
+    FALLOC(m->grad_tmp, BT * C);
+    FALLOC(m->grad_mlp, BT * F);
+    FALLOC(m->grad_ve, BT * kv);
+    FALLOC(m->grad_gate, BT * H);
+
+    // Scratch: the largest of every sequential user.
+    int64_t need = kSumBlocks + 64;
+    auto upd = [&](int64_t n) { if (n > need) need = n; };
+    const int64_t dw_shapes[][2] = {{C, C}, {kv, C}, {F, C}, {C, F}, {V, C}};
+    for (auto& s : dw_shapes)
+        upd(gemm_partial_elems(2, BT, s[0], s[1], gemm_auto_splits(2, m->bf16, BT, s[0], s[1])));
+    const int64_t muon_shapes[][2] = {{C, C}, {kv, C}, {F, C}, {C, F}};
+    for (auto& s : muon_shapes) upd(muon_scratch_elems(s[0], s[1], m->bf16));
+    upd(BT * (C > kv ? C : kv));                  // embedding scatter partials
+    upd((int64_t)kGateBlocks * H * kGateChannels);  // ve gate partials
+    m->scratch_elems = need;
+    FALLOC(m->scratch, need);
+    int bits = 1;
+    while ((int64_t(1) << bits) < V) ++bits;
+    m->sort_bits = bits;
+    AR_TRY(dalloc(m, (void**)&m->sorted_ids, (size_t)BT * sizeof(uint32_t)));
+    AR_TRY(dalloc(m, (void**)&m->sorted_tok, (size_t)BT * sizeof(int32_t)));
+    AR_TRY(ar_embedding_sort(AS(m), nullptr, nullptr, nullptr, BT, m->sort_bits, nullptr, 0, &m->sort_bytes));
+    AR_TRY(dalloc(m, &m->sort_scratch, m->sort_bytes));
+    return AR_OK;
+}
+
+extern "C" int32_t ar_gpt_create(ar_gpt** out, const ar_gpt_config* cfg, int64_t B, int64_t T, int32_t precision,
+                                 int64_t rope_period, ar_stream_t stream) {
+    AR_CHECK_ARG(out && cfg, "gpt_create: null pointer");
+    const ar_gpt_config& c = *cfg;
+    AR_CHECK_ARG(B > 0 && T > 0 && c.n_layer > 0 && c.n_head > 0 && c.head_dim > 0 && c.n_embd > 0 &&
+                     c.vocab_size > 0,
+                 "gpt_create: bad config");
+    AR_CHECK_ARG(c.n_head * c.head_dim == c.n_embd && c.kv_dim == c.n_embd && c.n_kv_head == c.n_head,
+                 "gpt_create: the reference model needs n_head*head_dim == n_embd == kv_dim, n_kv_head == n_head");
+    AR_CHECK_ARG(c.n_embd % 8 == 0 && c.vocab_size % 8 == 0 && (B * T) % 8 == 0,
+                 "gpt_create: n_embd, vocab_size and B*T must be multiples of 8");
+    AR_CHECK_ARG(c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128, "gpt_create: head_dim must be 32/64/128");
+    AR_CHECK_ARG(precision == AR_PREC_FP32 || precision == AR_PREC_BF16, "gpt_create: bad precision");
+    AR_CHECK_ARG(rope_period >= 0, "gpt_create: bad rope_period");
+    ar_gpt* m = new ar_gpt();
+    m->c = c;
+    m->B = B;
+    m->T = T;
+    m->BT = B * T;
+    m->period = rope_period > 0 ? rope_period : B * T;
+    m->bf16 = precision == AR_PREC_BF16;
+    m->st = S(stream);
+    int32_t r = gpt_build(m);
+    if (r != AR_OK) {
+        ar_gpt_destroy(m);
+        return r;
+    }
+    *out = m;
+    return AR_OK;
+}
+
+extern "C" int32_t ar_gpt_destroy(ar_gpt* m) {
+    if (!m) return AR_OK;
+    hipStreamSynchronize(m->st);
+    for (hipEvent_t e : m->ev) hipEventDestroy(e);
+    for (void* p : m->allocs) hipFree(p);
+    delete m;
+    return AR_OK;
+}
+
+extern "C" int64_t ar_gpt_num_tensors(const ar_gpt* m) { return (int64_t)m->t.size(); }
+extern "C" int64_t ar_gpt_tensor_info(const ar_gpt* m, int64_t i, int64_t* offset, const char** name) {
+    if (i < 0 || i >= (int64_t)m->t.size()) return -1;
+    if (offset) *offset = m->t[i].offset;
+    if (name) *name = m->t[i].name.c_str();
+    return m->t[i].size;
+}
+extern "C" int64_t ar_gpt_num_params(const ar_gpt* m) { return m->nparams; }
+extern "C" float* ar_gpt_params(ar_gpt* m) { return m->params; }
+extern "C" float* ar_gpt_grads(ar_gpt* m) { return m->grads; }
+extern "C" float* ar_gpt_token_loss(ar_gpt* m) { return m->loss; }
+extern "C" float* ar_gpt_mean_loss(ar_gpt* m) { return m->mean_loss; }
+
+// model.mojo:337-427
+extern "C" int32_t ar_gpt_init_weights(ar_gpt* m, uint64_t seed0) {
+    const ar_gpt_config& c = m->c;
+    const int64_t C = c.n_embd, V = c.vocab_size, Lr = c.n_layer, kv = c.kv_dim, F = kMlpExpansion * C;
+    const float s = (float)(sqrt(3.0) * pow((double)C, -0.5));
+    uint64_t seed = seed0;
+    ar_stream_t st = AS(m);
+    AR_TRY(ar_fill_normal(st, P(m, m->i_wte), seed, 1.0f, V * C)); seed++;
+    AR_TRY(ar_fill_normal(st, P(m, m->i_lm), seed, 0.001f, V * C)); seed++;
+    AR_TRY(ar_fill_value(st, P(m, m->i_res), 1.0f, Lr));
+    AR_TRY(ar_fill_value(st, P(m, m->i_x0), 0.1f, Lr));
+    for (int64_t i = 0; i < Lr; ++i) {
+        AR_TRY(ar_fill_uniform(st, P(m, m->i_q[i]), seed, -s, s, C * C)); seed++;
+        AR_TRY(ar_fill_uniform(st, P(m, m->i_k[i]), seed, -s, s, kv * C)); seed++;
+        AR_TRY(ar_fill_uniform(st, P(m, m->i_v[i]), seed, -s, s, kv * C)); seed++;
+        AR_TRY(ar_fill_zeros(st, P(m, m->i_proj[i]), C * C));
+        AR_TRY(ar_fill_uniform(st, P(m, m->i_fc[i]), seed, -s, s, F * C)); seed++;
+        AR_TRY(ar_fill_zeros(st, P(m, m->i_mlpp[i]), C * F));
+        if (has_ve(c, i)) {
+            AR_TRY(ar_fill_uniform(st, P(m, m->i_ve[i]), seed, -s, s, V * kv)); seed++;
+            AR_TRY(ar_fill_zeros(st, P(m, m->i_gate[i]), c.n_kv_head * kGateChannels));
+        }
+    }
+    AR_TRY(ar_precompute_rope(st, m->rope_cos, m->rope_sin, m->rope_rows, c.head_dim, 10000.0));  // config.mojo:87
+    if (hipStreamSynchronize(m->st) != hipSuccess) return set_error(AR_EHIP, "gpt_init_weights: sync failed");
+    return AR_OK;
+}
+
+// model.mojo:777-814
+extern "C" int32_t ar_gpt_zero_grads(ar_gpt* m) { return ar_zero_buffer(AS(m), m->grads, m->nparams); }
+
+// model.mojo:576-772
+extern "C" int32_t ar_gpt_forward(ar_gpt* m, const int64_t* inputs, const int64_t* targets, float* loss_host) {
+    AR_CHECK_ARG(m && inputs && targets, "gpt_forward: null pointer");
+    const ar_gpt_config& c = m->c;
+    const int64_t C = c.n_embd, V = c.vocab_size, BT = m->BT, H = c.n_head, hd = c.head_dim;
+    const int64_t kv = c.kv_dim, F = kMlpExpansion * C;
+    ar_stream_t st = AS(m);
+    AR_TRY(ar_embedding_fwd(st, m->x0, P(m, m->i_wte), inputs, BT, C));
+    AR_TRY(ar_rmsnorm_fwd(st, m->x0, m->rms_final, m->x0, BT, C));  // rms discarded, as bufs.rms
+    for (int64_t i = 0; i < c.n_layer; ++i) {
+        LayerBufs& b = m->L[i];
+        const float* xin = i == 0 ? m->x0 : m->x;
+        AR_TRY(ar_scaled_add_fwd(st, b.x, xin, m->x0, P(m, m->i_res), P(m, m->i_x0), i, BT * C));
+        AR_TRY(ar_rmsnorm_fwd(st, b.xn_attn, b.rms_attn, b.x, BT, C));
+        AR_TRY(linear(m, b.q, b.xn_attn, P(m, m->i_q[i]), BT, C, C));
+        AR_TRY(linear(m, b.k, b.xn_attn, P(m, m->i_k[i]), BT, kv, C));
+        AR_TRY(linear(m, b.v, b.xn_attn, P(m, m->i_v[i]), BT, kv, C));
+        if (has_ve(c, i)) {
+            AR_TRY(ar_embedding_fwd(st, b.ve, P(m, m->i_ve[i]), inputs, BT, kv));
+            AR_TRY(ar_ve_gate_fwd(st, b.gate, b.xn_attn, P(m, m->i_gate[i]), BT, H, kGateChannels, C));
+            AR_TRY(ar_ve_apply_fwd(st, b.v, b.gate, b.ve, BT, H, hd));
+        }
+        AR_TRY(rope_model(m, b.q, false));
+        AR_TRY(rope_model(m, b.k, false));
+        AR_TRY(ar_rmsnorm_fwd(st, b.q, m->rms_qk, b.q, BT * H, hd));
+        AR_TRY(ar_rmsnorm_fwd(st, b.k, m->rms_qk, b.k, BT * H, hd));
+        AR_TRY(attention(m, AttnOp::FWD, b.attn_out, b.lse, b.q, b.k, b.v, nullptr, nullptr, nullptr,
+                         window_size(c, i)));
+        AR_TRY(linear(m, m->proj_out, b.attn_out, P(m, m->i_proj[i]), BT, C, C));
+        AR_TRY(ar_add_residual_fwd(st, m->x, b.x, m->proj_out, BT * C));
+        AR_TRY(ar_rmsnorm_fwd(st, b.xn_mlp, b.rms_mlp, m->x, BT, C));
+        AR_TRY(linear(m, b.mlp_hidden, b.xn_mlp, P(m, m->i_fc[i]), BT, F, C));
+        AR_TRY(ar_relu_squared_fwd(st, b.mlp_act, b.mlp_hidden, BT * F));
+        AR_TRY(linear(m, m->mlp_out, b.mlp_act, P(m, m->i_mlpp[i]), BT, C, F));
+        AR_TRY(ar_add_residual_fwd(st, m->x, m->x, m->mlp_out, BT * C));
+    }
+    // m->x is the saved pre-final x.
+    AR_TRY(ar_rmsnorm_fwd(st, m->x_final, m->rms_final, m->x, BT, C));
+    AR_TRY(linear(m, m->logits, m->x_final, P(m, m->i_lm), BT, V, C));
+    AR_TRY(ar_softcap_fwd(st, m->logits, m->logits, kSoftcap, BT * V));
+    AR_TRY(ar_cross_entropy_fwd(st, m->loss, m->logits, targets, BT, V));
+    AR_TRY(fixed_sum(m->st, m->mean_loss, m->loss, nullptr, BT, 0, 0, 0, m->scratch));
+    if (loss_host) {
+        if (hipMemcpyAsync(loss_host, m->mean_loss, sizeof(float), hipMemcpyDeviceToHost, m->st) != hipSuccess ||
+            hipStreamSynchronize(m->st) != hipSuccess)
+            return set_error(AR_EHIP, "gpt_forward: loss copy failed");
+    }
+    return AR_OK;
+}
+
+// model.mojo:819-1037 (quirks Q4-Q10 of the reference backward reproduced)
+extern "C" int32_t ar_gpt_backward(ar_gpt* m, const int64_t* inputs, const int64_t* targets, float loss_scale) {
+    AR_CHECK_ARG(m && inputs && targets, "gpt_backward: null pointer");
+    const ar_gpt_config& c = m->c;
+    const int64_t C = c.n_embd, V = c.vocab_size, BT = m->BT, H = c.n_head, hd = c.head_dim;
+    const int64_t kv = c.kv_dim, F = kMlpExpansion * C;
+    ar_stream_t st = AS(m);
+    AR_TRY(ar_embedding_sort(st, m->sorted_ids, m->sorted_tok, inputs, BT, m->sort_bits, m->sort_scratch,
+                             m->sort_bytes, nullptr));
+    AR_TRY(ar_cross_entropy_softcap_bwd(st, m->grad_logits, m->logits, targets, kSoftcap, BT, V, loss_scale));
+    AR_TRY(linear_dx(m, m->grad_x, m->grad_logits, P(m, m->i_lm), BT, V, C));
+    AR_TRY(linear_dw(m, G(m, m->i_lm), m->grad_logits, m->x_final, BT, V, C));
+    AR_TRY(ar_rmsnorm_bwd(st, m->grad_x, m->grad_x, m->x, m->rms_final, BT, C));
+    for (int64_t r = 0; r < c.n_layer; ++r) {
+        const int64_t i = c.n_layer - 1 - r;
+        LayerBufs& b = m->L[i];
+        // MLP block; dY of mlp_proj is grad_x itself (model.mojo:873 copy elided)
+        AR_TRY(linear_dx(m, m->grad_mlp, m->grad_x, P(m, m->i_mlpp[i]), BT, C, F));
+        AR_TRY(linear_dw(m, G(m, m->i_mlpp[i]), m->grad_x, b.mlp_act, BT, C, F));
+        AR_TRY(ar_relu_squared_bwd(st, m->grad_mlp, m->grad_mlp, b.mlp_hidden, BT * F));
+        AR_TRY(linear_dx(m, m->grad_x_norm, m->grad_mlp, P(m, m->i_fc[i]), BT, F, C));
+        AR_TRY(linear_dw(m, G(m, m->i_fc[i]), m->grad_mlp, b.xn_mlp, BT, F, C));
+        AR_TRY(ar_rmsnorm_bwd(st, m->grad_x_norm, m->grad_x_norm, b.x, b.rms_mlp, BT, C));  // Q7
+        AR_TRY(ar_add_residual_fwd(st, m->grad_x, m->grad_x, m->grad_x_norm, BT * C));
+        // attention output projection (Q2: read all of dY, then write dX)
+        AR_TRY(linear_dx(m, m->grad_attn_out, m->grad_x, P(m, m->i_proj[i]), BT, C, C));
+        AR_TRY(linear_dw(m, G(m, m->i_proj[i]), m->grad_x, b.attn_out, BT, C, C));
+        const int64_t ws = window_size(c, i);
+        AR_TRY(ar_flash_attn_bwd_precompute_d(st, m->d_buf, b.attn_out, m->grad_attn_out, m->B, m->T, H, hd));
+        AR_TRY(attention(m, AttnOp::DQ, m->grad_q, nullptr, b.q, b.k, b.v, m->grad_attn_out, b.lse, m->d_buf, ws));
+        AR_TRY(attention(m, AttnOp::DKV, m->grad_k, m->grad_v, b.q, b.k, b.v, m->grad_attn_out, b.lse, m->d_buf,
+                         ws));
+        // Q6: q/k per-head norm backward skipped
+        if (has_ve(c, i)) {
+            AR_TRY(ar_ve_apply_bwd(st, m->grad_ve, m->grad_gate, m->grad_v, b.gate, b.ve, BT, H, hd));
+            AR_TRY(ar_embedding_bwd_sorted(st, G(m, m->i_ve[i]), m->grad_ve, m->sorted_ids, m->sorted_tok, BT, kv,
+                                           m->scratch));
+        }
+        AR_TRY(rope_model(m, m->grad_q, true));
+        AR_TRY(rope_model(m, m->grad_k, true));
+        AR_TRY(linear_dx(m, m->grad_x_norm, m->grad_q, P(m, m->i_q[i]), BT, C, C));
+        AR_TRY(linear_dw(m, G(m, m->i_q[i]), m->grad_q, b.xn_attn, BT, C, C));
+        AR_TRY(linear_dx(m, m->grad_tmp, m->grad_k, P(m, m->i_k[i]), BT, kv, C));
+        AR_TRY(ar_add_residual_fwd(st, m->grad_x_norm, m->grad_x_norm, m->grad_tmp, BT * C));
+        AR_TRY(linear_dw(m, G(m, m->i_k[i]), m->grad_k, b.xn_attn, BT, kv, C));
+        AR_TRY(linear_dx(m, m->grad_tmp, m->grad_v, P(m, m->i_v[i]), BT, kv, C));
+        AR_TRY(ar_add_residual_fwd(st, m->grad_x_norm, m->grad_x_norm, m->grad_tmp, BT * C));
+        AR_TRY(linear_dw(m, G(m, m->i_v[i]), m->grad_v, b.xn_attn, BT, kv, C));
+        if (has_ve(c, i))
+            AR_TRY(ve_gate_bwd(m->st, m->grad_x_norm, G(m, m->i_gate[i]), m->grad_gate, b.gate, b.xn_attn,
+                               P(m, m->i_gate[i]), BT, H, kGateChannels, C, m->scratch));
+        AR_TRY(ar_rmsnorm_bwd(st, m->grad_x_norm, m->grad_x_norm, b.x, b.rms_attn, BT, C));
+        AR_TRY(ar_add_residual_fwd(st, m->grad_x, m->grad_x, m->grad_x_norm, BT * C));
+        // Q8: post-scaled-add saved x; Q9: grad_x0 assigned and never consumed
+        AR_TRY(fixed_sum(m->st, G(m, m->i_res), m->grad_x, b.x, BT * C, 2, 1, i, m->scratch));
+        AR_TRY(fixed_sum(m->st, G(m, m->i_x0), m->grad_x, m->x0, BT * C, 2, 1, i, m->scratch));
+        AR_TRY(ar_scaled_add_bwd(st, m->grad_x, m->grad_x0, m->grad_x, P(m, m->i_res), P(m, m->i_x0), i, BT * C));
+    }
+    // Q10: embedding norm backward skipped
+    AR_TRY(ar_embedding_bwd_sorted(st, G(m, m->i_wte), m->grad_x, m->sorted_ids, m->sorted_tok, BT, C, m->scratch));
+    return AR_OK;
+}
+
+// train.mojo:25-33
+static double lr_multiplier(double progress) {
+    const double kWarmup = 0.0, kWarmdown = 0.5, kFinal = 0.0;  // config.mojo:81-83
+    if (progress < kWarmup) return kWarmup > 0 ? progress / kWarmup : 1.0;
+    if (progress < 1.0 - kWarmdown) return 1.0;
+    const double cd = (1.0 - progress) / kWarmdown;
+    return cd + (1.0 - cd) * kFinal;
+}
+
+// train.mojo:246-281
+extern "C" int32_t ar_gpt_optimizer_step(ar_gpt* m, double progress) {
+    AR_CHECK_ARG(m != nullptr, "gpt_optimizer_step: null model");
+    const ar_gpt_config& c = m->c;
+    if (progress > 1.0) progress = 1.0;
+    const double lrm = lr_multiplier(progress);
+    const double lr_scale = pow((double)c.n_embd / 768.0, -0.5);  // train.mojo:167
+    m->adam_step += 1;
+    ar_stream_t st = AS(m);
+    auto adam = [&](int64_t ti, double lr, double b1) -> int32_t {
+        const Tensor& t = m->t[ti];
+        return ar_adamw_step_group(st, m->params + t.offset, m->grads + t.offset, m->adam_m + t.offset,
+                                   m->adam_v + t.offset, t.size, lr, b1, 0.95, 1e-10, 0.0, lrm, m->adam_step);
+    };
+    AR_TRY(adam(m->i_lm, 0.004 * lr_scale, 0.8));   // UNEMBEDDING_LR
+    AR_TRY(adam(m->i_wte, 0.6 * lr_scale, 0.8));    // EMBEDDING_LR
+    AR_TRY(adam(m->i_res, 0.5 * 0.01, 0.8));        // SCALAR_LR * 0.01
+    AR_TRY(adam(m->i_x0, 0.5, 0.96));               // SCALAR_LR, beta1 0.96
+    for (int64_t i = 0; i < c.n_layer; ++i)
+        if (has_ve(c, i)) {
+            AR_TRY(adam(m->i_ve[i], 0.6 * lr_scale, 0.8));
+            AR_TRY(adam(m->i_gate[i], 0.04, 0.8));  // MATRIX_LR
+        }
+    double frac = (double)m->adam_step / 300.0;
+    if (frac > 1.0) frac = 1.0;
+    const double mu = (1.0 - frac) * 0.85 + frac * 0.95;
+    const double wd = 0.2 * (1.0 - progress);
+    for (int64_t i = 0; i < c.n_layer; ++i) {
+        const int64_t ids[6] = {m->i_q[i], m->i_k[i], m->i_v[i], m->i_proj[i], m->i_fc[i], m->i_mlpp[i]};
+        for (int j = 0; j < 6; ++j) {
+            const Tensor& t = m->t[ids[j]];
+            const int e = prof_begin(m);
+            AR_TRY(muon_step(m->st, m->params + t.offset, m->grads + t.offset, m->muon_buf + t.offset, t.rows, t.cols,
+                             0.04, lrm, mu, wd, m->bf16, m->scratch));
+            const double sm = (double)(t.rows < t.cols ? t.rows : t.cols), lg = (double)(t.rows < t.cols ? t.cols : t.rows);
+            prof_end(m, e, 6, 5.0 * (4.0 * lg * sm * sm + 2.0 * sm * sm * sm));
+        }
+    }
+    return AR_OK;
+}
+
+// train.mojo:231-282
+extern "C" int32_t ar_gpt_train_step(ar_gpt* m, const int64_t* inputs, const int64_t* targets, double progress,
+                                     float* loss_host) {
+    AR_TRY(ar_gpt_zero_grads(m));
+    AR_TRY(ar_gpt_forward(m, inputs, targets, nullptr));
+    AR_TRY(ar_gpt_backward(m, inputs, targets, 1.0f));
+    AR_TRY(ar_gpt_optimizer_step(m, progress));
+    if (loss_host) {
+        if (hipMemcpyAsync(loss_host, m->mean_loss, sizeof(float), hipMemcpyDeviceToHost, m->st) != hipSuccess ||
+            hipStreamSynchronize(m->st) != hipSuccess)
+            return set_error(AR_EHIP, "gpt_train_step: loss copy failed");
+    }
+    return AR_OK;
+}
+
+extern "C" int32_t ar_gpt_profile(ar_gpt* m, int32_t enable) {
+    AR_CHECK_ARG(m != nullptr, "gpt_profile: null model");
+    if (hipStreamSynchronize(m->st) != hipSuccess) return set_error(AR_EHIP, "gpt_profile: sync failed");
+    m->prof = enable != 0;
+    m->recs.clear();
+    m->ev_used = 0;
+    return AR_OK;
+}
+
+extern "C" int32_t ar_gpt_profile_read(ar_gpt* m, int32_t cls, double* ms, int64_t* launches, double* flops) {
+    AR_CHECK_ARG(m && ms && launches && flops, "gpt_profile_read: null pointer");
+    if (hipStreamSynchronize(m->st) != hipSuccess) return set_error(AR_EHIP, "gpt_profile_read: sync failed");
+    double t = 0, f = 0;
+    int64_t n = 0;
+    for (const auto& r : m->recs) {
+        if (r.cls != cls) continue;
+        float e = 0.f;
+        if (hipEventElapsedTime(&e, m->ev[r.e0], m->ev[r.e1]) != hipSuccess)
+            return set_error(AR_EHIP, "gpt_profile_read: elapsed time failed");
+        t += e;
+        f += r.flops;
+        ++n;
+    }
+    *ms = t;
+    *launches = n;
+    *flops = f;
+    return AR_OK;
+}

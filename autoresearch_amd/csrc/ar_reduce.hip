@@ -1,0 +1,549 @@
+// ar_reduce.hip -- row-reduction kernels: RMSNorm fwd/bwd, softmax, cross
+// entropy fwd/bwd, mean, the value-embedding gate kernels, the learned-scalar
+// gradient reduction, the Frobenius normalisation and the deterministic
+// embedding scatter.
+//
+// Reductions never use float atomics: multi-block sums write per-block
+// partials in a fixed assignment and a second kernel adds them in a fixed
+// order, so every result is run-to-run deterministic (the reference's float
+// atomics, ops.mojo:1160-1164 / 1267-1274 / 1307-1308, are not).
+#include <hipcub/hipcub.hpp>
+
+#include "ar_internal.hpp"
+
+using namespace ar;
+
+namespace {
+
+constexpr int kBlock = 256;
+__host__ __device__ inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// ---------------- K2 rmsnorm_fwd (ops.mojo:61-104): one wave per row ----------------
+template <bool VEC>
+__global__ void rmsnorm_fwd_k(float* out, float* rms_out, const float* in, int64_t rows, int64_t dim) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+    const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) / kWave;
+    for (int64_t r = wave; r < rows; r += nwaves) {
+        const float* x = in + r * dim;
+        float* y = out + r * dim;
+        float ss = 0.f;
+        if (VEC) {
+            for (int64_t i = lane; i < dim / 4; i += kWave) {
+                float4 v = reinterpret_cast<const float4*>(x)[i];
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+        } else {
+            for (int64_t i = lane; i < dim; i += kWave) ss += x[i] * x[i];
+        }
+        ss = wave_sum(ss);
+        const float rms = sqrtf(ss / (float)dim + 1e-5f);
+        if (lane == 0 && rms_out) rms_out[r] = rms;
+        if (VEC) {
+            for (int64_t i = lane; i < dim / 4; i += kWave) {
+                float4 v = reinterpret_cast<const float4*>(x)[i];
+                reinterpret_cast<float4*>(y)[i] = make_float4(v.x / rms, v.y / rms, v.z / rms, v.w / rms);
+            }
+        } else {
+            for (int64_t i = lane; i < dim; i += kWave) y[i] = x[i] / rms;
+        }
+    }
+}
+
+// ---------------- K21 rmsnorm_bwd (ops.mojo:1039-1085) ----------------
+template <bool VEC>
+__global__ void rmsnorm_bwd_k(float* dx, const float* dy, const float* x, const float* rms, int64_t rows,
+                              int64_t dim) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+    const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) / kWave;
+    for (int64_t r = wave; r < rows; r += nwaves) {
+        const float* xr = x + r * dim;
+        const float* gr = dy + r * dim;
+        float* o = dx + r * dim;
+        float dot = 0.f;
+        if (VEC) {
+            for (int64_t i = lane; i < dim / 4; i += kWave) {
+                float4 a = reinterpret_cast<const float4*>(xr)[i];
+                float4 g = reinterpret_cast<const float4*>(gr)[i];
+                dot += a.x * g.x + a.y * g.y + a.z * g.z + a.w * g.w;
+            }
+        } else {
+            for (int64_t i = lane; i < dim; i += kWave) dot += gr[i] * xr[i];
+        }
+        dot = wave_sum(dot);
+        const float rr = rms[r];
+        const float coef = dot / ((float)dim * (rr * rr));
+        if (VEC) {
+            for (int64_t i = lane; i < dim / 4; i += kWave) {
+                float4 a = reinterpret_cast<const float4*>(xr)[i];
+                float4 g = reinterpret_cast<const float4*>(gr)[i];
+                reinterpret_cast<float4*>(o)[i] = make_float4((g.x - a.x * coef) / rr, (g.y - a.y * coef) / rr,
+                                                              (g.z - a.z * coef) / rr, (g.w - a.w * coef) / rr);
+            }
+        } else {
+            for (int64_t i = lane; i < dim; i += kWave) o[i] = (gr[i] - xr[i] * coef) / rr;
+        }
+    }
+}
+
+// Online (max, sum-exp) over one row by a block; every thread gets (m, s).
+__device__ __forceinline__ void row_max_sumexp(const float* row, int64_t n, float* red, float& m_out, float& s_out) {
+    float m = -INFINITY, s = 0.f;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = row[i];
+        if (v > m) {
+            s = s * __expf(m - v) + 1.f;
+            m = v;
+        } else {
+            s += __expf(v - m);
+        }
+    }
+    const float bm = block_max(m, red);
+    s = (m == -INFINITY) ? 0.f : s * __expf(m - bm);
+    const float bs = block_sum(s, red + 32);
+    m_out = bm;
+    s_out = bs;
+}
+
+// ---------------- K16 cross_entropy_fwd (ops.mojo:672-740) ----------------
+__global__ void ce_fwd_k(float* loss, const float* logits, const int64_t* targets, int64_t V) {
+    __shared__ float red[64];
+    const int64_t t = blockIdx.x;
+    const float* row = logits + t * V;
+    float m, s;
+    row_max_sumexp(row, V, red, m, s);
+    if (threadIdx.x == 0) {
+        const int64_t tg = targets[t];
+        const float lse = m + logf(s);
+        loss[t] = tg >= 0 ? -row[tg] + lse : 0.f;
+    }
+}
+
+// ---------------- K18 cross_entropy_softcap_bwd (ops.mojo:778-864) ----------------
+__global__ void ce_bwd_k(float* grad, const float* logits, const int64_t* targets, int64_t V, float loss_scale) {
+    __shared__ float red[64];
+    const int64_t t = blockIdx.x;
+    const int64_t tg = targets[t];
+    float* g = grad + t * V;
+    if (tg < 0) {
+        for (int64_t i = threadIdx.x; i < V; i += blockDim.x) g[i] = 0.f;
+        return;
+    }
+    const float* row = logits + t * V;
+    float m, s;
+    row_max_sumexp(row, V, red, m, s);
+    for (int64_t i = threadIdx.x; i < V; i += blockDim.x) {
+        const float sm = __expf(row[i] - m) / s;
+        g[i] = (i == tg ? sm - 1.0f : sm) * loss_scale;
+    }
+}
+
+// ---------------- K15 softmax_fwd (ops.mojo:600-666) ----------------
+__global__ void softmax_k(float* out, const float* in, int64_t cols) {
+    __shared__ float red[64];
+    const int64_t r = blockIdx.x;
+    float m, s;
+    row_max_sumexp(in + r * cols, cols, red, m, s);
+    for (int64_t i = threadIdx.x; i < cols; i += blockDim.x) out[r * cols + i] = __expf(in[r * cols + i] - m) / s;
+}
+
+// ---------------- fixed-order multi-block sums ----------------
+// kSumBlocks (ar_internal.hpp) is fixed: the partial assignment never depends
+// on the device.
+
+// partial[b] = sum over i in block b's grid-stride set of a[i]*(b? b[i] : a[i]) or a[i]
+__global__ void dot_partial_k(float* partial, const float* a, const float* b, int64_t n, int mode) {
+    __shared__ float red[16];
+    float s = 0.f;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const float x = a[i];
+        s += mode == 0 ? x : (mode == 1 ? x * x : x * b[i]);
+    }
+    s = block_sum(s, red);
+    if (threadIdx.x == 0) partial[blockIdx.x] = s;
+}
+
+// mode 0: out[idx] = total / n (mean); mode 1: out[idx] += total;
+// mode 2: out[0] = 1 / (sqrt(total) * 1.02 + 1e-6) (Frobenius scale, optimizer.mojo:178)
+__global__ void finish_sum_k(float* out, const float* partial, int np, int64_t idx, int64_t n, int mode) {
+    __shared__ float red[16];
+    float s = 0.f;
+    for (int i = threadIdx.x; i < np; i += blockDim.x) s += partial[i];
+    s = block_sum(s, red);
+    if (threadIdx.x == 0) {
+        if (mode == 0) out[idx] = s / (float)n;
+        else if (mode == 1) out[idx] += s;
+        else out[0] = 1.0f / (sqrtf(s) * 1.02f + 1e-6f);
+    }
+}
+
+__global__ void scale_by_device_scalar_k(float* x, const float* scale, int64_t n) {
+    const float sc = scale[0];
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        x[i] = x[i] * sc;
+}
+
+// ---------------- K6 flash_attn_bwd_precompute_d (ops.mojo:329-346) ----------------
+__global__ void precompute_d_k(float* d, const float* o, const float* g, int64_t rows, int64_t hd) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+    const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) / kWave;
+    for (int64_t r = wave; r < rows; r += nwaves) {
+        float s = 0.f;
+        for (int64_t i = lane; i < hd; i += kWave) s += o[r * hd + i] * g[r * hd + i];
+        s = wave_sum(s);
+        if (lane == 0) d[r] = s;
+    }
+}
+
+// ---------------- K11 ve_gate_fwd (ops.mojo:516-541) ----------------
+__global__ void ve_gate_fwd_k(float* gate, const float* xn, const float* w, int64_t nt, int64_t nkv, int64_t gc,
+                              int64_t C) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nt * nkv;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = i / nkv, h = i % nkv;
+        float acc = 0.f;
+        for (int64_t c = 0; c < gc; ++c) acc += w[h * gc + c] * xn[t * C + c];
+        gate[i] = 2.0f * (1.0f / (1.0f + __expf(-acc)));
+    }
+}
+
+// ---------------- K26 ve_apply_bwd (ops.mojo:1193-1237): one wave per (t,h) ----------------
+__global__ void ve_apply_bwd_k(float* gve, float* ggate, const float* gv, const float* gate, const float* ve,
+                               int64_t rows, int64_t hd) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+    const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) / kWave;
+    for (int64_t r = wave; r < rows; r += nwaves) {
+        const float g = gate[r];
+        float dg = 0.f;
+        for (int64_t d = lane; d < hd; d += kWave) {
+            const float x = gv[r * hd + d];
+            gve[r * hd + d] = g * x;
+            dg += ve[r * hd + d] * x;
+        }
+        dg = wave_sum(dg);
+        if (lane == 0) ggate[r] = dg;
+    }
+}
+
+// ---------------- K27 ve_gate_bwd (ops.mojo:1240-1274), deterministic ----------------
+// Block b owns a fixed token range.  Thread (c = tid % 64, j = tid / 64):
+// gx[t,c] += sum_h dz[t,h] W[h,c] for its tokens (no conflicts), and a
+// per-block partial of gW[h,c] = sum_t dz[t,h] x[t,c] reduced over j in LDS.
+constexpr int kGateMaxH = 16;
+
+__global__ void ve_gate_bwd_partial_k(float* gx, float* partial, const float* ggate, const float* gate,
+                                      const float* xn, const float* w, int64_t nt, int64_t nkv, int64_t gc,
+                                      int64_t C) {
+    __shared__ float acc_s[4][kGateMaxH][64];
+    const int c = threadIdx.x % 64, j = threadIdx.x / 64;
+    const int64_t per = (nt + gridDim.x - 1) / gridDim.x;
+    const int64_t t0 = (int64_t)blockIdx.x * per;
+    const int64_t t1 = t0 + per < nt ? t0 + per : nt;
+    float accw[kGateMaxH];
+    for (int h = 0; h < kGateMaxH; ++h) accw[h] = 0.f;
+    if (c < gc) {
+        for (int64_t t = t0 + j; t < t1; t += 4) {
+            const float x = xn[t * C + c];
+            float ax = 0.f;
+            for (int64_t h = 0; h < nkv; ++h) {
+                const float g = gate[t * nkv + h];
+                const float dz = ggate[t * nkv + h] * g * (1.0f - g / 2.0f);
+                ax += dz * w[h * gc + c];
+                accw[h] += dz * x;
+            }
+            gx[t * C + c] += ax;
+        }
+    }
+    for (int h = 0; h < kGateMaxH; ++h) acc_s[j][h][c] = accw[h];
+    __syncthreads();
+    if (j == 0 && c < gc) {
+        for (int64_t h = 0; h < nkv; ++h) {
+            const float s = ((acc_s[0][h][c] + acc_s[1][h][c]) + acc_s[2][h][c]) + acc_s[3][h][c];
+            partial[(int64_t)blockIdx.x * nkv * gc + h * gc + c] = s;
+        }
+    }
+}
+
+__global__ void ve_gate_bwd_finish_k(float* gw, const float* partial, int nblocks, int64_t n) {
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+        float s = 0.f;
+        for (int b = 0; b < nblocks; ++b) s += partial[(int64_t)b * n + i];
+        gw[i] += s;
+    }
+}
+
+// ---------------- K24 embedding_bwd: deterministic sorted scatter ----------------
+// Tokens are stably sorted by id.  The sorted list is cut into chunks: a chunk
+// starts at every position p with p % kEmbChunk == 0 or id[p] != id[p-1].
+// A chunk's rows are summed in token order (starting from its first row);
+// then each id's row is G[v] = ((G[v] + chunk_0) + chunk_1) + ... in order.
+constexpr int kEmbChunk = 64;
+
+__global__ void emb_keys_k(uint32_t* keys, int32_t* vals, const int64_t* idx, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        keys[i] = (uint32_t)idx[i];
+        vals[i] = (int32_t)i;
+    }
+}
+
+__device__ __forceinline__ bool emb_chunk_start(const uint32_t* k, int64_t p) {
+    return p == 0 || (p % kEmbChunk) == 0 || k[p] != k[p - 1];
+}
+
+__global__ void emb_chunk_sum_k(float* partial, const uint32_t* keys, const int32_t* tok, const float* dy,
+                                int64_t n, int64_t dim) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t p = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+    if (p >= n || !emb_chunk_start(keys, p)) return;
+    int64_t q = p + 1;
+    while (q < n && (q % kEmbChunk) != 0 && keys[q] == keys[p]) ++q;
+    for (int64_t d = lane; d < dim; d += kWave) {
+        float s = dy[(int64_t)tok[p] * dim + d];
+        for (int64_t r = p + 1; r < q; ++r) s += dy[(int64_t)tok[r] * dim + d];
+        partial[p * dim + d] = s;
+    }
+}
+
+__global__ void emb_segment_apply_k(float* gw, const float* partial, const uint32_t* keys, int64_t n, int64_t dim) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t p = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+    if (p >= n || !(p == 0 || keys[p] != keys[p - 1])) return;
+    const uint32_t v = keys[p];
+    int64_t end = p + 1;
+    while (end < n && keys[end] == v) ++end;
+    float* row = gw + (int64_t)v * dim;
+    for (int64_t d = lane; d < dim; d += kWave) {
+        float acc = row[d];
+        for (int64_t c = p; c < end; c = (c / kEmbChunk + 1) * kEmbChunk) acc += partial[c * dim + d];
+        row[d] = acc;
+    }
+}
+
+}  // namespace
+
+// =====================================================================
+// C ABI
+// =====================================================================
+
+static unsigned wave_grid(int64_t rows) { return flat_grid(rows, kBlock / kWave); }
+
+extern "C" int32_t ar_rmsnorm_fwd(ar_stream_t stream, float* output, float* rms_out, const float* input,
+                                  int64_t num_rows, int64_t dim) {
+    AR_CHECK_ARG(output && input, "rmsnorm_fwd: null pointer");
+    AR_CHECK_ARG(num_rows >= 0 && dim > 0, "rmsnorm_fwd: bad shape");
+    if (num_rows == 0) return AR_OK;
+    if (dim % 4 == 0 && al16(output) && al16(input))
+        rmsnorm_fwd_k<true><<<wave_grid(num_rows), kBlock, 0, S(stream)>>>(output, rms_out, input, num_rows, dim);
+    else
+        rmsnorm_fwd_k<false><<<wave_grid(num_rows), kBlock, 0, S(stream)>>>(output, rms_out, input, num_rows, dim);
+    return AR_LAUNCH_CHECK("rmsnorm_fwd");
+}
+
+extern "C" int32_t ar_rmsnorm_bwd(ar_stream_t stream, float* grad_input, const float* grad_output,
+                                  const float* input, const float* rms_saved, int64_t num_rows, int64_t dim) {
+    AR_CHECK_ARG(grad_input && grad_output && input && rms_saved, "rmsnorm_bwd: null pointer");
+    AR_CHECK_ARG(num_rows >= 0 && dim > 0, "rmsnorm_bwd: bad shape");
+    if (num_rows == 0) return AR_OK;
+    if (dim % 4 == 0 && al16(grad_input) && al16(grad_output) && al16(input))
+        rmsnorm_bwd_k<true><<<wave_grid(num_rows), kBlock, 0, S(stream)>>>(grad_input, grad_output, input,
+                                                                         rms_saved, num_rows, dim);
+    else
+        rmsnorm_bwd_k<false><<<wave_grid(num_rows), kBlock, 0, S(stream)>>>(grad_input, grad_output, input,
+                                                                          rms_saved, num_rows, dim);
+    return AR_LAUNCH_CHECK("rmsnorm_bwd");
+}
+
+extern "C" int32_t ar_cross_entropy_fwd(ar_stream_t stream, float* loss_out, const float* logits,
+                                        const int64_t* targets, int64_t num_tokens, int64_t vocab_size) {
+    AR_CHECK_ARG(loss_out && logits && targets, "cross_entropy_fwd: null pointer");
+    AR_CHECK_ARG(num_tokens >= 0 && vocab_size > 0, "cross_entropy_fwd: bad shape");
+    if (num_tokens == 0) return AR_OK;
+    ce_fwd_k<<<(unsigned)num_tokens, kBlock, 0, S(stream)>>>(loss_out, logits, targets, vocab_size);
+    return AR_LAUNCH_CHECK("cross_entropy_fwd");
+}
+
+extern "C" int32_t ar_cross_entropy_softcap_bwd(ar_stream_t stream, float* grad_logits, const float* logits,
+                                                const int64_t* targets, float cap, int64_t num_tokens,
+                                                int64_t vocab_size, float loss_scale) {
+    (void)cap;  // the softcap derivative is not applied (ops.mojo:854-858)
+    AR_CHECK_ARG(grad_logits && logits && targets, "cross_entropy_softcap_bwd: null pointer");
+    AR_CHECK_ARG(num_tokens >= 0 && vocab_size > 0, "cross_entropy_softcap_bwd: bad shape");
+    if (num_tokens == 0) return AR_OK;
+    ce_bwd_k<<<(unsigned)num_tokens, kBlock, 0, S(stream)>>>(grad_logits, logits, targets, vocab_size, loss_scale);
+    return AR_LAUNCH_CHECK("cross_entropy_softcap_bwd");
+}
+
+extern "C" int32_t ar_softmax_fwd(ar_stream_t stream, float* output, const float* input, int64_t num_rows,
+                                  int64_t cols) {
+    AR_CHECK_ARG(output && input, "softmax_fwd: null pointer");
+    AR_CHECK_ARG(num_rows >= 0 && cols > 0, "softmax_fwd: bad shape");
+    if (num_rows == 0) return AR_OK;
+    softmax_k<<<(unsigned)num_rows, kBlock, 0, S(stream)>>>(output, input, cols);
+    return AR_LAUNCH_CHECK("softmax_fwd");
+}
+
+namespace ar {
+int32_t fixed_sum(hipStream_t st, float* out, const float* a, const float* b, int64_t n, int mode_in, int mode_out,
+                  int64_t idx, float* partial) {
+    dot_partial_k<<<kSumBlocks, kBlock, 0, st>>>(partial, a, b, n, mode_in);
+    finish_sum_k<<<1, 1024, 0, st>>>(out, partial, kSumBlocks, idx, n, mode_out);
+    return check_launch("fixed_sum");
+}
+
+int32_t frob_normalize(hipStream_t st, float* data, int64_t n, float* scratch) {
+    if (n == 0) return AR_OK;
+    float* scale = scratch + kSumBlocks;
+    dot_partial_k<<<kSumBlocks, kBlock, 0, st>>>(scratch, data, nullptr, n, 1);
+    finish_sum_k<<<1, 1024, 0, st>>>(scale, scratch, kSumBlocks, 0, n, 2);
+    scale_by_device_scalar_k<<<flat_grid(n, kBlock * 4), kBlock, 0, st>>>(data, scale, n);
+    return check_launch("normalize_frobenius");
+}
+
+int32_t ve_gate_bwd(hipStream_t st, float* gx, float* gw, const float* ggate, const float* gate, const float* xn,
+                    const float* w, int64_t nt, int64_t nkv, int64_t gc, int64_t C, float* partial) {
+    if (nt == 0) return AR_OK;
+    ve_gate_bwd_partial_k<<<kGateBlocks, 256, 0, st>>>(gx, partial, ggate, gate, xn, w, nt, nkv, gc, C);
+    ve_gate_bwd_finish_k<<<1, 256, 0, st>>>(gw, partial, kGateBlocks, nkv * gc);
+    return check_launch("ve_gate_bwd");
+}
+}  // namespace ar
+
+static int32_t ws_sum(ar_stream_t stream, float* out, const float* a, const float* b, int64_t n, int mi, int mo,
+                      int64_t idx) {
+    int32_t st;
+    float* partial = (float*)workspace(kSumBlocks * sizeof(float), &st);
+    if (!partial) return st;
+    return ar::fixed_sum(S(stream), out, a, b, n, mi, mo, idx, partial);
+}
+
+extern "C" int32_t ar_mean_reduce(ar_stream_t stream, float* output, const float* input, int64_t size) {
+    AR_CHECK_ARG(output && input && size > 0, "mean_reduce: bad argument");
+    return ws_sum(stream, output, input, nullptr, size, 0, 0, 0);
+}
+
+extern "C" int32_t ar_scalar_grad_reduce(ar_stream_t stream, float* grad_scalar, const float* grad_output,
+                                         const float* input, int64_t idx, int64_t size) {
+    AR_CHECK_ARG(grad_scalar && grad_output && input && size >= 0 && idx >= 0, "scalar_grad_reduce: bad argument");
+    return ws_sum(stream, grad_scalar, grad_output, input, size, 2, 1, idx);
+}
+
+extern "C" int32_t ar_normalize_frobenius(ar_stream_t stream, float* data, int64_t size) {
+    AR_CHECK_ARG(data && size >= 0, "normalize_frobenius: bad argument");
+    if (size == 0) return AR_OK;
+    int32_t st;
+    float* ws = (float*)workspace((kSumBlocks + 64) * sizeof(float), &st);
+    if (!ws) return st;
+    return ar::frob_normalize(S(stream), data, size, ws);
+}
+
+extern "C" int32_t ar_flash_attn_bwd_precompute_d(ar_stream_t stream, float* d_out, const float* output,
+                                                  const float* grad_output, int64_t B, int64_t T,
+                                                  int64_t num_heads, int64_t head_dim) {
+    AR_CHECK_ARG(d_out && output && grad_output, "flash_attn_bwd_precompute_d: null pointer");
+    AR_CHECK_ARG(B >= 0 && T >= 0 && num_heads > 0 && head_dim > 0, "flash_attn_bwd_precompute_d: bad shape");
+    const int64_t rows = B * T * num_heads;
+    if (rows == 0) return AR_OK;
+    precompute_d_k<<<wave_grid(rows), kBlock, 0, S(stream)>>>(d_out, output, grad_output, rows, head_dim);
+    return AR_LAUNCH_CHECK("flash_attn_bwd_precompute_d");
+}
+
+extern "C" int32_t ar_ve_gate_fwd(ar_stream_t stream, float* gate_out, const float* x_norm, const float* gate_weight,
+                                  int64_t num_tokens, int64_t n_kv_head, int64_t gate_channels, int64_t embd_dim) {
+    AR_CHECK_ARG(gate_out && x_norm && gate_weight, "ve_gate_fwd: null pointer");
+    AR_CHECK_ARG(num_tokens >= 0 && n_kv_head > 0 && gate_channels > 0 && gate_channels <= embd_dim,
+                 "ve_gate_fwd: bad shape");
+    if (num_tokens == 0) return AR_OK;
+    ve_gate_fwd_k<<<flat_grid(num_tokens * n_kv_head, kBlock), kBlock, 0, S(stream)>>>(
+        gate_out, x_norm, gate_weight, num_tokens, n_kv_head, gate_channels, embd_dim);
+    return AR_LAUNCH_CHECK("ve_gate_fwd");
+}
+
+extern "C" int32_t ar_ve_apply_bwd(ar_stream_t stream, float* grad_ve, float* grad_gate, const float* grad_v,
+                                   const float* gate, const float* ve, int64_t num_tokens, int64_t n_kv_head,
+                                   int64_t head_dim) {
+    AR_CHECK_ARG(grad_ve && grad_gate && grad_v && gate && ve, "ve_apply_bwd: null pointer");
+    AR_CHECK_ARG(num_tokens >= 0 && n_kv_head > 0 && head_dim > 0, "ve_apply_bwd: bad shape");
+    const int64_t rows = num_tokens * n_kv_head;
+    if (rows == 0) return AR_OK;
+    ve_apply_bwd_k<<<wave_grid(rows), kBlock, 0, S(stream)>>>(grad_ve, grad_gate, grad_v, gate, ve, rows, head_dim);
+    return AR_LAUNCH_CHECK("ve_apply_bwd");
+}
+
+extern "C" int32_t ar_ve_gate_bwd(ar_stream_t stream, float* grad_x_norm_out, float* grad_gate_weight,
+                                  const float* grad_gate, const float* gate, const float* x_norm,
+                                  const float* gate_weight, int64_t num_tokens, int64_t n_kv_head,
+                                  int64_t gate_channels, int64_t embd_dim) {
+    AR_CHECK_ARG(grad_x_norm_out && grad_gate_weight && grad_gate && gate && x_norm && gate_weight,
+                 "ve_gate_bwd: null pointer");
+    AR_CHECK_ARG(num_tokens >= 0 && n_kv_head > 0 && n_kv_head <= kGateMaxH && gate_channels > 0 &&
+                     gate_channels <= 64 && gate_channels <= embd_dim,
+                 "ve_gate_bwd: unsupported shape (n_kv_head <= 16, gate_channels <= 64)");
+    if (num_tokens == 0) return AR_OK;
+    int32_t st;
+    const int64_t n = n_kv_head * gate_channels;
+    float* partial = (float*)workspace((size_t)kGateBlocks * n * sizeof(float), &st);
+    if (!partial) return st;
+    return ar::ve_gate_bwd(S(stream), grad_x_norm_out, grad_gate_weight, grad_gate, gate, x_norm, gate_weight,
+                           num_tokens, n_kv_head, gate_channels, embd_dim, partial);
+}
+
+// Sort workspace layout: keys, keys_sorted, vals, vals_sorted (n each), flag,
+// cub temp, then partial sums [n, dim].
+extern "C" int32_t ar_embedding_bwd_sorted(ar_stream_t stream, float* grad_weight, const float* grad_output,
+                                           const uint32_t* sorted_ids, const int32_t* sorted_tokens,
+                                           int64_t num_tokens, int64_t embd_dim, float* partial) {
+    const int64_t n = num_tokens;
+    const unsigned grid = (unsigned)cdiv(n, kBlock / kWave);
+    emb_chunk_sum_k<<<grid, kBlock, 0, S(stream)>>>(partial, sorted_ids, sorted_tokens, grad_output, n, embd_dim);
+    emb_segment_apply_k<<<grid, kBlock, 0, S(stream)>>>(grad_weight, partial, sorted_ids, n, embd_dim);
+    return AR_LAUNCH_CHECK("embedding_bwd");
+}
+
+// Stable sort of token ids: sorted_ids/sorted_tokens (n each).  end_bit bounds
+// the radix passes (32 when the vocabulary size is unknown).
+extern "C" int32_t ar_embedding_sort(ar_stream_t stream, uint32_t* sorted_ids, int32_t* sorted_tokens,
+                                     const int64_t* indices, int64_t num_tokens, int32_t end_bit, void* scratch,
+                                     size_t scratch_bytes, size_t* scratch_needed) {
+    const int64_t n = num_tokens;
+    size_t cub_bytes = 0;
+    hipcub::DeviceRadixSort::SortPairs(nullptr, cub_bytes, (const uint32_t*)nullptr, (uint32_t*)nullptr,
+                                       (const int32_t*)nullptr, (int32_t*)nullptr, (int)n, 0, end_bit, S(stream));
+    const size_t keys_bytes = ((size_t)n * 4 + 255) & ~size_t(255);
+    const size_t need = 2 * keys_bytes + cub_bytes;
+    if (scratch_needed) *scratch_needed = need;
+    if (!scratch) return AR_OK;
+    if (scratch_bytes < need) return set_error(AR_EINVAL, "embedding_sort: scratch too small");
+    char* base = (char*)scratch;
+    uint32_t* keys = (uint32_t*)base;
+    int32_t* vals = (int32_t*)(base + keys_bytes);
+    void* cub_tmp = base + 2 * keys_bytes;
+    emb_keys_k<<<flat_grid(n, kBlock), kBlock, 0, S(stream)>>>(keys, vals, indices, n);
+    if (hipcub::DeviceRadixSort::SortPairs(cub_tmp, cub_bytes, keys, sorted_ids, vals, sorted_tokens, (int)n, 0,
+                                           end_bit, S(stream)) != hipSuccess)
+        return set_error(AR_EHIP, "embedding_sort: radix sort failed");
+    return AR_LAUNCH_CHECK("embedding_sort");
+}
+
+extern "C" int32_t ar_embedding_bwd(ar_stream_t stream, float* grad_weight, const float* grad_output,
+                                    const int64_t* indices, int64_t num_tokens, int64_t embd_dim) {
+    AR_CHECK_ARG(grad_weight && grad_output && indices, "embedding_bwd: null pointer");
+    AR_CHECK_ARG(num_tokens >= 0 && num_tokens < (int64_t)1 << 31 && embd_dim > 0, "embedding_bwd: bad shape");
+    if (num_tokens == 0) return AR_OK;
+    size_t sort_bytes = 0;
+    int32_t st = ar_embedding_sort(stream, nullptr, nullptr, indices, num_tokens, 32, nullptr, 0, &sort_bytes);
+    if (st) return st;
+    const size_t ids_bytes = ((size_t)num_tokens * 4 + 255) & ~size_t(255);
+    const size_t part_bytes = (size_t)num_tokens * embd_dim * sizeof(float);
+    char* ws = (char*)workspace(2 * ids_bytes + sort_bytes + part_bytes, &st);
+    if (!ws) return st;
+    uint32_t* sids = (uint32_t*)ws;
+    int32_t* stok = (int32_t*)(ws + ids_bytes);
+    char* sort_scratch = ws + 2 * ids_bytes;
+    float* partial = (float*)(sort_scratch + sort_bytes);
+    st = ar_embedding_sort(stream, sids, stok, indices, num_tokens, 32, sort_scratch, sort_bytes, nullptr);
+    if (st) return st;
+    return ar_embedding_bwd_sorted(stream, grad_weight, grad_output, sids, stok, num_tokens, embd_dim, partial);
+}

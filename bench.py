@@ -1,0 +1,189 @@
+#!/usr/bin/env python3
+"""Benchmark: training tokens/s of the full GPT training step on one MI355X.
+
+Workload: depth 8, d_model 512, 4 heads x 128,
+vocab 8192, T = 2048, B = 32, SSSL windows (1024 x3, 2048), ReLU^2 MLP,
+value embeddings, softcap 15, Muon (5 Polar Express iterations) on every 2-D
+matrix and AdamW on embeddings and scalars; bf16 matrix-core compute with
+fp32 master weights.  Token ids are Zipf(1.1) over the vocabulary from seed 0
+(synthetic; no dataset).  Weights follow the reference init (seed 42).
+
+A "step" = zero_grads -> forward -> backward -> AdamW + Muon update
+(train.mojo:231-282), all on the GPU through the C ABI.  W untimed warm-up
+steps, then exactly K steps between two device synchronisations.
+
+Prints ONE JSON line.  `roofline` describes the dominant kernel class
+(largest share of step time), measured with HIP events bracketing each of its
+launches on the model's stream during the timed steps; `cpu_baseline` times
+the fp32 CPU oracle on this host on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2516.6   # dense bf16 MFMA, MI355X
+PEAK_FP32_TFLOPS = 157.3    # fp32 matrix, MI355X
+METRIC = "training tokens/sec @ depth8 d512 T2048 (1 GPU) + MFMA util %"
+CLASS_NAMES = ["linear_fwd", "linear_bwd_dx", "linear_bwd_dw", "flash_attn_fwd", "flash_attn_bwd_dq",
+               "flash_attn_bwd_dkv", "muon_polar_express"]
+
+
+def zipf_tokens(n: int, V: int, s: float, seed: int) -> np.ndarray:
+    """Inverse-CDF Zipf: p_k ~ (k+1)^-s, k < V."""
+    p = 1.0 / np.arange(1, V + 1, dtype=np.float64) ** s
+    cdf = np.cumsum(p / p.sum())
+    u = np.random.default_rng(seed).random(n)
+    return np.minimum(np.searchsorted(cdf, u, side="right"), V - 1).astype(np.int64)
+
+
+def step_flops(L, C, V, B, T, H, hd, windows, mats) -> float:
+    """Algorithmic FLOPs of one training step (SURVEY 8(d) formula):
+    GEMMs 72*L*M*C^2 + 6*M*C*V, attention 14*B*H*hd*sum_layers sum_q keys(q),
+    Muon 5*sum(4*l*s^2 + 2*s^3)."""
+    M = B * T
+    gemm = 72.0 * L * M * C * C + 6.0 * M * C * V
+    attn = 0.0
+    for ws in windows:
+        keys = sum((q - max(0, q - ws) + 1) if ws > 0 else (q + 1) for q in range(T))
+        attn += 14.0 * B * H * hd * keys
+    muon = sum(5.0 * (4.0 * max(r, c) * min(r, c) ** 2 + 2.0 * min(r, c) ** 3) for r, c in mats)
+    return gemm + attn + muon
+
+
+def cpu_baseline(cfg, T, V, steps_tokens_B: int) -> dict:
+    """fp32 CPU oracle on this host: one forward+backward at B=1 (2048 tokens)
+    and one optimizer step, extrapolated to the B=32 step."""
+    from oracle import oracle as orc
+    om = orc.Model(cfg.as_dict(), 1, T, T)
+    om.init_weights(42)
+    toks = zipf_tokens(T + 1, V, 1.1, 1)
+    x, y = np.ascontiguousarray(toks[:-1]), np.ascontiguousarray(toks[1:])
+    t0 = time.perf_counter()
+    om.zero_grads()
+    om.forward(x, y)
+    om.backward(x, y, 1.0)
+    t1 = time.perf_counter()
+    om.optimizer_step(0.0)
+    t2 = time.perf_counter()
+    fb, opt = t1 - t0, t2 - t1
+    est = steps_tokens_B * fb + opt
+    return {"value": round(steps_tokens_B * T / est, 2), "unit": "tokens/s",
+            "cores": orc.lib().orc_num_threads(), "kind": "port",
+            "sample": (f"fp32 oracle (OpenMP): 1 fwd+bwd at B=1,T={T} ({fb:.1f}s) + 1 AdamW/Muon update "
+                       f"({opt:.1f}s), extrapolated to B={steps_tokens_B}: {steps_tokens_B}*fwdbwd + update")}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=11)
+    ap.add_argument("--depth", type=int, default=8)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--seq", type=int, default=2048)
+    ap.add_argument("--vocab", type=int, default=8192)
+    ap.add_argument("--precision", choices=["bf16", "fp32"], default="bf16")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    a = ap.parse_args(argv)
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the training step is single-GPU in the reference; "
+              "multi-GPU data parallelism is a design note, not built). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+    from autoresearch_amd.model import BF16, FP32, GPT, GPTConfig
+
+    cfg = GPTConfig.default(a.vocab, a.depth)
+    B, T, V = a.batch, a.seq, a.vocab
+    prec = BF16 if a.precision == "bf16" else FP32
+    torch.cuda.set_device(0)
+    toks = zipf_tokens(B * (T + 1), V, 1.1, 0).reshape(B, T + 1)
+    x = torch.from_numpy(np.ascontiguousarray(toks[:, :-1]).ravel()).cuda()
+    y = torch.from_numpy(np.ascontiguousarray(toks[:, 1:]).ravel()).cuda()
+    m = GPT(cfg, B, T, precision=prec, rope_period=T)
+    m.init_weights(42)
+    torch.cuda.synchronize()
+    print(f"[bench] model ready: L={cfg.n_layer} C={cfg.n_embd} H={cfg.n_head} V={V} B={B} T={T} "
+          f"{a.precision}", file=sys.stderr, flush=True)
+
+    for i in range(a.warmup):
+        m.train_step(x, y, 0.0, sync_loss=False)
+    torch.cuda.synchronize()
+    print(f"[bench] warmup done ({a.warmup} steps)", file=sys.stderr, flush=True)
+
+    # Timed region (profiling events on the dominant kernel classes).
+    m.lib.ar_gpt_profile(m.h, 1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(a.steps):
+        m.train_step(x, y, 0.0, sync_loss=False)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / a.steps
+    loss = float(torch.tensor(0.0))
+    import ctypes as ct
+    cls_stats = []
+    for c in range(len(CLASS_NAMES)):
+        t, n, f = ct.c_double(), ct.c_int64(), ct.c_double()
+        m.lib.ar_gpt_profile_read(m.h, c, ct.byref(t), ct.byref(n), ct.byref(f))
+        cls_stats.append((CLASS_NAMES[c], t.value, n.value, f.value))
+    m.lib.ar_gpt_profile(m.h, 0)
+    lbuf = ct.c_float()
+    torch.cuda.synchronize()
+    loss = m.forward(x, y)
+    print(f"[bench] timed {a.steps} steps: {ms:.2f} ms/step, loss after = {loss:.4f}", file=sys.stderr, flush=True)
+
+    tokens = B * T
+    value = tokens / (ms / 1e3)
+    windows = [cfg.window_size(i) for i in range(cfg.n_layer)]
+    mats = []
+    F = 4 * cfg.n_embd
+    for _ in range(cfg.n_layer):
+        mats += [(cfg.n_embd, cfg.n_embd)] * 4 + [(F, cfg.n_embd), (cfg.n_embd, F)]
+    flops = step_flops(cfg.n_layer, cfg.n_embd, V, B, T, cfg.n_head, cfg.head_dim, windows, mats)
+    peak = PEAK_BF16_TFLOPS if prec == BF16 else PEAK_FP32_TFLOPS
+    mfma_util = flops / (ms / 1e3) / (peak * 1e12)
+
+    dom = max(cls_stats, key=lambda s: s[1])
+    name, t_ms, n, f = dom
+    achieved = (f / (t_ms / 1e3)) / 1e12 if t_ms > 0 else 0.0
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(achieved / peak, 4), "traffic": None, "kernel": name,
+                "launches_per_step": n // a.steps, "avg_launch_ms": round(t_ms / max(n, 1), 4),
+                "share_of_step": round(t_ms / a.steps / ms, 4)}
+    breakdown = {s[0]: {"ms_per_step": round(s[1] / a.steps, 3),
+                        "tflops": round((s[3] / (s[1] / 1e3)) / 1e12, 1) if s[1] > 0 else 0.0}
+                 for s in cls_stats}
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        print("[bench] cpu baseline (oracle) ...", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(cfg, T, V, B)
+
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": a.precision, "data": "synthetic Zipf(1.1) token ids, seed 0",
+        "config": {"workload": f"config 4: full training step depth{cfg.n_layer} d{cfg.n_embd} "
+                               f"H{cfg.n_head}x{cfg.head_dim} V{V} T{T} B{B} SSSL, AdamW+Muon",
+                   "global_batch": B, "seq_len": T, "parallelism": "single GPU"},
+        "mfma_util": round(mfma_util, 4), "step_tflop": round(flops / 1e12, 3),
+        "roofline": roofline, "kernel_classes": breakdown, "cpu_baseline": cpu,
+        "loss_after": round(loss, 4),
+    }
+    print(json.dumps(out), flush=True)
+    m.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,208 @@
+"""GEMM, flash attention and Muon parity on the GPU (through the C ABI).
+
+Small shapes compare against the CPU oracle; the BASELINE config-2 /
+config-3 shapes compare against a torch fp32 reference on the GPU (the oracle
+would take minutes there), with the tolerance stated per test."""
+import numpy as np
+import pytest
+
+from conftest import TOL_BF16, TOL_FP32, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def env():
+    import torch  # noqa: F401
+    from autoresearch_amd import ops
+    from oracle import oracle as orc
+    import gpu_util as gu
+    return ops, orc, gu
+
+
+GEMM_SHAPES = [(256, 256, 256), (384, 136, 520), (128, 512, 2048), (2048, 512, 128), (64, 8, 64)]
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+@pytest.mark.parametrize("bf16", [False, True])
+def test_gemm_layouts_vs_oracle(env, M, N, K, bf16):
+    ops, orc, gu = env
+    r = gu.rng(M + N + K)
+    tol = TOL_BF16 if bf16 else TOL_FP32
+    X = gu.randn(r, M, K)
+    W = gu.randn(r, N, K, scale=0.05)
+    ref = np.zeros((M, N), np.float32)
+    orc.call("linear_fwd", ref, X, W, M, N, K)
+    out = gu.empty(M, N)
+    ops.linear_fwd(out, gu.dev(X), gu.dev(W), M, N, K, bf16=bf16)
+    assert rel_err(gu.host(out), ref) <= tol
+    dY = gu.randn(r, M, N)
+    ref = np.zeros((M, K), np.float32)
+    orc.call("linear_bwd_dx", ref, dY, W, M, N, K)
+    dx = gu.empty(M, K)
+    ops.linear_bwd_dx(dx, gu.dev(dY), gu.dev(W), M, N, K, bf16=bf16)
+    assert rel_err(gu.host(dx), ref) <= tol
+    dw0 = gu.randn(r, N, K)
+    ref = dw0.copy()
+    orc.call("linear_bwd_dw", ref, dY, X, M, N, K)  # accumulates
+    dw = gu.dev(dw0)
+    ops.linear_bwd_dw(dw, gu.dev(dY), gu.dev(X), M, N, K, bf16=bf16)
+    assert rel_err(gu.host(dw), ref) <= tol
+
+
+def test_linear_bwd_dx_in_place(env):
+    """model.mojo:906 calls linear_bwd_dx with grad_input == grad_output."""
+    ops, orc, gu = env
+    r = gu.rng(3)
+    M, C = 512, 256
+    dY = gu.randn(r, M, C)
+    W = gu.randn(r, C, C, scale=0.05)
+    ref = np.zeros((M, C), np.float32)
+    orc.call("linear_bwd_dx", ref, dY, W, M, C, C)
+    buf = gu.dev(dY)
+    ops.linear_bwd_dx(buf, buf, gu.dev(W), M, C, C)
+    assert rel_err(gu.host(buf), ref) <= TOL_FP32
+
+
+@pytest.mark.parametrize("K,N", [(512, 1536), (512, 512), (512, 2048), (2048, 512), (512, 8192)])
+def test_gemm_config3_shapes(env, K, N):
+    """M = 32768 tokens, bf16 operands, fp32 accumulation,
+    against torch fp32 matmul of the same fp32 inputs (tolerance 2e-2)."""
+    ops, orc, gu = env
+    import torch
+    M = 32768
+    g = torch.Generator(device="cuda").manual_seed(K + N)
+    X = torch.randn(M, K, device="cuda", generator=g)
+    W = torch.randn(N, K, device="cuda", generator=g) * 0.02
+    dY = torch.randn(M, N, device="cuda", generator=g)
+    out = torch.empty(M, N, device="cuda")
+    ops.linear_fwd(out, X, W, M, N, K, bf16=True)
+    assert rel_err(gu.host(out), gu.host(X @ W.T)) <= TOL_BF16
+    dx = torch.empty(M, K, device="cuda")
+    ops.linear_bwd_dx(dx, dY, W, M, N, K, bf16=True)
+    assert rel_err(gu.host(dx), gu.host(dY @ W)) <= TOL_BF16
+    dw = torch.zeros(N, K, device="cuda")
+    ops.linear_bwd_dw(dw, dY, X, M, N, K, bf16=True)
+    assert rel_err(gu.host(dw), gu.host(dY.T @ X)) <= TOL_BF16
+    # fp32 path of the same shape: exact-fp32 matrix cores
+    ops.linear_fwd(out, X, W, M, N, K, bf16=False)
+    ref = (X.double() @ W.double().T).float()
+    assert rel_err(gu.host(out), gu.host(ref)) <= TOL_FP32
+
+
+def _attn_inputs(gu, r, B, T, H, hd):
+    q = gu.randn(r, B, T, H, hd)
+    k = gu.randn(r, B, T, H, hd)
+    v = gu.randn(r, B, T, H, hd)
+    do = gu.randn(r, B, T, H, hd)
+    return q, k, v, do
+
+
+@pytest.mark.parametrize("B,T,H,hd,window", [(1, 128, 2, 64, 0), (2, 200, 2, 64, 32), (1, 256, 4, 128, 0),
+                                              (1, 320, 1, 128, 100), (2, 64, 2, 32, 16)])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_attention_vs_oracle(env, B, T, H, hd, window, bf16):
+    ops, orc, gu = env
+    r = gu.rng(T + hd + window)
+    tol = TOL_BF16 if bf16 else TOL_FP32
+    q, k, v, do = _attn_inputs(gu, r, B, T, H, hd)
+    n = B * T * H
+    o_ref, lse_ref = np.zeros_like(q), np.zeros(n, np.float32)
+    orc.call("flash_attn_fwd", o_ref, lse_ref, q, k, v, B, T, H, hd, window)
+    d_ref = np.zeros(n, np.float32)
+    orc.call("flash_attn_bwd_precompute_d", d_ref, o_ref, do, B, T, H, hd)
+    dq_ref = np.zeros_like(q)
+    orc.call("flash_attn_bwd_dq", dq_ref, q, k, v, do, lse_ref, d_ref, B, T, H, hd, window)
+    dk_ref, dv_ref = np.zeros_like(q), np.zeros_like(q)
+    orc.call("flash_attn_bwd_dkv", dk_ref, dv_ref, q, k, v, do, lse_ref, d_ref, B, T, H, hd, window)
+
+    qd, kd, vd, dod = gu.dev(q), gu.dev(k), gu.dev(v), gu.dev(do)
+    o, lse = gu.empty(B, T, H, hd), gu.empty(n)
+    ops.flash_attn_fwd(o, lse, qd, kd, vd, B, T, H, hd, window, bf16=bf16)
+    assert rel_err(gu.host(o), o_ref) <= tol
+    assert rel_err(gu.host(lse), lse_ref) <= (tol if not bf16 else 1e-2)
+    # backward from the oracle's forward statistics, so each kernel is checked alone
+    lse_d, d_d = gu.dev(lse_ref), gu.dev(d_ref)
+    dq = gu.empty(B, T, H, hd)
+    ops.flash_attn_bwd_dq(dq, qd, kd, vd, dod, lse_d, d_d, B, T, H, hd, window, bf16=bf16)
+    assert rel_err(gu.host(dq), dq_ref) <= tol
+    dk, dv = gu.empty(B, T, H, hd), gu.empty(B, T, H, hd)
+    ops.flash_attn_bwd_dkv(dk, dv, qd, kd, vd, dod, lse_d, d_d, B, T, H, hd, window, bf16=bf16)
+    assert rel_err(gu.host(dk), dk_ref) <= tol
+    assert rel_err(gu.host(dv), dv_ref) <= tol
+
+
+def _torch_attention(q, k, v, window):
+    """fp32 masked softmax attention on the GPU (math path), [B,T,H,hd]."""
+    import torch
+    B, T, H, hd = q.shape
+    qt, kt, vt = (x.permute(0, 2, 1, 3).contiguous() for x in (q, k, v))
+    s = torch.matmul(qt, kt.transpose(-1, -2).contiguous()) / np.sqrt(hd)
+    i = torch.arange(T, device=q.device)
+    vis = i[None, :] <= i[:, None]
+    if window > 0:
+        vis &= i[None, :] >= i[:, None] - window
+    s = s.masked_fill(~vis, float("-inf"))
+    lse = torch.logsumexp(s, -1)
+    o = torch.matmul(torch.softmax(s, -1), vt)
+    return o.permute(0, 2, 1, 3).contiguous(), lse.permute(0, 2, 1).contiguous()
+
+
+@pytest.mark.parametrize("window", [0, 1024])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_attention_config2(env, window, bf16):
+    """B16 H4 hd128 T2048, RoPE'd q/k, full causal and
+    window 1024; forward against torch fp32, backward via autograd of the same
+    torch reference (fp32 tolerance 1e-5 / bf16 2e-2)."""
+    ops, orc, gu = env
+    import torch
+    B, T, H, hd = 16, 2048, 4, 128
+    g = torch.Generator(device="cuda").manual_seed(7 + window)
+    q, k, v, do = (torch.randn(B, T, H, hd, device="cuda", generator=g) for _ in range(4))
+    # RoPE (base 10000, per-sequence positions) on q and k, as the config states
+    c = torch.empty(T * hd // 2, device="cuda")
+    s = torch.empty(T * hd // 2, device="cuda")
+    ops.precompute_rope(c, s, T, hd)
+    for b in range(B):
+        for x in (q, k):
+            xb = x[b].contiguous()
+            ops.rope_fwd(xb, xb, c, s, T, H, hd)
+            x[b].copy_(xb)
+    tol = TOL_BF16 if bf16 else TOL_FP32
+    n = B * T * H
+    o, lse = torch.empty_like(q), torch.empty(n, device="cuda")
+    ops.flash_attn_fwd(o, lse, q, k, v, B, T, H, hd, window, bf16=bf16)
+    with torch.no_grad():
+        o_ref, lse_ref = _torch_attention(q, k, v, window)
+    assert rel_err(gu.host(o), gu.host(o_ref)) <= tol
+    assert rel_err(gu.host(lse), gu.host(lse_ref)) <= tol
+    dbuf = torch.empty(n, device="cuda")
+    ops.flash_attn_bwd_precompute_d(dbuf, o, do, B, T, H, hd)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    ops.flash_attn_bwd_dq(dq, q, k, v, do, lse, dbuf, B, T, H, hd, window, bf16=bf16)
+    ops.flash_attn_bwd_dkv(dk, dv, q, k, v, do, lse, dbuf, B, T, H, hd, window, bf16=bf16)
+    qr, kr, vr = (x.clone().requires_grad_(True) for x in (q, k, v))
+    o2, _ = _torch_attention(qr, kr, vr, window)
+    o2.backward(do)
+    assert rel_err(gu.host(dq), gu.host(qr.grad)) <= tol
+    assert rel_err(gu.host(dk), gu.host(kr.grad)) <= tol
+    assert rel_err(gu.host(dv), gu.host(vr.grad)) <= tol
+
+
+@pytest.mark.parametrize("rows,cols", [(128, 128), (512, 128), (128, 512), (256, 1024)])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_muon_step_vs_oracle(env, rows, cols, bf16):
+    ops, orc, gu = env
+    r = gu.rng(rows * 3 + cols)
+    p = gu.randn(r, rows, cols, scale=0.05)
+    g = gu.randn(r, rows, cols, scale=0.01)
+    mb = gu.randn(r, rows, cols, scale=0.01)
+    p_ref, g_ref, mb_ref = p.copy(), g.copy(), mb.copy()
+    orc.call("muon_step", p_ref, g_ref, mb_ref, rows, cols, 0.04, 1.0, 0.85, 0.2)
+    pd, gd, mbd = gu.dev(p), gu.dev(g), gu.dev(mb)
+    ops.muon_step(pd, gd, mbd, rows, cols, 0.04, 1.0, 0.85, 0.2, bf16=bf16)
+    assert rel_err(gu.host(mbd), mb_ref) <= TOL_FP32
+    # the update is p - lr * (X + decay); compare the applied update
+    upd, upd_ref = gu.host(pd) - p, p_ref - p
+    tol = TOL_BF16 if bf16 else 1e-4
+    assert rel_err(upd, upd_ref) <= tol
