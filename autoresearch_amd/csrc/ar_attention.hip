@@ -76,6 +76,17 @@ template <> struct AT<true> {
         for (int e = 0; e < 8; ++e) f[e] = (bf16)a[8 * s + e];
         return f;
     }
+    // The bf16 rounding residual of accfrag: accfrag + accfrag_lo carries
+    // ~16 significant bits of the fp32 value.
+    __device__ static Frag accfrag_lo(const f32x16& a, int s) {
+        Frag f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float x = a[8 * s + e];
+            f[e] = (bf16)(x - (float)(bf16)x);
+        }
+        return f;
+    }
 };
 
 template <> struct AT<false> {
@@ -94,6 +105,7 @@ template <> struct AT<false> {
         return natural[r * ldn + d];
     }
     __device__ static Frag accfrag(const f32x16& a, int s) { return a[s]; }
+    __device__ static Frag accfrag_lo(const f32x16& a, int s) { (void)a; (void)s; return 0.0f; }
 };
 
 // Load rows [row0, row0 + 64) of a [T, rs]-strided operand (columns [0, HD))
@@ -287,15 +299,24 @@ __global__ __launch_bounds__(kThreads) void fa_fwd_k(float* out, float* lse, con
             for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+            // O^T += V^T P^T.  With bf16 operands P goes in as a two-term bf16
+            // split (hi + lo), so O keeps fp32-level accuracy in P: the
+            // backward's D = rowsum(dO * O) must equal sum_j P_j dP_j, and a
+            // bf16-rounded P would bias every dS_j = P_j (dP_j - D) by the same
+            // amount, which the attention-weighted mean key then multiplies.
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int st = 0; st < A::STEPS32; ++st) {
                     const typename A::Frag pb = A::accfrag(s[kb], st);
+                    typename A::Frag pl{};
+                    if constexpr (BF16) pl = A::accfrag_lo(s[kb], st);
 #pragma unroll
                     for (int dt = 0; dt < HD / 32; ++dt) {
                         const int d = dt * 32 + (lane & 31);
-                        o[dt] = A::mma(A::permfrag(sV, LDN, sVT, d, kb, st, lane), pb, o[dt]);
+                        const typename A::Frag va = A::permfrag(sV, LDN, sVT, d, kb, st, lane);
+                        o[dt] = A::mma(va, pb, o[dt]);
+                        if constexpr (BF16) o[dt] = A::mma(va, pl, o[dt]);
                     }
                 }
         }

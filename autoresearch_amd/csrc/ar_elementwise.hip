@@ -217,28 +217,30 @@ __device__ __forceinline__ uint64_t xs_mix(uint64_t s) {
     return s;
 }
 
+// Contraction is off for the init kernels so every product and sum rounds
+// where the reference expression does (hipcc otherwise fuses lo + u*span).
 __global__ void fill_normal_k(float* out, uint64_t seed, float std_, int64_t n) {
+#pragma clang fp contract(off)
     const float PI = 3.14159265358979323846f;
     AR_GRID_LOOP(i, n) {
         uint64_t st = seed + (uint64_t)i * 6364136223846793005ULL + 1442695040888963407ULL;
         st = xs_mix(st);
-        float u1 = __fadd_rn((float)(st & 0xFFFFFFULL) / 16777216.0f, 1e-10f);
+        float u1 = (float)(st & 0xFFFFFFULL) / 16777216.0f + 1e-10f;
         st = st * 6364136223846793005ULL + 1442695040888963407ULL;
         st = xs_mix(st);
         float u2 = (float)(st & 0xFFFFFFULL) / 16777216.0f;
-        float z = sqrtf(-2.0f * logf(u1)) * cosf(__fmul_rn(2.0f * PI, u2));
+        float z = sqrtf(-2.0f * logf(u1)) * cosf(2.0f * PI * u2);
         out[i] = z * std_;
     }
 }
 
 __global__ void fill_uniform_k(float* out, uint64_t seed, float lo, float hi, int64_t n) {
+#pragma clang fp contract(off)
     AR_GRID_LOOP(i, n) {
         uint64_t st = seed + (uint64_t)i * 6364136223846793005ULL + 1442695040888963407ULL;
         st = xs_mix(st);
         float u = (float)(st & 0xFFFFFFULL) / 16777216.0f;
-        // __fmul_rn/__fadd_rn: no contraction into an FMA, so the result is
-        // bit-identical to the uncontracted reference expression.
-        out[i] = __fadd_rn(lo, __fmul_rn(u, hi - lo));
+        out[i] = lo + u * (hi - lo);
     }
 }
 

@@ -160,11 +160,14 @@ struct TileLoader {
     }
 };
 
-// Linear block id -> (tile_m, tile_n, split) with an XCD-contiguous order.
-__device__ __forceinline__ void tile_coords(int64_t tiles_n, int64_t tiles_mn, int64_t total, int64_t& tm,
-                                            int64_t& tn, int64_t& z) {
+// Linear block id -> (batch, split, tile_m, tile_n) with an XCD-contiguous
+// order: each of the 8 XCDs owns a contiguous run of (batch, split, m, n).
+__device__ __forceinline__ void tile_coords(int64_t tiles_n, int64_t tiles_mn, int64_t splits, int64_t total,
+                                            int64_t& bt, int64_t& tm, int64_t& tn, int64_t& z) {
     int64_t id = blockIdx.x;
     if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
+    bt = id / (tiles_mn * splits);
+    id %= tiles_mn * splits;
     z = id / tiles_mn;
     const int64_t r = id % tiles_mn;
     tm = r / tiles_n;
@@ -174,7 +177,8 @@ __device__ __forceinline__ void tile_coords(int64_t tiles_n, int64_t tiles_mn, i
 template <typename TA, typename TB, typename TC, bool AK, bool BKM, bool BF16, int EPI>
 __global__ __launch_bounds__(kThreads) void gemm_k(TC* C, const TA* A, const TB* B, int64_t M, int64_t N,
                                                       int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
-                                                      int64_t k_per_split, float* partial) {
+                                                      int64_t k_per_split, float* partial, int64_t batch,
+                                                      int64_t sA, int64_t sB, int64_t sC) {
     using MM = Mfma<BF16>;
     using LT = typename MM::LT;
     constexpr int BK = MM::BK, LDK = MM::LDK, CW = MM::CW;
@@ -186,8 +190,12 @@ __global__ __launch_bounds__(kThreads) void gemm_k(TC* C, const TA* A, const TB*
     const int64_t tiles_n = (N + BN - 1) / BN, tiles_m = (M + BM - 1) / BM;
     const int64_t tiles_mn = tiles_m * tiles_n;
     const int64_t splits = (K + k_per_split - 1) / k_per_split;
-    int64_t tm, tn, z;
-    tile_coords(tiles_n, tiles_mn, tiles_mn * splits, tm, tn, z);
+    int64_t bt, tm, tn, z;
+    tile_coords(tiles_n, tiles_mn, splits, tiles_mn * splits * batch, bt, tm, tn, z);
+    A += bt * sA;
+    B += bt * sB;
+    C += bt * sC;
+    if constexpr (EPI == EPI_PARTIAL) partial += bt * splits * M * N;
     const int64_t m0 = tm * BM, n0 = tn * BN;
     const int64_t kbeg = z * k_per_split;
     const int64_t kend = (kbeg + k_per_split < K) ? kbeg + k_per_split : K;
@@ -265,16 +273,20 @@ __global__ __launch_bounds__(kThreads) void gemm_k(TC* C, const TA* A, const TB*
         }
 }
 
-// C[i] (+)= sum_z partial[z][i], z in order (row stride ldc for C).
+// C[b][i] (+)= sum_z partial[b][z][i], z in order (row stride ldc for C).
 template <typename TC>
 __global__ void splitk_reduce_k(TC* C, const float* partial, int64_t M, int64_t N, int64_t ldc, int64_t splits,
-                                int accumulate) {
-    const int64_t total = M * N;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+                                int accumulate, int64_t batch, int64_t sC) {
+    const int64_t mn = M * N;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < mn * batch;
+         j += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t b = j / mn, i = j % mn;
         const int64_t r = i / N, c = i % N;
-        float s = accumulate ? to_f32(C[r * ldc + c]) : 0.f;
-        for (int64_t z = 0; z < splits; ++z) s += partial[z * total + i];
-        C[r * ldc + c] = from_f32<TC>(s);
+        TC* Cb = C + b * sC;
+        const float* pb = partial + b * splits * mn;
+        float s = accumulate ? to_f32(Cb[r * ldc + c]) : 0.f;
+        for (int64_t z = 0; z < splits; ++z) s += pb[z * mn + i];
+        Cb[r * ldc + c] = from_f32<TC>(s);
     }
 }
 
@@ -307,26 +319,27 @@ static int64_t choose_splits(int64_t tiles, int64_t K, int64_t splits_req, int64
 template <typename TA, typename TB, typename TC, bool AK, bool BKM, bool BF16>
 static int32_t gemm_launch(hipStream_t st, TC* C, const TA* A, const TB* B, int64_t M, int64_t N, int64_t K,
                            int64_t lda, int64_t ldb, int64_t ldc, bool accumulate, int64_t splits_req,
-                           float* partial, const char* nm) {
+                           float* partial, const char* nm, int64_t batch = 1, int64_t sA = 0, int64_t sB = 0,
+                           int64_t sC = 0) {
     const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     int64_t kps = 0;
-    const int64_t splits = choose_splits<BF16>(tiles, K, splits_req, kps);
+    const int64_t splits = choose_splits<BF16>(tiles * batch, K, splits_req, kps);
     const size_t lds = lds_bytes<BF16>();
+    const unsigned grid = (unsigned)(tiles * splits * batch);
     if (splits == 1) {
-        const unsigned grid = (unsigned)tiles;
         if (accumulate)
-            gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_ACCUM><<<grid, kThreads, lds, st>>>(C, A, B, M, N, K, lda, ldb, ldc,
-                                                                                    kps, nullptr);
+            gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_ACCUM><<<grid, kThreads, lds, st>>>(
+                C, A, B, M, N, K, lda, ldb, ldc, kps, nullptr, batch, sA, sB, sC);
         else
-            gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_STORE><<<grid, kThreads, lds, st>>>(C, A, B, M, N, K, lda, ldb, ldc,
-                                                                                    kps, nullptr);
+            gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_STORE><<<grid, kThreads, lds, st>>>(
+                C, A, B, M, N, K, lda, ldb, ldc, kps, nullptr, batch, sA, sB, sC);
         return check_launch(nm);
     }
     if (!partial) return set_error(AR_EINVAL, "%s: split-K scratch missing", nm);
-    const unsigned grid = (unsigned)(tiles * splits);
     gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_PARTIAL><<<grid, kThreads, lds, st>>>(C, A, B, M, N, K, lda, ldb, ldc, kps,
-                                                                              partial);
-    splitk_reduce_k<TC><<<flat_grid(M * N, 256 * 4), 256, 0, st>>>(C, partial, M, N, ldc, splits, accumulate ? 1 : 0);
+                                                                              partial, batch, sA, sB, sC);
+    splitk_reduce_k<TC><<<flat_grid(M * N * batch, 256 * 4), 256, 0, st>>>(C, partial, M, N, ldc, splits,
+                                                                           accumulate ? 1 : 0, batch, sC);
     return check_launch(nm);
 }
 
@@ -349,6 +362,24 @@ int64_t gemm_partial_elems(int layout, int64_t M, int64_t N, int64_t K, int64_t 
     int64_t gm, gn, gk;
     gemm_space(layout, M, N, K, gm, gn, gk);
     return splits > 1 ? splits * gm * gn : 0;
+}
+
+// Batched, GEMM-space form used by Muon: C_b[mo,no] = sum_r A_b(mo,r) B_b(no,r)
+// with A/B K-major (ak/bk) or MN-major, operand b at base + b * stride.  No
+// reduction split: the batch supplies the parallelism.
+int32_t gemm_batched_f32(hipStream_t st, bool bf, bool ak, bool bk, float* C, const float* A, const float* B,
+                         int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch,
+                         int64_t sA, int64_t sB, int64_t sC) {
+#define AR_GB(AKv, BKv)                                                                                        \
+    (bf ? gemm_launch<float, float, float, AKv, BKv, true>(st, C, A, B, M, N, K, lda, ldb, ldc, false, 1, nullptr, \
+                                                           "gemm_batched", batch, sA, sB, sC)                  \
+        : gemm_launch<float, float, float, AKv, BKv, false>(st, C, A, B, M, N, K, lda, ldb, ldc, false, 1, nullptr, \
+                                                            "gemm_batched", batch, sA, sB, sC))
+    if (ak && bk) return AR_GB(true, true);
+    if (ak && !bk) return AR_GB(true, false);
+    if (!ak && !bk) return AR_GB(false, false);
+    return AR_GB(false, true);
+#undef AR_GB
 }
 
 int32_t gemm_f32(hipStream_t st, int layout, bool bf, float* C, const float* X, const float* W, int64_t M, int64_t N,

@@ -20,6 +20,11 @@ int64_t gemm_auto_splits(int layout, bool bf16, int64_t M, int64_t N, int64_t K)
 int64_t gemm_partial_elems(int layout, int64_t M, int64_t N, int64_t K, int64_t splits);
 int32_t gemm_f32(hipStream_t st, int layout, bool bf16, float* C, const float* X, const float* W, int64_t M,
                  int64_t N, int64_t K, bool accumulate, int64_t splits, float* partial);
+// Batched GEMM-space form: C_b[mo,no] = sum_r A_b(mo,r) B_b(no,r); ak / bk
+// select K-major (r contiguous, row stride lda/ldb) vs MN-major storage.
+int32_t gemm_batched_f32(hipStream_t st, bool bf16, bool ak, bool bk, float* C, const float* A, const float* B,
+                         int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch,
+                         int64_t sA, int64_t sB, int64_t sC);
 
 // ---- reductions (ar_reduce.hip) ----
 constexpr int kSumBlocks = 512;
@@ -46,10 +51,13 @@ int32_t rope(hipStream_t st, float* out, const float* in, const float* cos_t, co
              int64_t nh, int64_t hd, int64_t period, bool inverse);
 
 // ---- Muon (ar_optim.hip) ----
-// Scratch (floats) needed by muon_step for a [rows, cols] matrix.
-int64_t muon_scratch_elems(int64_t rows, int64_t cols, bool bf16);
-int32_t muon_step(hipStream_t st, float* params, float* grads, float* momentum_buf, int64_t rows, int64_t cols,
-                  double initial_lr, double lrm, double momentum, double wd, bool bf16, float* scratch);
+constexpr int kMuonMaxGroup = 48;
+// Scratch (floats) for a group of n same-shape [rows, cols] matrices.
+int64_t muon_scratch_elems(int64_t rows, int64_t cols, bool bf16, int64_t n);
+// MuonState.step for n same-shape matrices at once (batched GEMMs).
+int32_t muon_group_step(hipStream_t st, float* const* params, const float* const* grads, float* const* mbufs, int n,
+                        int64_t rows, int64_t cols, double initial_lr, double lrm, double momentum, double wd,
+                        bool bf16, float* scratch);
 
 }  // namespace ar
 

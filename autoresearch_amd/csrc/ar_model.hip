@@ -282,8 +282,11 @@ static int32_t gpt_build(ar_gpt* m) {
     const int64_t dw_shapes[][2] = {{C, C}, {kv, C}, {F, C}, {C, F}, {V, C}};
     for (auto& s : dw_shapes)
         upd(gemm_partial_elems(2, BT, s[0], s[1], gemm_auto_splits(2, m->bf16, BT, s[0], s[1])));
-    const int64_t muon_shapes[][2] = {{C, C}, {kv, C}, {F, C}, {C, F}};
-    for (auto& s : muon_shapes) upd(muon_scratch_elems(s[0], s[1], m->bf16));
+    const int64_t groups = (4 * Lr + kMuonMaxGroup - 1) / kMuonMaxGroup;
+    const int64_t sq = (4 * Lr + groups - 1) / groups;  // square matrices per launch group
+    upd(muon_scratch_elems(C, C, m->bf16, sq));
+    upd(muon_scratch_elems(F, C, m->bf16, Lr < kMuonMaxGroup ? Lr : kMuonMaxGroup));
+    upd(muon_scratch_elems(C, F, m->bf16, Lr < kMuonMaxGroup ? Lr : kMuonMaxGroup));
     upd(BT * (C > kv ? C : kv));                  // embedding scatter partials
     upd((int64_t)kGateBlocks * H * kGateChannels);  // ve gate partials
     m->scratch_elems = need;
@@ -460,7 +463,10 @@ extern "C" int32_t ar_gpt_backward(ar_gpt* m, const int64_t* inputs, const int64
         AR_TRY(linear_dx(m, m->grad_attn_out, m->grad_x, P(m, m->i_proj[i]), BT, C, C));
         AR_TRY(linear_dw(m, G(m, m->i_proj[i]), m->grad_x, b.attn_out, BT, C, C));
         const int64_t ws = window_size(c, i);
-        AR_TRY(ar_flash_attn_bwd_precompute_d(st, m->d_buf, b.attn_out, m->grad_attn_out, m->B, m->T, H, hd));
+        if (m->bf16)
+            AR_TRY(ar_flash_attn_bwd_precompute_d_bf16(st, m->d_buf, b.attn_out, m->grad_attn_out, m->B, m->T, H, hd));
+        else
+            AR_TRY(ar_flash_attn_bwd_precompute_d(st, m->d_buf, b.attn_out, m->grad_attn_out, m->B, m->T, H, hd));
         AR_TRY(attention(m, AttnOp::DQ, m->grad_q, nullptr, b.q, b.k, b.v, m->grad_attn_out, b.lse, m->d_buf, ws));
         AR_TRY(attention(m, AttnOp::DKV, m->grad_k, m->grad_v, b.q, b.k, b.v, m->grad_attn_out, b.lse, m->d_buf,
                          ws));
@@ -531,15 +537,38 @@ extern "C" int32_t ar_gpt_optimizer_step(ar_gpt* m, double progress) {
     if (frac > 1.0) frac = 1.0;
     const double mu = (1.0 - frac) * 0.85 + frac * 0.95;
     const double wd = 0.2 * (1.0 - progress);
+    // Muon on every 2-D matrix, grouped by shape (c_q/c_k/c_v/c_proj are
+    // [C, C]; c_fc [4C, C]; mlp_proj [C, 4C]) and run as batched GEMMs.
+    std::vector<int64_t> sq, fc, mp;
     for (int64_t i = 0; i < c.n_layer; ++i) {
-        const int64_t ids[6] = {m->i_q[i], m->i_k[i], m->i_v[i], m->i_proj[i], m->i_fc[i], m->i_mlpp[i]};
-        for (int j = 0; j < 6; ++j) {
-            const Tensor& t = m->t[ids[j]];
+        sq.push_back(m->i_q[i]);
+        sq.push_back(m->i_k[i]);
+        sq.push_back(m->i_v[i]);
+        sq.push_back(m->i_proj[i]);
+        fc.push_back(m->i_fc[i]);
+        mp.push_back(m->i_mlpp[i]);
+    }
+    for (const std::vector<int64_t>* grp : {&sq, &fc, &mp}) {
+        const int64_t total = (int64_t)grp->size();
+        const int64_t ngroups = (total + kMuonMaxGroup - 1) / kMuonMaxGroup;
+        const int64_t per = (total + ngroups - 1) / ngroups;
+        for (int64_t g0 = 0; g0 < total; g0 += per) {
+            const int n = (int)(g0 + per <= total ? per : total - g0);
+            float* ps[kMuonMaxGroup];
+            const float* gs[kMuonMaxGroup];
+            float* ms[kMuonMaxGroup];
+            const Tensor& t0 = m->t[(*grp)[g0]];
+            for (int j = 0; j < n; ++j) {
+                const Tensor& t = m->t[(*grp)[g0 + j]];
+                ps[j] = m->params + t.offset;
+                gs[j] = m->grads + t.offset;
+                ms[j] = m->muon_buf + t.offset;
+            }
             const int e = prof_begin(m);
-            AR_TRY(muon_step(m->st, m->params + t.offset, m->grads + t.offset, m->muon_buf + t.offset, t.rows, t.cols,
-                             0.04, lrm, mu, wd, m->bf16, m->scratch));
-            const double sm = (double)(t.rows < t.cols ? t.rows : t.cols), lg = (double)(t.rows < t.cols ? t.cols : t.rows);
-            prof_end(m, e, 6, 5.0 * (4.0 * lg * sm * sm + 2.0 * sm * sm * sm));
+            AR_TRY(muon_group_step(m->st, ps, gs, ms, n, t0.rows, t0.cols, 0.04, lrm, mu, wd, m->bf16, m->scratch));
+            const double smd = (double)(t0.rows < t0.cols ? t0.rows : t0.cols);
+            const double lgd = (double)(t0.rows < t0.cols ? t0.cols : t0.rows);
+            prof_end(m, e, 6, n * 5.0 * (4.0 * lgd * smd * smd + 2.0 * smd * smd * smd));
         }
     }
     return AR_OK;

@@ -1,6 +1,15 @@
 // ar_optim.hip -- Muon (optimizer.mojo:255-342): Nesterov momentum ->
 // Frobenius normalisation -> 5 Polar Express iterations -> cautious update,
-// built on the MFMA GEMMs.
+// for a *group* of same-shape matrices at once.
+//
+// The reference runs ~27 launches per matrix, one matrix at a time (about
+// 1,300 launches per step at depth 8, most of them 512x512 GEMMs that fill a
+// fraction of the GPU).  Here every product of an iteration is one batched
+// MFMA GEMM over the whole group (e.g. all 32 512x512 attention matrices),
+// and the element-wise steps are multi-tensor kernels over the group:
+// 29 launches per group per step.  A wide matrix (rows < cols) uses the
+// A = X X^T / B @ X formulation directly through the GEMM operand layouts,
+// exactly as the reference's wide branch (optimizer.mojo:297-303, 327-332).
 #include <math.h>
 
 #include "ar_internal.hpp"
@@ -15,56 +24,135 @@ static const double kPolarB[5] = {-22.48329292557795, -2.808917465908714, -2.772
 static const double kPolarC[5] = {15.878769915207462, 0.5000178451051316, 0.5060648178503393,
                                   0.46449024233003106, 0.42323551169305323};
 
-static inline int64_t align64(int64_t n) { return (n + 63) & ~int64_t(63); }
+namespace {
 
-int64_t muon_scratch_elems(int64_t rows, int64_t cols, bool bf16) {
-    const int64_t size = rows * cols;
-    const int64_t small = rows >= cols ? cols : rows;
-    int64_t gram_partial = 0;
-    if (rows >= cols) gram_partial = gemm_partial_elems(2, rows, cols, cols, gemm_auto_splits(2, bf16, rows, cols, cols));
-    return align64(kSumBlocks + 64) + align64(size) + 3 * align64(small * small) + align64(gram_partial);
+constexpr int kNormBlocks = 64;  // fixed per-matrix partial count (deterministic)
+
+struct GroupTable {
+    float* p[kMuonMaxGroup];
+    const float* g[kMuonMaxGroup];
+    float* m[kMuonMaxGroup];
+};
+
+inline int64_t align64(int64_t n) { return (n + 63) & ~int64_t(63); }
+
+// X_j = (1-mu) g + mu * (mu buf + (1-mu) g); buf updated (optimizer.mojo:132-146);
+// partial[j][b] = this block's sum of X^2.
+__global__ void nesterov_multi_k(GroupTable t, float* X, int64_t size, float mu, float* partial) {
+    __shared__ float red[4];
+    const int j = blockIdx.y;
+    const float* g = t.g[j];
+    float* buf = t.m[j];
+    float* x = X + (int64_t)j * size;
+    float ss = 0.f;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size; i += (int64_t)gridDim.x * blockDim.x) {
+        const float gv = g[i];
+        const float mm = mu * buf[i] + (1.0f - mu) * gv;
+        buf[i] = mm;
+        const float o = (1.0f - mu) * gv + mu * mm;
+        x[i] = o;
+        ss += o * o;
+    }
+    ss = block_sum(ss, red);
+    if (threadIdx.x == 0) partial[j * kNormBlocks + blockIdx.x] = ss;
 }
 
-int32_t muon_step(hipStream_t st, float* params, float* grads, float* momentum_buf, int64_t rows, int64_t cols,
-                  double initial_lr, double lrm, double momentum, double wd, bool bf16, float* scratch) {
+// scale[j] = 1 / (||X_j||_F * 1.02 + 1e-6)  (optimizer.mojo:178)
+__global__ void norm_finish_k(float* scale, const float* partial) {
+    const int j = threadIdx.x;
+    float s = 0.f;
+    for (int b = 0; b < kNormBlocks; ++b) s += partial[j * kNormBlocks + b];
+    scale[j] = 1.0f / (sqrtf(s) * 1.02f + 1e-6f);
+}
+
+__global__ void scale_multi_k(float* X, int64_t size, const float* scale) {
+    const int j = blockIdx.y;
+    const float sc = scale[j];
+    float* x = X + (int64_t)j * size;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size; i += (int64_t)gridDim.x * blockDim.x)
+        x[i] = x[i] * sc;
+}
+
+// p -= lr (X + wd p [X p >= 0])  (optimizer.mojo:197-210)
+__global__ void update_multi_k(GroupTable t, const float* X, int64_t size, float lr, float wd) {
+    const int j = blockIdx.y;
+    float* p = t.p[j];
+    const float* x = X + (int64_t)j * size;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size; i += (int64_t)gridDim.x * blockDim.x) {
+        const float pv = p[i], gv = x[i];
+        const float decay = (gv * pv) >= 0.0f ? wd * pv : 0.0f;
+        p[i] = pv - lr * (gv + decay);
+    }
+}
+
+}  // namespace
+
+int64_t muon_scratch_elems(int64_t rows, int64_t cols, bool bf16, int64_t n) {
+    (void)bf16;
     const int64_t size = rows * cols;
     const int64_t small = rows >= cols ? cols : rows;
-    const int64_t ss = small * small;
-    const bool tall = rows >= cols;
-    float* sum_scratch = scratch;
-    float* X = sum_scratch + align64(kSumBlocks + 64);
-    float* A = X + align64(size);
-    float* AA = A + align64(ss);
-    float* Bm = AA + align64(ss);
-    float* partial = Bm + align64(ss);
-    ar_stream_t s = reinterpret_cast<ar_stream_t>(st);
+    return align64(n * kNormBlocks) + align64(n) + 2 * align64(n * size) + 3 * align64(n * small * small);
+}
 
+int32_t muon_group_step(hipStream_t st, float* const* params, const float* const* grads, float* const* mbufs, int n,
+                        int64_t rows, int64_t cols, double initial_lr, double lrm, double momentum, double wd,
+                        bool bf16, float* scratch) {
+    if (n <= 0) return AR_OK;
+    if (n > kMuonMaxGroup) return set_error(AR_EINVAL, "muon: group of %d > %d matrices", n, kMuonMaxGroup);
+    const int64_t size = rows * cols;
+    const bool tall = rows >= cols;
+    const int64_t sm = tall ? cols : rows;
+    const int64_t ss = sm * sm;
+    float* partial = scratch;
+    float* scale = partial + align64(n * kNormBlocks);
+    float* X = scale + align64(n);
+    float* Y = X + align64(n * size);
+    float* A = Y + align64(n * size);
+    float* AA = A + align64(n * ss);
+    float* Bm = AA + align64(n * ss);
+
+    GroupTable t{};
+    for (int j = 0; j < n; ++j) {
+        t.p[j] = params[j];
+        t.g[j] = grads[j];
+        t.m[j] = mbufs[j];
+    }
     const double aspect = (double)rows / (double)cols;
     const float lr = (float)(initial_lr * lrm * (aspect > 1.0 ? sqrt(aspect) : 1.0));
-    int32_t r;
-    if ((r = ar_nesterov_momentum(s, X, grads, momentum_buf, (float)momentum, size))) return r;
-    if ((r = frob_normalize(st, X, size, sum_scratch))) return r;
+    const dim3 eg(kNormBlocks, n);
+    nesterov_multi_k<<<eg, 256, 0, st>>>(t, X, size, (float)momentum, partial);
+    norm_finish_k<<<1, n, 0, st>>>(scale, partial);
+    scale_multi_k<<<eg, 256, 0, st>>>(X, size, scale);
+    int32_t r = check_launch("muon: normalise");
+    if (r) return r;
+    ar_stream_t s = reinterpret_cast<ar_stream_t>(st);
     for (int it = 0; it < 5; ++it) {
         const float ca = (float)kPolarA[it], cb = (float)kPolarB[it], cc = (float)kPolarC[it];
-        if (tall)  // A = X^T X (the reference zero-fills then accumulates; storing is identical)
-            r = gemm_f32(st, 2, bf16, A, X, X, rows, cols, cols, false, 0, partial);
-        else  // A = X X^T
-            r = gemm_f32(st, 0, bf16, A, X, X, rows, rows, cols, false, 1, nullptr);
+        if (tall)  // A = X^T X : mo = c1, no = c2, r = row (both operands MN-major)
+            r = gemm_batched_f32(st, bf16, false, false, A, X, X, cols, cols, rows, cols, cols, cols, n, size, size,
+                                 ss);
+        else  // A = X X^T : mo = r1, no = r2, r = col (both K-major)
+            r = gemm_batched_f32(st, bf16, true, true, A, X, X, rows, rows, cols, cols, cols, rows, n, size, size, ss);
         if (r) return r;
-        if ((r = gemm_f32(st, 1, bf16, AA, A, A, small, small, small, false, 1, nullptr))) return r;  // A @ A
-        if ((r = ar_scale_add(s, Bm, A, AA, cb, cc, ss))) return r;
-        if (tall)  // grads := X @ B
-            r = gemm_f32(st, 1, bf16, grads, X, Bm, rows, cols, cols, false, 1, nullptr);
-        else  // grads := B @ X
-            r = gemm_f32(st, 1, bf16, grads, Bm, X, rows, rows, cols, false, 1, nullptr);
+        // AA = A @ A
+        if ((r = gemm_batched_f32(st, bf16, true, false, AA, A, A, sm, sm, sm, sm, sm, sm, n, ss, ss, ss))) return r;
+        if ((r = ar_scale_add(s, Bm, A, AA, cb, cc, n * ss))) return r;
+        if (tall)  // Y = X @ B
+            r = gemm_batched_f32(st, bf16, true, false, Y, X, Bm, rows, cols, cols, cols, cols, cols, n, size, ss,
+                                 size);
+        else  // Y = B @ X
+            r = gemm_batched_f32(st, bf16, true, false, Y, Bm, X, rows, cols, rows, rows, cols, cols, n, ss, size,
+                                 size);
         if (r) return r;
-        if ((r = ar_scale_add(s, X, X, grads, ca, 1.0f, size))) return r;
+        if ((r = ar_scale_add(s, X, X, Y, ca, 1.0f, n * size))) return r;
     }
-    return ar_muon_update(s, params, X, lr, (float)wd, size);
+    update_multi_k<<<eg, 256, 0, st>>>(t, X, size, lr, (float)wd);
+    return check_launch("muon: update");
 }
 
 }  // namespace ar
 
+// optimizer.mojo:255-342 for one matrix (a group of one).
 extern "C" int32_t ar_muon_step(ar_stream_t stream, float* params, float* grads, float* momentum_buf, int64_t rows,
                                 int64_t cols, double initial_lr, double lr_multiplier, double momentum,
                                 double weight_decay, int32_t precision) {
@@ -72,8 +160,11 @@ extern "C" int32_t ar_muon_step(ar_stream_t stream, float* params, float* grads,
     AR_CHECK_ARG(rows > 0 && cols > 0 && rows % 8 == 0 && cols % 8 == 0, "muon_step: rows, cols must be multiples of 8");
     const bool bf = precision == AR_PREC_BF16;
     int32_t st;
-    float* scratch = (float*)ar::workspace((size_t)ar::muon_scratch_elems(rows, cols, bf) * sizeof(float), &st);
+    float* scratch = (float*)ar::workspace((size_t)ar::muon_scratch_elems(rows, cols, bf, 1) * sizeof(float), &st);
     if (!scratch) return st;
-    return ar::muon_step(ar::S(stream), params, grads, momentum_buf, rows, cols, initial_lr, lr_multiplier, momentum,
-                         weight_decay, bf, scratch);
+    float* p[1] = {params};
+    const float* g[1] = {grads};
+    float* m[1] = {momentum_buf};
+    return ar::muon_group_step(ar::S(stream), p, g, m, 1, rows, cols, initial_lr, lr_multiplier, momentum,
+                               weight_decay, bf, scratch);
 }

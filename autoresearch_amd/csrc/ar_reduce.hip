@@ -185,13 +185,21 @@ __global__ void scale_by_device_scalar_k(float* x, const float* scale, int64_t n
 }
 
 // ---------------- K6 flash_attn_bwd_precompute_d (ops.mojo:329-346) ----------------
+// ROUND_DO: dO is rounded to bf16 first, as the bf16 backward rounds it for
+// dP = dO V^T.  D must equal sum_j P_j dP_j for dS_j = P_j (dP_j - D) to be
+// unbiased; a D from the unrounded dO differs from that sum by the same amount
+// for every key of the row, which the attention-weighted mean key amplifies.
+template <bool ROUND_DO>
 __global__ void precompute_d_k(float* d, const float* o, const float* g, int64_t rows, int64_t hd) {
     const int lane = threadIdx.x % kWave;
     const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
     const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) / kWave;
     for (int64_t r = wave; r < rows; r += nwaves) {
         float s = 0.f;
-        for (int64_t i = lane; i < hd; i += kWave) s += o[r * hd + i] * g[r * hd + i];
+        for (int64_t i = lane; i < hd; i += kWave) {
+            const float gv = ROUND_DO ? (float)(bf16)g[r * hd + i] : g[r * hd + i];
+            s += o[r * hd + i] * gv;
+        }
         s = wave_sum(s);
         if (lane == 0) d[r] = s;
     }
@@ -293,27 +301,64 @@ __device__ __forceinline__ bool emb_chunk_start(const uint32_t* k, int64_t p) {
     return p == 0 || (p % kEmbChunk) == 0 || k[p] != k[p - 1];
 }
 
-__global__ void emb_chunk_sum_k(float* partial, const uint32_t* keys, const int32_t* tok, const float* dy,
-                                int64_t n, int64_t dim) {
+// First index in [lo, hi) whose key exceeds v (keys sorted ascending).
+__device__ __forceinline__ int64_t emb_upper(const uint32_t* k, int64_t lo, int64_t hi, uint32_t v) {
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (k[mid] <= v) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// One wave per chunk start: partial[p] = rows of the chunk summed in token
+// order.  Lanes own float4 columns (dim % 4 == 0, 16-byte aligned rows) or
+// scalar columns otherwise; rows are read 4 at a time so their loads overlap.
+template <bool VEC>
+__global__ void emb_chunk_sum_k(float* partial, const uint32_t* keys, const int32_t* tok, const float* dy, int64_t n,
+                                int64_t dim) {
     const int lane = threadIdx.x % kWave;
     const int64_t p = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
     if (p >= n || !emb_chunk_start(keys, p)) return;
-    int64_t q = p + 1;
-    while (q < n && (q % kEmbChunk) != 0 && keys[q] == keys[p]) ++q;
-    for (int64_t d = lane; d < dim; d += kWave) {
-        float s = dy[(int64_t)tok[p] * dim + d];
-        for (int64_t r = p + 1; r < q; ++r) s += dy[(int64_t)tok[r] * dim + d];
-        partial[p * dim + d] = s;
+    int64_t q = (p / kEmbChunk + 1) * kEmbChunk;
+    if (q > n) q = n;
+    q = emb_upper(keys, p, q, keys[p]);
+    if (VEC) {
+        for (int64_t d = lane; d < dim / 4; d += kWave) {
+            float4 s = reinterpret_cast<const float4*>(dy + (int64_t)tok[p] * dim)[d];
+            int64_t r = p + 1;
+            for (; r + 4 <= q; r += 4) {
+                const float4 a = reinterpret_cast<const float4*>(dy + (int64_t)tok[r] * dim)[d];
+                const float4 b = reinterpret_cast<const float4*>(dy + (int64_t)tok[r + 1] * dim)[d];
+                const float4 c = reinterpret_cast<const float4*>(dy + (int64_t)tok[r + 2] * dim)[d];
+                const float4 e = reinterpret_cast<const float4*>(dy + (int64_t)tok[r + 3] * dim)[d];
+                s.x += a.x; s.y += a.y; s.z += a.z; s.w += a.w;
+                s.x += b.x; s.y += b.y; s.z += b.z; s.w += b.w;
+                s.x += c.x; s.y += c.y; s.z += c.z; s.w += c.w;
+                s.x += e.x; s.y += e.y; s.z += e.z; s.w += e.w;
+            }
+            for (; r < q; ++r) {
+                const float4 a = reinterpret_cast<const float4*>(dy + (int64_t)tok[r] * dim)[d];
+                s.x += a.x; s.y += a.y; s.z += a.z; s.w += a.w;
+            }
+            reinterpret_cast<float4*>(partial + p * dim)[d] = s;
+        }
+    } else {
+        for (int64_t d = lane; d < dim; d += kWave) {
+            float s = dy[(int64_t)tok[p] * dim + d];
+            for (int64_t r = p + 1; r < q; ++r) s += dy[(int64_t)tok[r] * dim + d];
+            partial[p * dim + d] = s;
+        }
     }
 }
 
+// One wave per id segment: G[v] = ((G[v] + chunk_0) + chunk_1) + ...
 __global__ void emb_segment_apply_k(float* gw, const float* partial, const uint32_t* keys, int64_t n, int64_t dim) {
     const int lane = threadIdx.x % kWave;
     const int64_t p = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
     if (p >= n || !(p == 0 || keys[p] != keys[p - 1])) return;
     const uint32_t v = keys[p];
-    int64_t end = p + 1;
-    while (end < n && keys[end] == v) ++end;
+    const int64_t end = emb_upper(keys, p + 1, n, v);
     float* row = gw + (int64_t)v * dim;
     for (int64_t d = lane; d < dim; d += kWave) {
         float acc = row[d];
@@ -439,15 +484,29 @@ extern "C" int32_t ar_normalize_frobenius(ar_stream_t stream, float* data, int64
     return ar::frob_normalize(S(stream), data, size, ws);
 }
 
-extern "C" int32_t ar_flash_attn_bwd_precompute_d(ar_stream_t stream, float* d_out, const float* output,
-                                                  const float* grad_output, int64_t B, int64_t T,
-                                                  int64_t num_heads, int64_t head_dim) {
+static int32_t precompute_d(ar_stream_t stream, float* d_out, const float* output, const float* grad_output,
+                            int64_t B, int64_t T, int64_t num_heads, int64_t head_dim, bool round_do) {
     AR_CHECK_ARG(d_out && output && grad_output, "flash_attn_bwd_precompute_d: null pointer");
     AR_CHECK_ARG(B >= 0 && T >= 0 && num_heads > 0 && head_dim > 0, "flash_attn_bwd_precompute_d: bad shape");
     const int64_t rows = B * T * num_heads;
     if (rows == 0) return AR_OK;
-    precompute_d_k<<<wave_grid(rows), kBlock, 0, S(stream)>>>(d_out, output, grad_output, rows, head_dim);
+    if (round_do)
+        precompute_d_k<true><<<wave_grid(rows), kBlock, 0, S(stream)>>>(d_out, output, grad_output, rows, head_dim);
+    else
+        precompute_d_k<false><<<wave_grid(rows), kBlock, 0, S(stream)>>>(d_out, output, grad_output, rows, head_dim);
     return AR_LAUNCH_CHECK("flash_attn_bwd_precompute_d");
+}
+
+extern "C" int32_t ar_flash_attn_bwd_precompute_d(ar_stream_t stream, float* d_out, const float* output,
+                                                  const float* grad_output, int64_t B, int64_t T,
+                                                  int64_t num_heads, int64_t head_dim) {
+    return precompute_d(stream, d_out, output, grad_output, B, T, num_heads, head_dim, false);
+}
+
+extern "C" int32_t ar_flash_attn_bwd_precompute_d_bf16(ar_stream_t stream, float* d_out, const float* output,
+                                                       const float* grad_output, int64_t B, int64_t T,
+                                                       int64_t num_heads, int64_t head_dim) {
+    return precompute_d(stream, d_out, output, grad_output, B, T, num_heads, head_dim, true);
 }
 
 extern "C" int32_t ar_ve_gate_fwd(ar_stream_t stream, float* gate_out, const float* x_norm, const float* gate_weight,
@@ -497,7 +556,12 @@ extern "C" int32_t ar_embedding_bwd_sorted(ar_stream_t stream, float* grad_weigh
                                            int64_t num_tokens, int64_t embd_dim, float* partial) {
     const int64_t n = num_tokens;
     const unsigned grid = (unsigned)cdiv(n, kBlock / kWave);
-    emb_chunk_sum_k<<<grid, kBlock, 0, S(stream)>>>(partial, sorted_ids, sorted_tokens, grad_output, n, embd_dim);
+    if (embd_dim % 4 == 0 && al16(grad_output) && al16(partial))
+        emb_chunk_sum_k<true><<<grid, kBlock, 0, S(stream)>>>(partial, sorted_ids, sorted_tokens, grad_output, n,
+                                                              embd_dim);
+    else
+        emb_chunk_sum_k<false><<<grid, kBlock, 0, S(stream)>>>(partial, sorted_ids, sorted_tokens, grad_output, n,
+                                                               embd_dim);
     emb_segment_apply_k<<<grid, kBlock, 0, S(stream)>>>(grad_weight, partial, sorted_ids, n, embd_dim);
     return AR_LAUNCH_CHECK("embedding_bwd");
 }

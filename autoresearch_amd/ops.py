@@ -72,8 +72,8 @@ def flash_attn_fwd(output, lse_out, q, k, v, B, T, num_heads, head_dim, window_s
     _call("flash_attn_fwd" + _sfx(bf16), output, lse_out, q, k, v, B, T, num_heads, head_dim, window_size)
 
 
-def flash_attn_bwd_precompute_d(d_out, output, grad_output, B, T, num_heads, head_dim):
-    _call("flash_attn_bwd_precompute_d", d_out, output, grad_output, B, T, num_heads, head_dim)
+def flash_attn_bwd_precompute_d(d_out, output, grad_output, B, T, num_heads, head_dim, bf16=False):
+    _call("flash_attn_bwd_precompute_d" + _sfx(bf16), d_out, output, grad_output, B, T, num_heads, head_dim)
 
 
 def flash_attn_bwd_dq(grad_q, q, k, v, grad_output, lse, d_buf, B, T, num_heads, head_dim, window_size, bf16=False):

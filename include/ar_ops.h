@@ -73,7 +73,7 @@ int32_t ar_rope_fwd(ar_stream_t stream, float* output, const float* input, const
 /* ops.mojo:244-323  causal / sliding-window softmax attention + LSE.
  * q,k,v,output: [B*T*num_heads, head_dim]; lse_out: [B*T*num_heads].
  * Key kp visible from qp iff kp <= qp and (window_size <= 0 or kp >= qp - window_size).
- * head_dim must be 64 or 128 (AR_EUNSUPPORTED otherwise). */
+ * head_dim must be 32, 64 or 128 (AR_EUNSUPPORTED otherwise). */
 int32_t ar_flash_attn_fwd(ar_stream_t stream, float* output, float* lse_out, const float* q, const float* k,
                           const float* v, int64_t B, int64_t T, int64_t num_heads, int64_t head_dim,
                           int64_t window_size);
@@ -84,6 +84,12 @@ int32_t ar_flash_attn_fwd_bf16(ar_stream_t stream, float* output, float* lse_out
 int32_t ar_flash_attn_bwd_precompute_d(ar_stream_t stream, float* d_out, const float* output,
                                        const float* grad_output, int64_t B, int64_t T, int64_t num_heads,
                                        int64_t head_dim);
+/* D for the _bf16 backward kernels: dO is rounded to bf16 exactly as those
+ * kernels round it for dP = dO V^T, so that D = sum_j P_j dP_j holds and
+ * dS = P (dP - D) is unbiased (pair with ar_flash_attn_fwd_bf16's O). */
+int32_t ar_flash_attn_bwd_precompute_d_bf16(ar_stream_t stream, float* d_out, const float* output,
+                                            const float* grad_output, int64_t B, int64_t T, int64_t num_heads,
+                                            int64_t head_dim);
 /* ops.mojo:349-411  dQ = scale * sum_kp P (dP - D) K */
 int32_t ar_flash_attn_bwd_dq(ar_stream_t stream, float* grad_q, const float* q, const float* k, const float* v,
                              const float* grad_output, const float* lse, const float* d_buf, int64_t B, int64_t T,
@@ -190,7 +196,8 @@ int32_t ar_scale_add(ar_stream_t stream, float* output, const float* a, const fl
 int32_t ar_muon_update(ar_stream_t stream, float* params, const float* grads, float lr, float wd, int64_t size);
 /* optimizer.mojo:255-342  MuonState.step for one [rows, cols] matrix:
  * Nesterov -> Frobenius normalise -> 5 Polar Express iterations -> cautious
- * update.  Like the reference, `grads` is used as scratch and is clobbered.
+ * update.  `grads` is read only (the reference uses it as scratch after its
+ * last read, optimizer.mojo:317-332; its contents are not used afterwards).
  * precision selects the GEMM path (AR_PREC_FP32 / AR_PREC_BF16). */
 int32_t ar_muon_step(ar_stream_t stream, float* params, float* grads, float* momentum_buf, int64_t rows,
                      int64_t cols, double initial_lr, double lr_multiplier, double momentum,

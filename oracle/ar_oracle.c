@@ -694,6 +694,9 @@ struct orc_model {
     /* optimizer state */
     float *adam_m, *adam_v, *muon_buf;
     int64_t adam_step;
+    /* sum_i |g_i x_i| of the last backward's scalar-gradient reductions:
+     * the L1 mass that bounds their rounding sensitivity (tests only) */
+    double *l1_res, *l1_x0;
 };
 
 static int has_ve(const orc_config* c, int64_t i) { return (i % 2) == ((c->n_layer - 1) % 2); } /* config.mojo:45-47 */
@@ -748,6 +751,8 @@ orc_model* orc_model_create(const orc_config* cfg, int64_t B, int64_t T, int64_t
             m->i_ve[i] = m->i_gate[i] = -1;
         }
     }
+    m->l1_res = (double*)calloc((size_t)Lr, sizeof(double));
+    m->l1_x0 = (double*)calloc((size_t)Lr, sizeof(double));
     m->params = fz(m->nparams);
     m->grads = fz(m->nparams);
     m->adam_m = fz(m->nparams);
@@ -784,6 +789,7 @@ orc_model* orc_model_create(const orc_config* cfg, int64_t B, int64_t T, int64_t
 
 void orc_model_destroy(orc_model* m) {
     if (!m) return;
+    free(m->l1_res); free(m->l1_x0);
     free(m->params); free(m->grads); free(m->adam_m); free(m->adam_v); free(m->muon_buf);
     free(m->rope_cos); free(m->rope_sin);
     free(m->x); free(m->x0); free(m->x_norm); free(m->rms); free(m->q); free(m->k); free(m->v);
@@ -815,6 +821,25 @@ float* orc_model_params(orc_model* m) { return m->params; }
 float* orc_model_grads(orc_model* m) { return m->grads; }
 const float* orc_model_token_loss(const orc_model* m) { return m->loss; }
 int64_t orc_model_adam_step(const orc_model* m) { return m->adam_step; }
+/* Named activation buffers of the last forward/backward (tests only). */
+float* orc_model_buffer(orc_model* m, const char* name, int64_t layer) {
+    orc_layer_bufs* b = (layer >= 0 && layer < m->c.n_layer) ? &m->L[layer] : NULL;
+    if (!strcmp(name, "q") && b) return b->saved_q;
+    if (!strcmp(name, "k") && b) return b->saved_k;
+    if (!strcmp(name, "v") && b) return b->saved_v;
+    if (!strcmp(name, "attn_out") && b) return b->saved_attn_out;
+    if (!strcmp(name, "lse") && b) return b->saved_lse;
+    if (!strcmp(name, "grad_attn_out")) return m->grad_attn_out;
+    if (!strcmp(name, "grad_q")) return m->grad_q;
+    return NULL;
+}
+
+void orc_model_scalar_grad_l1(const orc_model* m, double* res, double* x0) {
+    for (int64_t i = 0; i < m->c.n_layer; ++i) {
+        res[i] = m->l1_res[i];
+        x0[i] = m->l1_x0[i];
+    }
+}
 
 #define P(i) (m->params + m->t[(i)].offset)
 #define G(i) (m->grads + m->t[(i)].offset)
@@ -971,6 +996,15 @@ void orc_model_backward(orc_model* m, const int64_t* inputs, const int64_t* targ
         /* Q8: post-scaled-add saved_x; Q9: grad_x0 assigned, never consumed */
         orc_scalar_grad_reduce(G(m->i_res), m->grad_x, b->saved_x, i, BT * C);
         orc_scalar_grad_reduce(G(m->i_x0), m->grad_x, m->x0, i, BT * C);
+        {
+            double a1 = 0.0, a2 = 0.0;
+            for (int64_t j = 0; j < BT * C; ++j) {
+                a1 += fabs((double)m->grad_x[j] * (double)b->saved_x[j]);
+                a2 += fabs((double)m->grad_x[j] * (double)m->x0[j]);
+            }
+            m->l1_res[i] = a1;
+            m->l1_x0[i] = a2;
+        }
         orc_scaled_add_bwd(m->grad_x, m->grad_x0, m->grad_x, P(m->i_res), P(m->i_x0), i, BT * C);
     }
     /* Q10: embedding norm backward skipped */

@@ -135,6 +135,12 @@ float orc_model_train_step(orc_model* m, const int64_t* inputs, const int64_t* t
 /* per-token loss of the last forward, [B*T] */
 const float* orc_model_token_loss(const orc_model* m);
 int64_t orc_model_adam_step(const orc_model* m);
+/* sum_i |g_i x_i| of each layer's resid_lambdas / x0_lambdas gradient sum in
+ * the last backward: the scale of their rounding sensitivity */
+void orc_model_scalar_grad_l1(const orc_model* m, double* res, double* x0);
+/* Saved activations by name ("q","k","v","attn_out","lse" per layer;
+ * "grad_attn_out","grad_q" = last layer processed by backward). */
+float* orc_model_buffer(orc_model* m, const char* name, int64_t layer);
 
 int orc_num_threads(void);
 

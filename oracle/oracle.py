@@ -113,6 +113,7 @@ def lib():
         L.orc_model_token_loss.argtypes = [ct.c_void_p]
         L.orc_model_token_loss.restype = F
         L.orc_num_threads.restype = ct.c_int
+        L.orc_model_scalar_grad_l1.argtypes = [ct.c_void_p, ct.POINTER(ct.c_double), ct.POINTER(ct.c_double)]
         _lib = L
     return _lib
 
@@ -172,6 +173,14 @@ class Model:
 
     def zero_grads(self):
         lib().orc_model_zero_grads(self.h)
+
+    def scalar_grad_l1(self):
+        """(resid, x0) arrays of sum |g x| per layer from the last backward."""
+        n = self.cfg.n_layer
+        a, b = np.zeros(n), np.zeros(n)
+        lib().orc_model_scalar_grad_l1(self.h, a.ctypes.data_as(ct.POINTER(ct.c_double)),
+                                       b.ctypes.data_as(ct.POINTER(ct.c_double)))
+        return a, b
 
     def forward(self, inputs: np.ndarray, targets: np.ndarray) -> float:
         return float(lib().orc_model_forward(self.h, _p(inputs), _p(targets)))
