@@ -35,8 +35,21 @@ using namespace ar;
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int BM = 128, BN = 128;
+// Block tile BM x BN computed by NWM x NWN wave64s; each wave owns a
+// (BM/NWM) x (BN/NWN) sub-tile made of 32x32 MFMA tiles.
+template <int BM_, int BN_, int NWM_, int NWN_>
+struct Tile {
+    static constexpr int BM = BM_, BN = BN_, NWM = NWM_, NWN = NWN_;
+    static constexpr int THREADS = 64 * NWM * NWN;
+    static constexpr int WM = BM / NWM, WN = BN / NWN;
+    static constexpr int TM = WM / 32, TN = WN / 32;
+};
+// 128x128, 4 waves of 64x64: small problems (Muon, config 1) keep >= 1 tile per CU.
+using TileS = Tile<128, 128, 2, 2>;
+// 256x256, 8 waves of 128x64: the model GEMMs (M = B*T).  Per k-step a wave
+// reads 4 A + 2 B fragments for 8 MFMAs, and a block re-reads each operand
+// panel half as often as with 128x128 tiles.
+using TileL = Tile<256, 256, 2, 4>;
 
 enum Epi { EPI_STORE = 0, EPI_ACCUM = 1, EPI_PARTIAL = 2 };
 
@@ -89,7 +102,7 @@ __device__ __forceinline__ void vzero(T (&dst)[N]) {
 }
 
 // Global -> register -> LDS tile loader for one operand (ROWS x BK tile).
-template <typename TG, typename LT, bool KMAJ, int ROWS, int BK, int CW>
+template <typename TG, typename LT, bool KMAJ, int ROWS, int BK, int CW, int kThreads>
 struct TileLoader {
     static constexpr int MW = 4;  // rows per MN-major item
     static constexpr int NPASS = KMAJ ? (ROWS * BK / CW) / kThreads : ((BK / CW) * (ROWS / MW)) / kThreads;
@@ -174,18 +187,21 @@ __device__ __forceinline__ void tile_coords(int64_t tiles_n, int64_t tiles_mn, i
     tn = r % tiles_n;
 }
 
-template <typename TA, typename TB, typename TC, bool AK, bool BKM, bool BF16, int EPI>
-__global__ __launch_bounds__(kThreads) void gemm_k(TC* C, const TA* A, const TB* B, int64_t M, int64_t N,
+template <typename TA, typename TB, typename TC, bool AK, bool BKM, bool BF16, int EPI, typename TL>
+__global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const TB* B, int64_t M, int64_t N,
                                                       int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
                                                       int64_t k_per_split, float* partial, int64_t batch,
                                                       int64_t sA, int64_t sB, int64_t sC) {
     using MM = Mfma<BF16>;
     using LT = typename MM::LT;
+    constexpr int BM = TL::BM, BN = TL::BN, TM = TL::TM, TN = TL::TN;
     constexpr int BK = MM::BK, LDK = MM::LDK, CW = MM::CW;
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    LT* lds = reinterpret_cast<LT*>(smem_raw);
-    LT* lA[2] = {lds, lds + (BM + BN) * LDK};
-    LT* lB[2] = {lds + BM * LDK, lds + (BM + BN) * LDK + BM * LDK};
+    // Stage s occupies [s*(BM+BN)*LDK, (s+1)*(BM+BN)*LDK): A rows then B rows.
+    // Stage addresses are formed by arithmetic on the __shared__ base (never
+    // through a pointer array), so every access stays a ds_read / ds_write.
+    LT* const lds = reinterpret_cast<LT*>(smem_raw);
+    constexpr int STAGE = (BM + BN) * LDK;
 
     const int64_t tiles_n = (N + BN - 1) / BN, tiles_m = (M + BM - 1) / BM;
     const int64_t tiles_mn = tiles_m * tiles_n;
@@ -201,16 +217,16 @@ __global__ __launch_bounds__(kThreads) void gemm_k(TC* C, const TA* A, const TB*
     const int64_t kend = (kbeg + k_per_split < K) ? kbeg + k_per_split : K;
 
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    const int wm = wave / 2, wn = wave % 2;
+    const int wm = wave / TL::NWN, wn = wave % TL::NWN;
 
-    TileLoader<TA, LT, AK, BM, BK, CW> la;
-    TileLoader<TB, LT, BKM, BN, BK, CW> lb;
+    TileLoader<TA, LT, AK, BM, BK, CW, TL::THREADS> la;
+    TileLoader<TB, LT, BKM, BN, BK, CW, TL::THREADS> lb;
 
-    f32x16 acc[2][2];
+    f32x16 acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
@@ -218,8 +234,8 @@ __global__ __launch_bounds__(kThreads) void gemm_k(TC* C, const TA* A, const TB*
     if (nk > 0) {
         la.load(A, lda, m0, M, kbeg, kend);
         lb.load(B, ldb, n0, N, kbeg, kend);
-        la.store(lA[0], LDK);
-        lb.store(lB[0], LDK);
+        la.store(lds, LDK);
+        lb.store(lds + BM * LDK, LDK);
     }
     __syncthreads();
     for (int64_t kt = 0; kt < nk; ++kt) {
@@ -229,37 +245,37 @@ __global__ __launch_bounds__(kThreads) void gemm_k(TC* C, const TA* A, const TB*
             la.load(A, lda, m0, M, kbeg + (kt + 1) * BK, kend);
             lb.load(B, ldb, n0, N, kbeg + (kt + 1) * BK, kend);
         }
-        const LT* a_base = lA[cur] + (wm * 64 + (lane & 31)) * LDK + MM::lane_k(lane);
-        const LT* b_base = lB[cur] + (wn * 64 + (lane & 31)) * LDK + MM::lane_k(lane);
+        const LT* a_base = lds + cur * STAGE + (wm * TL::WM + (lane & 31)) * LDK + MM::lane_k(lane);
+        const LT* b_base = lds + cur * STAGE + (BM + wn * TL::WN + (lane & 31)) * LDK + MM::lane_k(lane);
 #pragma unroll
         for (int ks = 0; ks < BK / MM::KS; ++ks) {
-            typename MM::Frag fa[2], fb[2];
+            typename MM::Frag fa[TM], fb[TN];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) fa[i] = MM::frag(a_base + i * 32 * LDK + ks * MM::KS);
+            for (int i = 0; i < TM; ++i) fa[i] = MM::frag(a_base + i * 32 * LDK + ks * MM::KS);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) fb[j] = MM::frag(b_base + j * 32 * LDK + ks * MM::KS);
+            for (int j = 0; j < TN; ++j) fb[j] = MM::frag(b_base + j * 32 * LDK + ks * MM::KS);
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = MM::mma(fa[i], fb[j], acc[i][j]);
+                for (int j = 0; j < TN; ++j) acc[i][j] = MM::mma(fa[i], fb[j], acc[i][j]);
         }
         if (more) {
-            la.store(lA[cur ^ 1], LDK);
-            lb.store(lB[cur ^ 1], LDK);
+            la.store(lds + (cur ^ 1) * STAGE, LDK);
+            lb.store(lds + (cur ^ 1) * STAGE + BM * LDK, LDK);
         }
         __syncthreads();
     }
 
     // Epilogue.
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+        for (int j = 0; j < TN; ++j) {
+            const int64_t col = n0 + wn * TL::WN + j * 32 + (lane & 31);
             if (col >= N) continue;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int64_t row = m0 + wm * 64 + i * 32 + acc_row(v, lane);
+                const int64_t row = m0 + wm * TL::WM + i * 32 + acc_row(v, lane);
                 if (row >= M) continue;
                 const float x = acc[i][j][v];
                 if constexpr (EPI == EPI_STORE) {
@@ -290,10 +306,10 @@ __global__ void splitk_reduce_k(TC* C, const float* partial, int64_t M, int64_t 
     }
 }
 
-template <bool BF16>
+template <bool BF16, typename TL>
 constexpr size_t lds_bytes() {
     using MM = Mfma<BF16>;
-    return (size_t)2 * (BM + BN) * MM::LDK * sizeof(typename MM::LT);
+    return (size_t)2 * (TL::BM + TL::BN) * MM::LDK * sizeof(typename MM::LT);
 }
 
 }  // namespace
@@ -316,31 +332,47 @@ static int64_t choose_splits(int64_t tiles, int64_t K, int64_t splits_req, int64
 }
 
 // Launches one GEMM in GEMM space: C[mo, no] (+)= sum_r A(mo, r) B(no, r).
+template <typename TA, typename TB, typename TC, bool AK, bool BKM, bool BF16, typename TL>
+static int32_t gemm_launch_t(hipStream_t st, TC* C, const TA* A, const TB* B, int64_t M, int64_t N, int64_t K,
+                             int64_t lda, int64_t ldb, int64_t ldc, bool accumulate, int64_t splits_req,
+                             float* partial, const char* nm, int64_t batch, int64_t sA, int64_t sB, int64_t sC) {
+    const int64_t tiles = ((M + TL::BM - 1) / TL::BM) * ((N + TL::BN - 1) / TL::BN);
+    int64_t kps = 0;
+    const int64_t splits = choose_splits<BF16>(tiles * batch, K, splits_req, kps);
+    const size_t lds = lds_bytes<BF16, TL>();
+    const unsigned grid = (unsigned)(tiles * splits * batch);
+    if (splits == 1) {
+        if (accumulate)
+            gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_ACCUM, TL><<<grid, TL::THREADS, lds, st>>>(
+                C, A, B, M, N, K, lda, ldb, ldc, kps, nullptr, batch, sA, sB, sC);
+        else
+            gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_STORE, TL><<<grid, TL::THREADS, lds, st>>>(
+                C, A, B, M, N, K, lda, ldb, ldc, kps, nullptr, batch, sA, sB, sC);
+        return check_launch(nm);
+    }
+    if (!partial) return set_error(AR_EINVAL, "%s: split-K scratch missing", nm);
+    gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_PARTIAL, TL><<<grid, TL::THREADS, lds, st>>>(
+        C, A, B, M, N, K, lda, ldb, ldc, kps, partial, batch, sA, sB, sC);
+    splitk_reduce_k<TC><<<flat_grid(M * N * batch, 256 * 4), 256, 0, st>>>(C, partial, M, N, ldc, splits,
+                                                                           accumulate ? 1 : 0, batch, sC);
+    return check_launch(nm);
+}
+
+// Large tiles when the problem has enough of them to fill the chip.
+inline bool use_large(int64_t M, int64_t N, int64_t batch) {
+    return ((M + 255) / 256) * ((N + 255) / 256) * batch >= 256;
+}
+
 template <typename TA, typename TB, typename TC, bool AK, bool BKM, bool BF16>
 static int32_t gemm_launch(hipStream_t st, TC* C, const TA* A, const TB* B, int64_t M, int64_t N, int64_t K,
                            int64_t lda, int64_t ldb, int64_t ldc, bool accumulate, int64_t splits_req,
                            float* partial, const char* nm, int64_t batch = 1, int64_t sA = 0, int64_t sB = 0,
                            int64_t sC = 0) {
-    const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    int64_t kps = 0;
-    const int64_t splits = choose_splits<BF16>(tiles * batch, K, splits_req, kps);
-    const size_t lds = lds_bytes<BF16>();
-    const unsigned grid = (unsigned)(tiles * splits * batch);
-    if (splits == 1) {
-        if (accumulate)
-            gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_ACCUM><<<grid, kThreads, lds, st>>>(
-                C, A, B, M, N, K, lda, ldb, ldc, kps, nullptr, batch, sA, sB, sC);
-        else
-            gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_STORE><<<grid, kThreads, lds, st>>>(
-                C, A, B, M, N, K, lda, ldb, ldc, kps, nullptr, batch, sA, sB, sC);
-        return check_launch(nm);
-    }
-    if (!partial) return set_error(AR_EINVAL, "%s: split-K scratch missing", nm);
-    gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_PARTIAL><<<grid, kThreads, lds, st>>>(C, A, B, M, N, K, lda, ldb, ldc, kps,
-                                                                              partial, batch, sA, sB, sC);
-    splitk_reduce_k<TC><<<flat_grid(M * N * batch, 256 * 4), 256, 0, st>>>(C, partial, M, N, ldc, splits,
-                                                                           accumulate ? 1 : 0, batch, sC);
-    return check_launch(nm);
+    if (use_large(M, N, batch))
+        return gemm_launch_t<TA, TB, TC, AK, BKM, BF16, TileL>(st, C, A, B, M, N, K, lda, ldb, ldc, accumulate,
+                                                               splits_req, partial, nm, batch, sA, sB, sC);
+    return gemm_launch_t<TA, TB, TC, AK, BKM, BF16, TileS>(st, C, A, B, M, N, K, lda, ldb, ldc, accumulate,
+                                                           splits_req, partial, nm, batch, sA, sB, sC);
 }
 
 // GEMM-space sizes of a reference-layout call.
@@ -354,7 +386,8 @@ int64_t gemm_auto_splits(int layout, bool bf16, int64_t M, int64_t N, int64_t K)
     if (layout != 2) return 1;
     int64_t gm, gn, gk, kps;
     gemm_space(layout, M, N, K, gm, gn, gk);
-    const int64_t tiles = ((gm + BM - 1) / BM) * ((gn + BN - 1) / BN);
+    const int64_t tiles = use_large(gm, gn, 1) ? ((gm + 255) / 256) * ((gn + 255) / 256)
+                                               : ((gm + 127) / 128) * ((gn + 127) / 128);
     return bf16 ? choose_splits<true>(tiles, gk, 0, kps) : choose_splits<false>(tiles, gk, 0, kps);
 }
 
@@ -380,6 +413,35 @@ int32_t gemm_batched_f32(hipStream_t st, bool bf, bool ak, bool bk, float* C, co
     if (!ak && !bk) return AR_GB(false, false);
     return AR_GB(false, true);
 #undef AR_GB
+}
+
+// Reference-layout GEMM with per-operand storage types (bf16 compute).
+template <typename TX, typename TW, typename TC>
+static int32_t gemm_typed(hipStream_t st, int layout, TC* C, const TX* X, const TW* W, int64_t M, int64_t N,
+                          int64_t K, bool accumulate, int64_t splits, float* partial) {
+    if (layout == 0)
+        return gemm_launch<TX, TW, TC, true, true, true>(st, C, X, W, M, N, K, K, K, N, accumulate, 1, nullptr,
+                                                         "linear_fwd");
+    if (layout == 1)
+        return gemm_launch<TX, TW, TC, true, false, true>(st, C, X, W, M, K, N, N, K, K, accumulate, 1, nullptr,
+                                                          "linear_bwd_dx");
+    if (splits < 1) splits = gemm_auto_splits(2, true, M, N, K);
+    return gemm_launch<TX, TW, TC, false, false, true>(st, C, X, W, N, K, M, N, K, K, accumulate, splits, partial,
+                                                       "linear_bwd_dw");
+}
+
+int32_t gemm_bf16io(hipStream_t st, int layout, void* C, int c_bf16, const void* X, int x_bf16, const void* W,
+                    int w_bf16, int64_t M, int64_t N, int64_t K, bool accumulate, int64_t splits, float* partial) {
+#define AR_GT(TX, TW, TC) \
+    gemm_typed<TX, TW, TC>(st, layout, (TC*)C, (const TX*)X, (const TW*)W, M, N, K, accumulate, splits, partial)
+    if (x_bf16 && w_bf16 && c_bf16) return AR_GT(bf16, bf16, bf16);
+    if (x_bf16 && w_bf16 && !c_bf16) return AR_GT(bf16, bf16, float);
+    if (x_bf16 && !w_bf16 && !c_bf16) return AR_GT(bf16, float, float);
+    if (!x_bf16 && w_bf16 && !c_bf16) return AR_GT(float, bf16, float);
+    if (!x_bf16 && w_bf16 && c_bf16) return AR_GT(float, bf16, bf16);
+    if (!x_bf16 && !w_bf16 && c_bf16) return AR_GT(float, float, bf16);
+    return AR_GT(float, float, float);
+#undef AR_GT
 }
 
 int32_t gemm_f32(hipStream_t st, int layout, bool bf, float* C, const float* X, const float* W, int64_t M, int64_t N,
@@ -500,4 +562,24 @@ extern "C" int32_t ar_linear_bwd_dw(ar_stream_t stream, float* grad_weight, cons
 extern "C" int32_t ar_linear_bwd_dw_bf16(ar_stream_t stream, float* grad_weight, const float* grad_output,
                                          const float* input, int64_t M, int64_t N, int64_t K) {
     return linear_bwd_dw_impl(stream, grad_weight, grad_output, input, M, N, K, true);
+}
+
+// Reference-layout GEMM with bf16 or fp32 storage per operand; bf16 matrix
+// cores, fp32 accumulation.  No counterpart in the reference (fp32 only): the
+// storage-typed form the bf16 training step uses.
+extern "C" int32_t ar_gemm_mixed(ar_stream_t stream, int32_t layout, void* C, int32_t c_bf16, const void* X,
+                                 int32_t x_bf16, const void* W, int32_t w_bf16, int64_t M, int64_t N, int64_t K,
+                                 int32_t accumulate) {
+    int32_t st = check_gemm_args(C, X, W, M, N, K, "gemm_mixed");
+    if (st) return st;
+    if (layout < 0 || layout > 2) return set_error(AR_EINVAL, "gemm_mixed: layout must be 0 (NT), 1 (NN) or 2 (TN)");
+    if (M == 0 || N == 0 || K == 0) return AR_OK;
+    const int64_t splits = layout == 2 ? ar::gemm_auto_splits(2, true, M, N, K) : 1;
+    float* partial = nullptr;
+    if (splits > 1) {
+        partial = (float*)ar::workspace((size_t)ar::gemm_partial_elems(2, M, N, K, splits) * sizeof(float), &st);
+        if (!partial) return st;
+    }
+    return ar::gemm_bf16io(S(stream), layout, C, c_bf16, X, x_bf16, W, w_bf16, M, N, K, accumulate != 0, splits,
+                           partial);
 }

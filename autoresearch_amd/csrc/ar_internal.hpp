@@ -20,6 +20,9 @@ int64_t gemm_auto_splits(int layout, bool bf16, int64_t M, int64_t N, int64_t K)
 int64_t gemm_partial_elems(int layout, int64_t M, int64_t N, int64_t K, int64_t splits);
 int32_t gemm_f32(hipStream_t st, int layout, bool bf16, float* C, const float* X, const float* W, int64_t M,
                  int64_t N, int64_t K, bool accumulate, int64_t splits, float* partial);
+// Same, with each operand stored as bf16 (flag set) or fp32; bf16 compute.
+int32_t gemm_bf16io(hipStream_t st, int layout, void* C, int c_bf16, const void* X, int x_bf16, const void* W,
+                    int w_bf16, int64_t M, int64_t N, int64_t K, bool accumulate, int64_t splits, float* partial);
 // Batched GEMM-space form: C_b[mo,no] = sum_r A_b(mo,r) B_b(no,r); ak / bk
 // select K-major (r contiguous, row stride lda/ldb) vs MN-major storage.
 int32_t gemm_batched_f32(hipStream_t st, bool bf16, bool ak, bool bk, float* C, const float* A, const float* B,

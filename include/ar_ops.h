@@ -143,6 +143,12 @@ int32_t ar_linear_bwd_dw(ar_stream_t stream, float* grad_weight, const float* gr
                          int64_t M, int64_t N, int64_t K);
 int32_t ar_linear_bwd_dw_bf16(ar_stream_t stream, float* grad_weight, const float* grad_output,
                               const float* input, int64_t M, int64_t N, int64_t K);
+/* Storage-typed GEMM (no counterpart in the reference, which is fp32 only):
+ * layout 0/1/2 = linear_fwd / linear_bwd_dx / linear_bwd_dw semantics with
+ * X, W and C each stored as bf16 (flag 1) or fp32 (flag 0); bf16 matrix
+ * cores with fp32 accumulation.  accumulate: C += result. */
+int32_t ar_gemm_mixed(ar_stream_t stream, int32_t layout, void* C, int32_t c_bf16, const void* X, int32_t x_bf16,
+                      const void* W, int32_t w_bf16, int64_t M, int64_t N, int64_t K, int32_t accumulate);
 /* ops.mojo:1039-1085  dx = (dy - x <dy,x> / (dim rms^2)) / rms; grad_input may alias grad_output */
 int32_t ar_rmsnorm_bwd(ar_stream_t stream, float* grad_input, const float* grad_output, const float* input,
                        const float* rms_saved, int64_t num_rows, int64_t dim);
