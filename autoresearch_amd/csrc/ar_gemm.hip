@@ -51,7 +51,15 @@ using TileS = Tile<128, 128, 2, 2>;
 // panel half as often as with 128x128 tiles.
 using TileL = Tile<256, 256, 2, 4>;
 
-enum Epi { EPI_STORE = 0, EPI_ACCUM = 1, EPI_PARTIAL = 2 };
+// Epilogues.  STORE: C = acc.  ACCUM: C += acc.  PARTIAL: split-K partial.
+// ADD: C = R + acc (R = aux, fp32, row stride ldc; may alias C).
+// RELU2: C = acc (the pre-activation) and aux_out = relu(acc)^2, both TC
+//   (c_fc + relu_squared_fwd, ops.mojo:486-497, fused).
+// SOFTCAP: C = cap * tanh(acc / cap) (lm_head + softcap_fwd, ops.mojo:500-510).
+// RELU2_BWD: C = h > 0 ? 2 h acc : 0 with h = aux (TC, row stride ldc)
+//   (mlp_proj dX + relu_squared_bwd, ops.mojo:1126-1140).
+enum Epi { EPI_STORE = 0, EPI_ACCUM = 1, EPI_PARTIAL = 2, EPI_ADD = 3, EPI_RELU2 = 4, EPI_SOFTCAP = 5,
+           EPI_RELU2_BWD = 6 };
 
 template <bool BF16> struct Mfma;
 
@@ -191,7 +199,8 @@ template <typename TA, typename TB, typename TC, bool AK, bool BKM, bool BF16, i
 __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const TB* B, int64_t M, int64_t N,
                                                       int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
                                                       int64_t k_per_split, float* partial, int64_t batch,
-                                                      int64_t sA, int64_t sB, int64_t sC) {
+                                                      int64_t sA, int64_t sB, int64_t sC, const void* aux,
+                                                      void* aux_out, float cap) {
     using MM = Mfma<BF16>;
     using LT = typename MM::LT;
     constexpr int BM = TL::BM, BN = TL::BN, TM = TL::TM, TN = TL::TN;
@@ -278,10 +287,22 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
                 const int64_t row = m0 + wm * TL::WM + i * 32 + acc_row(v, lane);
                 if (row >= M) continue;
                 const float x = acc[i][j][v];
+                const int64_t o = row * ldc + col;
                 if constexpr (EPI == EPI_STORE) {
-                    C[row * ldc + col] = from_f32<TC>(x);
+                    C[o] = from_f32<TC>(x);
                 } else if constexpr (EPI == EPI_ACCUM) {
-                    C[row * ldc + col] = from_f32<TC>(to_f32(C[row * ldc + col]) + x);
+                    C[o] = from_f32<TC>(to_f32(C[o]) + x);
+                } else if constexpr (EPI == EPI_ADD) {
+                    C[o] = from_f32<TC>(static_cast<const float*>(aux)[o] + x);
+                } else if constexpr (EPI == EPI_RELU2) {
+                    const float r = x > 0.f ? x : 0.f;
+                    C[o] = from_f32<TC>(x);
+                    static_cast<TC*>(aux_out)[o] = from_f32<TC>(r * r);
+                } else if constexpr (EPI == EPI_SOFTCAP) {
+                    C[o] = from_f32<TC>(cap * tanhf(x / cap));
+                } else if constexpr (EPI == EPI_RELU2_BWD) {
+                    const float h = to_f32(static_cast<const TC*>(aux)[o]);
+                    C[o] = from_f32<TC>(h > 0.f ? 2.f * h * x : 0.f);
                 } else {
                     partial[(z * M + row) * N + col] = x;
                 }
@@ -332,27 +353,40 @@ static int64_t choose_splits(int64_t tiles, int64_t K, int64_t splits_req, int64
 }
 
 // Launches one GEMM in GEMM space: C[mo, no] (+)= sum_r A(mo, r) B(no, r).
+// epi: EPI_STORE / EPI_ACCUM select by `accumulate` when epi < 0.
 template <typename TA, typename TB, typename TC, bool AK, bool BKM, bool BF16, typename TL>
 static int32_t gemm_launch_t(hipStream_t st, TC* C, const TA* A, const TB* B, int64_t M, int64_t N, int64_t K,
                              int64_t lda, int64_t ldb, int64_t ldc, bool accumulate, int64_t splits_req,
-                             float* partial, const char* nm, int64_t batch, int64_t sA, int64_t sB, int64_t sC) {
+                             float* partial, const char* nm, int64_t batch, int64_t sA, int64_t sB, int64_t sC,
+                             int epi, const void* aux, void* aux_out, float cap) {
     const int64_t tiles = ((M + TL::BM - 1) / TL::BM) * ((N + TL::BN - 1) / TL::BN);
     int64_t kps = 0;
-    const int64_t splits = choose_splits<BF16>(tiles * batch, K, splits_req, kps);
+    const int64_t splits = epi >= 0 ? 1 : choose_splits<BF16>(tiles * batch, K, splits_req, kps);
+    if (epi >= 0) choose_splits<BF16>(tiles * batch, K, 1, kps);
     const size_t lds = lds_bytes<BF16, TL>();
     const unsigned grid = (unsigned)(tiles * splits * batch);
+#define AR_GK(E)                                                                                              \
+    gemm_k<TA, TB, TC, AK, BKM, BF16, E, TL><<<grid, TL::THREADS, lds, st>>>(C, A, B, M, N, K, lda, ldb, ldc, kps, \
+                                                                            partial, batch, sA, sB, sC, aux,    \
+                                                                            aux_out, cap)
+    if (epi >= 0) {
+        switch (epi) {
+            case EPI_ADD: AR_GK(EPI_ADD); break;
+            case EPI_RELU2: AR_GK(EPI_RELU2); break;
+            case EPI_SOFTCAP: AR_GK(EPI_SOFTCAP); break;
+            case EPI_RELU2_BWD: AR_GK(EPI_RELU2_BWD); break;
+            default: return set_error(AR_EINVAL, "%s: bad epilogue %d", nm, epi);
+        }
+        return check_launch(nm);
+    }
     if (splits == 1) {
-        if (accumulate)
-            gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_ACCUM, TL><<<grid, TL::THREADS, lds, st>>>(
-                C, A, B, M, N, K, lda, ldb, ldc, kps, nullptr, batch, sA, sB, sC);
-        else
-            gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_STORE, TL><<<grid, TL::THREADS, lds, st>>>(
-                C, A, B, M, N, K, lda, ldb, ldc, kps, nullptr, batch, sA, sB, sC);
+        if (accumulate) AR_GK(EPI_ACCUM);
+        else AR_GK(EPI_STORE);
         return check_launch(nm);
     }
     if (!partial) return set_error(AR_EINVAL, "%s: split-K scratch missing", nm);
-    gemm_k<TA, TB, TC, AK, BKM, BF16, EPI_PARTIAL, TL><<<grid, TL::THREADS, lds, st>>>(
-        C, A, B, M, N, K, lda, ldb, ldc, kps, partial, batch, sA, sB, sC);
+    AR_GK(EPI_PARTIAL);
+#undef AR_GK
     splitk_reduce_k<TC><<<flat_grid(M * N * batch, 256 * 4), 256, 0, st>>>(C, partial, M, N, ldc, splits,
                                                                            accumulate ? 1 : 0, batch, sC);
     return check_launch(nm);
@@ -367,12 +401,15 @@ template <typename TA, typename TB, typename TC, bool AK, bool BKM, bool BF16>
 static int32_t gemm_launch(hipStream_t st, TC* C, const TA* A, const TB* B, int64_t M, int64_t N, int64_t K,
                            int64_t lda, int64_t ldb, int64_t ldc, bool accumulate, int64_t splits_req,
                            float* partial, const char* nm, int64_t batch = 1, int64_t sA = 0, int64_t sB = 0,
-                           int64_t sC = 0) {
+                           int64_t sC = 0, int epi = -1, const void* aux = nullptr, void* aux_out = nullptr,
+                           float cap = 0.f) {
     if (use_large(M, N, batch))
         return gemm_launch_t<TA, TB, TC, AK, BKM, BF16, TileL>(st, C, A, B, M, N, K, lda, ldb, ldc, accumulate,
-                                                               splits_req, partial, nm, batch, sA, sB, sC);
+                                                               splits_req, partial, nm, batch, sA, sB, sC, epi, aux,
+                                                               aux_out, cap);
     return gemm_launch_t<TA, TB, TC, AK, BKM, BF16, TileS>(st, C, A, B, M, N, K, lda, ldb, ldc, accumulate,
-                                                           splits_req, partial, nm, batch, sA, sB, sC);
+                                                           splits_req, partial, nm, batch, sA, sB, sC, epi, aux,
+                                                           aux_out, cap);
 }
 
 // GEMM-space sizes of a reference-layout call.
@@ -442,6 +479,27 @@ int32_t gemm_bf16io(hipStream_t st, int layout, void* C, int c_bf16, const void*
     if (!x_bf16 && !w_bf16 && c_bf16) return AR_GT(float, float, bf16);
     return AR_GT(float, float, float);
 #undef AR_GT
+}
+
+// NT (layout 0) / NN (layout 1) GEMM with a fused epilogue (bf16 compute).
+// epi: 3 ADD (aux = fp32 R), 4 RELU2 (aux_out = act), 5 SOFTCAP (cap),
+// 6 RELU2_BWD (aux = pre-activation).  TX/TW/TC per the flags.
+int32_t gemm_epilogue(hipStream_t st, int layout, int epi, void* C, int c_bf16, const void* X, int x_bf16,
+                      const void* W, int w_bf16, int64_t M, int64_t N, int64_t K, const void* aux, void* aux_out,
+                      float cap) {
+#define AR_GE(TX, TW, TC)                                                                                          \
+    (layout == 0 ? gemm_launch<TX, TW, TC, true, true, true>(st, (TC*)C, (const TX*)X, (const TW*)W, M, N, K, K, K, N, \
+                                                             false, 1, nullptr, "gemm_epilogue", 1, 0, 0, 0, epi, aux, \
+                                                             aux_out, cap)                                         \
+                 : gemm_launch<TX, TW, TC, true, false, true>(st, (TC*)C, (const TX*)X, (const TW*)W, M, K, N, N, K,  \
+                                                              K, false, 1, nullptr, "gemm_epilogue", 1, 0, 0, 0, epi, \
+                                                              aux, aux_out, cap))
+    if (x_bf16 && w_bf16 && c_bf16) return AR_GE(bf16, bf16, bf16);
+    if (x_bf16 && w_bf16 && !c_bf16) return AR_GE(bf16, bf16, float);
+    if (!x_bf16 && w_bf16 && c_bf16) return AR_GE(float, bf16, bf16);
+    if (!x_bf16 && w_bf16 && !c_bf16) return AR_GE(float, bf16, float);
+    return set_error(AR_EINVAL, "gemm_epilogue: unsupported operand types");
+#undef AR_GE
 }
 
 int32_t gemm_f32(hipStream_t st, int layout, bool bf, float* C, const float* X, const float* W, int64_t M, int64_t N,

@@ -23,6 +23,13 @@ int32_t gemm_f32(hipStream_t st, int layout, bool bf16, float* C, const float* X
 // Same, with each operand stored as bf16 (flag set) or fp32; bf16 compute.
 int32_t gemm_bf16io(hipStream_t st, int layout, void* C, int c_bf16, const void* X, int x_bf16, const void* W,
                     int w_bf16, int64_t M, int64_t N, int64_t K, bool accumulate, int64_t splits, float* partial);
+// NT (layout 0) / NN (layout 1) GEMM with a fused epilogue, bf16 compute:
+// epi 3 ADD (C = aux + acc, aux fp32), 4 RELU2 (C = acc, aux_out = relu(acc)^2),
+// 5 SOFTCAP (C = cap tanh(acc/cap)), 6 RELU2_BWD (C = aux > 0 ? 2 aux acc : 0).
+enum { GEMM_EPI_ADD = 3, GEMM_EPI_RELU2 = 4, GEMM_EPI_SOFTCAP = 5, GEMM_EPI_RELU2_BWD = 6 };
+int32_t gemm_epilogue(hipStream_t st, int layout, int epi, void* C, int c_bf16, const void* X, int x_bf16,
+                      const void* W, int w_bf16, int64_t M, int64_t N, int64_t K, const void* aux, void* aux_out,
+                      float cap);
 // Batched GEMM-space form: C_b[mo,no] = sum_r A_b(mo,r) B_b(no,r); ak / bk
 // select K-major (r contiguous, row stride lda/ldb) vs MN-major storage.
 int32_t gemm_batched_f32(hipStream_t st, bool bf16, bool ak, bool bk, float* C, const float* A, const float* B,
