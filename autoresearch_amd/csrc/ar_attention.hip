@@ -642,3 +642,6 @@ template int32_t ar::attn_dispatch<false, float>(hipStream_t, ar::AttnOp, float*
 template int32_t ar::attn_dispatch<true, float>(hipStream_t, ar::AttnOp, float*, float*, const float*, const float*,
                                                 const float*, const float*, const float*, const float*, int64_t,
                                                 int64_t, int64_t, int64_t, int64_t);
+template int32_t ar::attn_dispatch<true, ar::bf16>(hipStream_t, ar::AttnOp, float*, float*, const ar::bf16*,
+                                                   const ar::bf16*, const ar::bf16*, const ar::bf16*, const float*,
+                                                   const float*, int64_t, int64_t, int64_t, int64_t, int64_t);

@@ -1,0 +1,578 @@
+// ar_fused.hip -- fused row kernels of the bf16 whole-step path.
+//
+// In bf16 mode every GEMM / attention operand is stored as bf16: the kernel
+// that produces it rounds it once, where the fp32-storage path rounds the
+// same fp32 value inside every consumer.  The small element-wise steps of the
+// reference around each GEMM are folded into single passes over a row:
+//
+//   resid_norm    scaled_add_fwd + rmsnorm_fwd (ops.mojo:61-104, 566-579),
+//                 on layer 0 also embedding_fwd + its rmsnorm (model.mojo:
+//                 598-603), on value-embedding layers also ve_gate_fwd
+//                 (ops.mojo:516-541) from the fp32 normalised row
+//   qkv_post      rope_fwd of q and k (ops.mojo:386-419), their per-head
+//                 rmsnorm (model.mojo:661-668), ve_apply_fwd on v
+//                 (ops.mojo:543-564), written as bf16 attention operands
+//   ce_fused      cross_entropy_fwd + cross_entropy_softcap_bwd (ops.mojo:
+//                 713-864) from one read of the logits row
+//   qkv_bwd_post  rope_bwd of dq and dk (ops.mojo:1088-1123), ve_apply_bwd
+//                 (ops.mojo:1193-1237), packing [dq | dk | dv] as bf16 for
+//                 the fused QKV dX / dW GEMMs
+//   norm_bwd      rmsnorm_bwd (ops.mojo:1039-1085) + add_residual, and on the
+//                 attention norm the two learned-scalar gradient dots
+//                 (ops.mojo:1277-1308) and scaled_add_bwd (ops.mojo:1311-1336)
+//
+// Per element the arithmetic is the reference kernels'; only the order of
+// the row sums (wave reductions) differs.  All reductions are fixed-order.
+#include <math.h>
+
+#include "ar_internal.hpp"
+
+namespace ar {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr float kNormEps = 1e-5f;  // ops.mojo:61-104
+
+__device__ __forceinline__ void st_bf16x4(bf16* p, float4 v) {
+    bf16x4 o;
+    o[0] = (bf16)v.x;
+    o[1] = (bf16)v.y;
+    o[2] = (bf16)v.z;
+    o[3] = (bf16)v.w;
+    *reinterpret_cast<bf16x4*>(p) = o;
+}
+__device__ __forceinline__ float dot4(float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; }
+__device__ __forceinline__ float4 axpby4(float sa, float4 a, float sb, float4 b) {
+    return make_float4(sa * a.x + sb * b.x, sa * a.y + sb * b.y, sa * a.z + sb * b.z, sa * a.w + sb * b.w);
+}
+__device__ __forceinline__ float4 div4(float4 a, float s) { return make_float4(a.x / s, a.y / s, a.z / s, a.w / s); }
+__device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
+__device__ __forceinline__ float4 mul4(float4 a, float s) { return make_float4(a.x * s, a.y * s, a.z * s, a.w * s); }
+
+__device__ __forceinline__ int64_t wave_id() { return ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave; }
+__device__ __forceinline__ int64_t wave_count() { return ((int64_t)gridDim.x * blockDim.x) / kWave; }
+
+// Sum over aligned groups of G lanes (G a power of two <= 64).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// ---------------------------------------------------------------------
+// resid_norm: one wave per row; the row stays in registers (NC float4 per
+// lane, chunk i = lane + 64 j).
+//   MODE 0 (layer 0): x0 = rmsnorm(table[idx]); x = sa x0 + sb x0
+//   MODE 1:           x = sa xin + sb x0
+//   MODE 2:           x = xin (no residual mix; x not written)
+// then rms = sqrt(mean(x^2) + eps), xn = x / rms (bf16), and with a gate:
+// xg = xn[:, :gc] (fp32) and gate[h] = 2 sigmoid(sum_c w[h, c] xn[c]).
+struct NormArgs {
+    float* x0_out;
+    float* x_out;
+    float* rms_out;
+    bf16* xn_out;
+    float* xg_out;
+    float* gate_out;
+    const float* xin;
+    const float* x0;
+    const float* table;
+    const int64_t* idx;
+    const float* sa;
+    const float* sb;
+    const float* gate_w;
+    int64_t layer, rows, C;
+    int nkv, gc;
+};
+
+template <int NC, int MODE>
+__global__ __launch_bounds__(kBlock) void resid_norm_k(NormArgs a) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t C4 = a.C / 4;
+    float sa = 0.f, sb = 0.f;
+    if (MODE != 2) {
+        sa = a.sa[a.layer];
+        sb = a.sb[a.layer];
+    }
+    for (int64_t r = wave_id(); r < a.rows; r += wave_count()) {
+        float4 v[NC];
+        if (MODE == 0) {
+            const float4* e = reinterpret_cast<const float4*>(a.table + a.idx[r] * a.C);
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                const int64_t i = lane + 64 * j;
+                v[j] = i < C4 ? e[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                ss += dot4(v[j], v[j]);
+            }
+            ss = wave_sum(ss);
+            const float rms0 = sqrtf(ss / (float)a.C + kNormEps);
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                const int64_t i = lane + 64 * j;
+                v[j] = div4(v[j], rms0);
+                if (i < C4) reinterpret_cast<float4*>(a.x0_out + r * a.C)[i] = v[j];
+                v[j] = axpby4(sa, v[j], sb, v[j]);
+            }
+        } else {
+            const float4* xi = reinterpret_cast<const float4*>(a.xin + r * a.C);
+            const float4* x0 = reinterpret_cast<const float4*>(a.x0 + r * a.C);
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                const int64_t i = lane + 64 * j;
+                if (i < C4) v[j] = MODE == 1 ? axpby4(sa, xi[i], sb, x0[i]) : xi[i];
+                else v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int64_t i = lane + 64 * j;
+            if (MODE != 2 && i < C4) reinterpret_cast<float4*>(a.x_out + r * a.C)[i] = v[j];
+            ss += dot4(v[j], v[j]);
+        }
+        ss = wave_sum(ss);
+        const float rms = sqrtf(ss / (float)a.C + kNormEps);
+        if (lane == 0) a.rms_out[r] = rms;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int64_t i = lane + 64 * j;
+            v[j] = div4(v[j], rms);
+            if (i < C4) st_bf16x4(a.xn_out + r * a.C + 4 * i, v[j]);
+        }
+        if (a.gate_out) {
+            // channels [0, gc) are chunk 0 of lanes [0, gc / 4)
+            const bool own = lane < a.gc / 4;
+            if (own) reinterpret_cast<float4*>(a.xg_out + r * a.gc)[lane] = v[0];
+            for (int h = 0; h < a.nkv; ++h) {
+                float p = own ? dot4(reinterpret_cast<const float4*>(a.gate_w + (int64_t)h * a.gc)[lane], v[0]) : 0.f;
+                p = wave_sum(p);
+                if (lane == h) a.gate_out[r * a.nkv + h] = 2.0f * (1.0f / (1.0f + __expf(-p)));
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------
+// qkv_post: wave per (token, part); part 0 / 1 = q / k: rope then per-head
+// rmsnorm (lane d of head group `sub` holds the pair (d, d + HD/2));
+// part 2 = v (+ gate * value embedding).  Writes bf16 [nt, C] each.
+struct QkvArgs {
+    bf16 *q, *k, *v;
+    const float* qkv;  // [nt, 3C]
+    const float *cos_t, *sin_t;
+    const float* gate;     // [nt, H] (value-embedding layers)
+    const float* table;    // value-embedding table [V, C] or null
+    const int64_t* idx;
+    int64_t nt, C, period;
+    int H;
+};
+
+template <int HD>
+__global__ __launch_bounds__(kBlock) void qkv_post_k(QkvArgs a) {
+    constexpr int HALF = HD / 2;
+    constexpr int HPI = 64 / HALF;  // heads per wave iteration
+    const int lane = threadIdx.x % kWave;
+    const int sub = lane / HALF, d = lane % HALF;
+    const int64_t C = a.C;
+    for (int64_t w = wave_id(); w < a.nt * 3; w += wave_count()) {
+        const int64_t t = w / 3;
+        const int part = (int)(w % 3);
+        const float* src = a.qkv + t * 3 * C + part * C;
+        if (part < 2) {
+            bf16* dst = (part == 0 ? a.q : a.k) + t * C;
+            const int64_t tok = t % a.period;
+            const float c = a.cos_t[tok * HALF + d], s = a.sin_t[tok * HALF + d];
+            for (int h0 = 0; h0 < a.H; h0 += HPI) {
+                const int h = h0 + sub;
+                float y1 = 0.f, y2 = 0.f;
+                if (h < a.H) {
+                    const float x1 = src[h * HD + d], x2 = src[h * HD + HALF + d];
+                    y1 = x1 * c + x2 * s;
+                    y2 = x1 * (-s) + x2 * c;
+                }
+                const float ss = group_sum<HALF>(y1 * y1 + y2 * y2);
+                const float rms = sqrtf(ss / (float)HD + kNormEps);
+                if (h < a.H) {
+                    dst[h * HD + d] = (bf16)(y1 / rms);
+                    dst[h * HD + HALF + d] = (bf16)(y2 / rms);
+                }
+            }
+        } else {
+            bf16* dst = a.v + t * C;
+            const float4* s4 = reinterpret_cast<const float4*>(src);
+            const float4* ve = a.table ? reinterpret_cast<const float4*>(a.table + a.idx[t] * C) : nullptr;
+            for (int64_t i = lane; i < C / 4; i += kWave) {
+                float4 x = s4[i];
+                if (ve) {
+                    const float g = a.gate[t * a.H + (4 * i) / HD];
+                    const float4 e = ve[i];
+                    x = make_float4(x.x + g * e.x, x.y + g * e.y, x.z + g * e.z, x.w + g * e.w);
+                }
+                st_bf16x4(dst + 4 * i, x);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------
+// ce_fused: block per token row.  loss = lse - l[target] (0 for an ignored
+// target, < 0 or >= V); grad = (softmax - onehot) * scale as bf16 (0 rows for ignored
+// targets).  NV4 > 0: the row is held in registers (NV4 float4 per thread).
+template <int NV4>
+__global__ __launch_bounds__(kBlock) void ce_fused_k(float* loss, bf16* grad, const float* logits,
+                                                     const int64_t* targets, int64_t V, float scale) {
+    __shared__ float red[kBlock / kWave];
+    const int64_t t = blockIdx.x;
+    const int64_t tg = targets[t];
+    const float4* row = reinterpret_cast<const float4*>(logits + t * V);
+    const int64_t V4 = V / 4;
+    constexpr int R = NV4 > 0 ? NV4 : 1;
+    float4 x[R];
+    float m = -INFINITY;
+    if (NV4 > 0) {
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const int64_t i = threadIdx.x + (int64_t)kBlock * j;
+            x[j] = i < V4 ? row[i] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+            m = fmaxf(m, fmaxf(fmaxf(x[j].x, x[j].y), fmaxf(x[j].z, x[j].w)));
+        }
+    } else {
+        for (int64_t i = threadIdx.x; i < V4; i += kBlock) {
+            const float4 y = row[i];
+            m = fmaxf(m, fmaxf(fmaxf(y.x, y.y), fmaxf(y.z, y.w)));
+        }
+    }
+    m = block_max(m, red);
+    float s = 0.f;
+    if (NV4 > 0) {
+#pragma unroll
+        for (int j = 0; j < R; ++j)
+            s += __expf(x[j].x - m) + __expf(x[j].y - m) + __expf(x[j].z - m) + __expf(x[j].w - m);
+    } else {
+        for (int64_t i = threadIdx.x; i < V4; i += kBlock) {
+            const float4 y = row[i];
+            s += __expf(y.x - m) + __expf(y.y - m) + __expf(y.z - m) + __expf(y.w - m);
+        }
+    }
+    s = block_sum(s, red);
+    const bool live = tg >= 0 && tg < V;  // other targets are ignored rows
+    if (loss && threadIdx.x == 0) loss[t] = live ? -logits[t * V + tg] + (m + logf(s)) : 0.f;
+    bf16* g = grad + t * V;
+    auto emit = [&](int64_t i, float4 y) {
+        float4 o;
+        if (!live) {
+            o = make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+            o = make_float4(__expf(y.x - m) / s, __expf(y.y - m) / s, __expf(y.z - m) / s, __expf(y.w - m) / s);
+            const int64_t e = tg - 4 * i;
+            if (e == 0) o.x -= 1.0f;
+            if (e == 1) o.y -= 1.0f;
+            if (e == 2) o.z -= 1.0f;
+            if (e == 3) o.w -= 1.0f;
+            o = mul4(o, scale);
+        }
+        st_bf16x4(g + 4 * i, o);
+    };
+    if (NV4 > 0) {
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const int64_t i = threadIdx.x + (int64_t)kBlock * j;
+            if (i < V4) emit(i, x[j]);
+        }
+    } else {
+        for (int64_t i = threadIdx.x; i < V4; i += kBlock) emit(i, row[i]);
+    }
+}
+
+// ---------------------------------------------------------------------
+// qkv_bwd_post: wave per (token, part).  Parts 0 / 1: inverse rope of dq /
+// dk; part 2: dv, and on value-embedding layers gve = gate * dv and
+// ggate[h] = sum_d ve[d] dv[d] (groups of HD/4 lanes hold one head).
+struct QkvBwdArgs {
+    bf16* gqkv;  // [nt, 3C]
+    float* gve;  // [nt, C]
+    float* ggate;
+    const float *gq, *gk, *gv;
+    const float *cos_t, *sin_t;
+    const float* gate;
+    const float* table;
+    const int64_t* idx;
+    int64_t nt, C, period;
+    int H;
+};
+
+template <int HD>
+__global__ __launch_bounds__(kBlock) void qkv_bwd_post_k(QkvBwdArgs a) {
+    constexpr int HALF = HD / 2;
+    constexpr int HPI = 64 / HALF;
+    constexpr int G = HD / 4;
+    const int lane = threadIdx.x % kWave;
+    const int sub = lane / HALF, d = lane % HALF;
+    const int64_t C = a.C;
+    for (int64_t w = wave_id(); w < a.nt * 3; w += wave_count()) {
+        const int64_t t = w / 3;
+        const int part = (int)(w % 3);
+        bf16* dst = a.gqkv + t * 3 * C + part * C;
+        if (part < 2) {
+            const float* src = (part == 0 ? a.gq : a.gk) + t * C;
+            const int64_t tok = t % a.period;
+            const float c = a.cos_t[tok * HALF + d], s = -a.sin_t[tok * HALF + d];
+            for (int h0 = 0; h0 < a.H; h0 += HPI) {
+                const int h = h0 + sub;
+                if (h < a.H) {
+                    const float x1 = src[h * HD + d], x2 = src[h * HD + HALF + d];
+                    dst[h * HD + d] = (bf16)(x1 * c + x2 * s);
+                    dst[h * HD + HALF + d] = (bf16)(x1 * (-s) + x2 * c);
+                }
+            }
+        } else {
+            const float4* s4 = reinterpret_cast<const float4*>(a.gv + t * C);
+            const float4* ve = a.table ? reinterpret_cast<const float4*>(a.table + a.idx[t] * C) : nullptr;
+            for (int64_t i0 = 0; i0 < C / 4; i0 += kWave) {
+                const int64_t i = i0 + lane;
+                const bool ok = i < C / 4;
+                const float4 x = ok ? s4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                if (ok) st_bf16x4(dst + 4 * i, x);
+                if (ve) {
+                    const int h = (int)((4 * i) / HD);
+                    float dg = 0.f;
+                    if (ok) {
+                        const float g = a.gate[t * a.H + h];
+                        reinterpret_cast<float4*>(a.gve + t * C)[i] = mul4(x, g);
+                        dg = dot4(ve[i], x);
+                    }
+                    dg = group_sum<G>(dg);
+                    if (ok && lane % G == 0) a.ggate[t * a.H + h] = dg;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------
+// norm_bwd: wave per row, row in registers.
+//   MODE 0: gx = rmsnorm_bwd(gx, x, rms)                      (final norm)
+//   MODE 1: gx = gx + rmsnorm_bwd(gn, x, rms)                 (MLP norm)
+//   MODE 2: g = gx + rmsnorm_bwd(gn, x, rms); dots g.x, g.x0 into this
+//           wave's partial; gx = res[layer] * g               (attention norm)
+// and gxb = bf16(gx).  MODE 2 runs on a fixed grid of kNormBwdWaves waves.
+struct NormBwdArgs {
+    float* gx;
+    bf16* gxb;
+    const float* gn;
+    const float* x;
+    const float* rms;
+    const float* x0;
+    const float* res;
+    float* partial;
+    int64_t layer, rows, C;
+};
+
+template <int NC, int MODE>
+__global__ __launch_bounds__(kBlock) void norm_bwd_k(NormBwdArgs a) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t C4 = a.C / 4;
+    const float scale = MODE == 2 ? a.res[a.layer] : 1.0f;
+    float p1 = 0.f, p2 = 0.f;
+    for (int64_t r = wave_id(); r < a.rows; r += wave_count()) {
+        const float4* g4 = reinterpret_cast<const float4*>((MODE == 0 ? a.gx : a.gn) + r * a.C);
+        const float4* x4 = reinterpret_cast<const float4*>(a.x + r * a.C);
+        float4 g[NC], x[NC];
+        float dot = 0.f;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int64_t i = lane + 64 * j;
+            g[j] = i < C4 ? g4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            x[j] = i < C4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            dot += dot4(g[j], x[j]);
+        }
+        dot = wave_sum(dot);
+        const float rr = a.rms[r];
+        const float coef = dot / ((float)a.C * (rr * rr));
+        float4* o4 = reinterpret_cast<float4*>(a.gx + r * a.C);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int64_t i = lane + 64 * j;
+            if (i >= C4) continue;
+            float4 o = make_float4((g[j].x - x[j].x * coef) / rr, (g[j].y - x[j].y * coef) / rr,
+                                   (g[j].z - x[j].z * coef) / rr, (g[j].w - x[j].w * coef) / rr);
+            if (MODE != 0) o = add4(o4[i], o);
+            if (MODE == 2) {
+                p1 += dot4(o, x[j]);
+                p2 += dot4(o, reinterpret_cast<const float4*>(a.x0 + r * a.C)[i]);
+                o = mul4(o, scale);
+            }
+            o4[i] = o;
+            st_bf16x4(a.gxb + r * a.C + 4 * i, o);
+        }
+    }
+    if (MODE == 2) {
+        p1 = wave_sum(p1);
+        p2 = wave_sum(p2);
+        if (lane == 0) {
+            a.partial[2 * wave_id()] = p1;
+            a.partial[2 * wave_id() + 1] = p2;
+        }
+    }
+}
+
+__global__ void scalar_finish_k(float* g_res, float* g_x0, const float* partial, int64_t nwaves, int64_t layer) {
+    __shared__ float red[kBlock / kWave];
+    float s1 = 0.f, s2 = 0.f;
+    for (int64_t i = threadIdx.x; i < nwaves; i += kBlock) {
+        s1 += partial[2 * i];
+        s2 += partial[2 * i + 1];
+    }
+    s1 = block_sum(s1, red);
+    s2 = block_sum(s2, red);
+    if (threadIdx.x == 0) {
+        g_res[layer] += s1;
+        g_x0[layer] += s2;
+    }
+}
+
+__global__ void to_bf16_k(bf16* out, const float* in, int64_t n4) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x)
+        st_bf16x4(out + 4 * i, reinterpret_cast<const float4*>(in)[i]);
+}
+
+// D[r] = sum_d O[r, d] * dO[r, d] with dO stored as bf16; groups of HD/4
+// lanes hold one row.
+template <int G>
+__global__ __launch_bounds__(kBlock) void precompute_d_mixed_k(float* d, const float* o, const bf16* g, int64_t rows) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t total = rows * G;
+    for (int64_t base = wave_id() * kWave; base < total; base += wave_count() * kWave) {
+        const int64_t f = base + lane;
+        float s = 0.f;
+        if (f < total) {
+            const float4 ov = reinterpret_cast<const float4*>(o)[f];
+            const bf16x4 gv = reinterpret_cast<const bf16x4*>(g)[f];
+            s = ov.x * (float)gv[0] + ov.y * (float)gv[1] + ov.z * (float)gv[2] + ov.w * (float)gv[3];
+        }
+        s = group_sum<G>(s);
+        if (f < total && lane % G == 0) d[f / G] = s;
+    }
+}
+
+inline unsigned wave_blocks(int64_t rows) { return flat_grid(rows, kBlock / kWave); }
+
+}  // namespace
+
+// ---------------------------------------------------------------------
+// host entry points (shapes validated by the caller, ar_model.hip)
+
+int32_t resid_norm(hipStream_t st, int mode, float* x0_out, float* x_out, float* rms_out, bf16* xn_out,
+                   float* xg_out, float* gate_out, const float* xin, const float* x0, const float* table,
+                   const int64_t* idx, const float* sa, const float* sb, int64_t layer, const float* gate_w,
+                   int64_t nkv, int64_t gc, int64_t rows, int64_t C) {
+    if (C % 4 != 0 || C > 256 * 16) return set_error(AR_EUNSUPPORTED, "resid_norm: n_embd %lld", (long long)C);
+    if (gate_out && (gc % 4 != 0 || gc > 256 || gc > C))
+        return set_error(AR_EUNSUPPORTED, "resid_norm: gate channels %lld", (long long)gc);
+    NormArgs a{x0_out, x_out, rms_out, xn_out, xg_out, gate_out, xin, x0, table, idx, sa, sb, gate_w,
+               layer, rows, C, (int)nkv, (int)gc};
+    const int nc = (int)cdiv(C, 256);
+    const unsigned grid = wave_blocks(rows);
+#define AR_RN(NC)                                                                              \
+    do {                                                                                       \
+        if (mode == 0) resid_norm_k<NC, 0><<<grid, kBlock, 0, st>>>(a);                        \
+        else if (mode == 1) resid_norm_k<NC, 1><<<grid, kBlock, 0, st>>>(a);                   \
+        else resid_norm_k<NC, 2><<<grid, kBlock, 0, st>>>(a);                                  \
+    } while (0)
+    if (nc <= 1) AR_RN(1);
+    else if (nc <= 2) AR_RN(2);
+    else if (nc <= 4) AR_RN(4);
+    else if (nc <= 8) AR_RN(8);
+    else AR_RN(16);
+#undef AR_RN
+    return check_launch("resid_norm");
+}
+
+int32_t qkv_post(hipStream_t st, bf16* q, bf16* k, bf16* v, const float* qkv, const float* cos_t, const float* sin_t,
+                 int64_t period, const float* gate, const float* table, const int64_t* idx, int64_t nt, int64_t C,
+                 int64_t H, int64_t hd) {
+    QkvArgs a{q, k, v, qkv, cos_t, sin_t, gate, table, idx, nt, C, period, (int)H};
+    const unsigned grid = wave_blocks(nt * 3);
+    switch (hd) {
+        case 32: qkv_post_k<32><<<grid, kBlock, 0, st>>>(a); break;
+        case 64: qkv_post_k<64><<<grid, kBlock, 0, st>>>(a); break;
+        case 128: qkv_post_k<128><<<grid, kBlock, 0, st>>>(a); break;
+        default: return set_error(AR_EUNSUPPORTED, "qkv_post: head_dim %lld", (long long)hd);
+    }
+    return check_launch("qkv_post");
+}
+
+int32_t ce_fused(hipStream_t st, float* loss, bf16* grad, const float* logits, const int64_t* targets, int64_t rows,
+                 int64_t V, float scale) {
+    if (V % 4 != 0) return set_error(AR_EUNSUPPORTED, "ce_fused: vocab %lld not a multiple of 4", (long long)V);
+    if (rows == 0) return AR_OK;
+    if (rows > 0x7fffffff) return set_error(AR_EINVAL, "ce_fused: too many rows");
+    const int64_t nv4 = cdiv(V, 4 * kBlock);
+    const unsigned grid = (unsigned)rows;
+    if (nv4 <= 2) ce_fused_k<2><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
+    else if (nv4 <= 4) ce_fused_k<4><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
+    else if (nv4 <= 8) ce_fused_k<8><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
+    else if (nv4 <= 16) ce_fused_k<16><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
+    else ce_fused_k<0><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
+    return check_launch("ce_fused");
+}
+
+int32_t qkv_bwd_post(hipStream_t st, bf16* gqkv, float* gve, float* ggate, const float* gq, const float* gk,
+                     const float* gv, const float* cos_t, const float* sin_t, int64_t period, const float* gate,
+                     const float* table, const int64_t* idx, int64_t nt, int64_t C, int64_t H, int64_t hd) {
+    QkvBwdArgs a{gqkv, gve, ggate, gq, gk, gv, cos_t, sin_t, gate, table, idx, nt, C, period, (int)H};
+    const unsigned grid = wave_blocks(nt * 3);
+    switch (hd) {
+        case 32: qkv_bwd_post_k<32><<<grid, kBlock, 0, st>>>(a); break;
+        case 64: qkv_bwd_post_k<64><<<grid, kBlock, 0, st>>>(a); break;
+        case 128: qkv_bwd_post_k<128><<<grid, kBlock, 0, st>>>(a); break;
+        default: return set_error(AR_EUNSUPPORTED, "qkv_bwd_post: head_dim %lld", (long long)hd);
+    }
+    return check_launch("qkv_bwd_post");
+}
+
+int32_t norm_bwd(hipStream_t st, int mode, float* gx, bf16* gxb, const float* gn, const float* x, const float* rms,
+                 const float* x0, const float* res, int64_t layer, float* g_res, float* g_x0, float* partial,
+                 int64_t rows, int64_t C) {
+    if (C % 4 != 0 || C > 256 * 16) return set_error(AR_EUNSUPPORTED, "norm_bwd: n_embd %lld", (long long)C);
+    NormBwdArgs a{gx, gxb, gn, x, rms, x0, res, partial, layer, rows, C};
+    const int nc = (int)cdiv(C, 256);
+    const unsigned grid = mode == 2 ? (unsigned)(kNormBwdWaves / (kBlock / kWave)) : wave_blocks(rows);
+#define AR_NB(NC)                                                                            \
+    do {                                                                                     \
+        if (mode == 0) norm_bwd_k<NC, 0><<<grid, kBlock, 0, st>>>(a);                        \
+        else if (mode == 1) norm_bwd_k<NC, 1><<<grid, kBlock, 0, st>>>(a);                   \
+        else norm_bwd_k<NC, 2><<<grid, kBlock, 0, st>>>(a);                                  \
+    } while (0)
+    if (nc <= 1) AR_NB(1);
+    else if (nc <= 2) AR_NB(2);
+    else if (nc <= 4) AR_NB(4);
+    else if (nc <= 8) AR_NB(8);
+    else AR_NB(16);
+#undef AR_NB
+    if (mode == 2) scalar_finish_k<<<1, kBlock, 0, st>>>(g_res, g_x0, partial, kNormBwdWaves, layer);
+    return check_launch("norm_bwd");
+}
+
+int32_t to_bf16(hipStream_t st, bf16* out, const float* in, int64_t n) {
+    if (n % 4 != 0) return set_error(AR_EINVAL, "to_bf16: size %lld not a multiple of 4", (long long)n);
+    if (n == 0) return AR_OK;
+    to_bf16_k<<<flat_grid(n / 4, kBlock * 4), kBlock, 0, st>>>(out, in, n / 4);
+    return check_launch("to_bf16");
+}
+
+int32_t precompute_d_mixed(hipStream_t st, float* d, const float* o, const bf16* g, int64_t rows, int64_t hd) {
+    if (rows == 0) return AR_OK;
+    const unsigned grid = flat_grid(cdiv(rows * hd / 4, kWave), kBlock / kWave);
+    switch (hd) {
+        case 32: precompute_d_mixed_k<8><<<grid, kBlock, 0, st>>>(d, o, g, rows); break;
+        case 64: precompute_d_mixed_k<16><<<grid, kBlock, 0, st>>>(d, o, g, rows); break;
+        case 128: precompute_d_mixed_k<32><<<grid, kBlock, 0, st>>>(d, o, g, rows); break;
+        default: return set_error(AR_EUNSUPPORTED, "precompute_d: head_dim %lld", (long long)hd);
+    }
+    return check_launch("precompute_d_mixed");
+}
+
+}  // namespace ar

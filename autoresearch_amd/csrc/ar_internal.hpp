@@ -45,9 +45,11 @@ int32_t fixed_sum(hipStream_t st, float* out, const float* a, const float* b, in
 // data /= (||data||_F * 1.02 + 1e-6); scratch: kSumBlocks + 1 floats.
 int32_t frob_normalize(hipStream_t st, float* data, int64_t n, float* scratch);
 constexpr int kGateBlocks = 256;
-// partial: kGateBlocks * n_kv_head * gate_channels floats.
+// partial: kGateBlocks * n_kv_head * gate_channels floats.  gx has row
+// stride C, xn row stride ldx.
 int32_t ve_gate_bwd(hipStream_t st, float* gx, float* gw, const float* ggate, const float* gate, const float* xn,
-                    const float* w, int64_t nt, int64_t nkv, int64_t gc, int64_t C, float* partial);
+                    const float* w, int64_t nt, int64_t nkv, int64_t gc, int64_t C, int64_t ldx, float* partial);
+constexpr int kGateMaxH = 16;
 
 // ---- attention (ar_attention.hip) ----
 enum class AttnOp { FWD, DQ, DKV };
@@ -59,6 +61,37 @@ int32_t attn_dispatch(hipStream_t st, AttnOp op, float* o1, float* o2, const TIN
 // ---- element-wise (ar_elementwise.hip) ----
 int32_t rope(hipStream_t st, float* out, const float* in, const float* cos_t, const float* sin_t, int64_t nt,
              int64_t nh, int64_t hd, int64_t period, bool inverse);
+
+// ---- fused row kernels of the bf16 step (ar_fused.hip) ----
+// mode 0: x0 = rmsnorm(table[idx]), x = sa[l] x0 + sb[l] x0; 1: x = sa[l] xin +
+// sb[l] x0; 2: x = xin.  Then rms, xn = bf16(x / rms); with gate_out also
+// xg = xn[:, :gc] (fp32) and gate = 2 sigmoid(gate_w . xg).
+int32_t resid_norm(hipStream_t st, int mode, float* x0_out, float* x_out, float* rms_out, bf16* xn_out,
+                   float* xg_out, float* gate_out, const float* xin, const float* x0, const float* table,
+                   const int64_t* idx, const float* sa, const float* sb, int64_t layer, const float* gate_w,
+                   int64_t nkv, int64_t gc, int64_t rows, int64_t C);
+// qkv [nt, 3C] fp32 -> q, k (rope + per-head rmsnorm), v (+ gate * table[idx]), bf16.
+int32_t qkv_post(hipStream_t st, bf16* q, bf16* k, bf16* v, const float* qkv, const float* cos_t, const float* sin_t,
+                 int64_t period, const float* gate, const float* table, const int64_t* idx, int64_t nt, int64_t C,
+                 int64_t H, int64_t hd);
+// loss (may be null) and bf16 grad = (softmax - onehot) * scale per row.
+int32_t ce_fused(hipStream_t st, float* loss, bf16* grad, const float* logits, const int64_t* targets, int64_t rows,
+                 int64_t V, float scale);
+// [dq | dk | dv] bf16 [nt, 3C] with inverse rope on dq, dk; with a table
+// also gve = gate * dv and ggate = per-head sum of ve * dv.
+int32_t qkv_bwd_post(hipStream_t st, bf16* gqkv, float* gve, float* ggate, const float* gq, const float* gk,
+                     const float* gv, const float* cos_t, const float* sin_t, int64_t period, const float* gate,
+                     const float* table, const int64_t* idx, int64_t nt, int64_t C, int64_t H, int64_t hd);
+// mode 0: gx = rmsnorm_bwd(gx); 1: gx += rmsnorm_bwd(gn); 2: g = gx +
+// rmsnorm_bwd(gn), g_res[l] += g.x, g_x0[l] += g.x0, gx = res[l] g.  gxb = bf16(gx).
+// partial: 2 * kNormBwdWaves floats (mode 2).
+constexpr int kNormBwdWaves = 4096;
+int32_t norm_bwd(hipStream_t st, int mode, float* gx, bf16* gxb, const float* gn, const float* x, const float* rms,
+                 const float* x0, const float* res, int64_t layer, float* g_res, float* g_x0, float* partial,
+                 int64_t rows, int64_t C);
+int32_t to_bf16(hipStream_t st, bf16* out, const float* in, int64_t n);
+// D = rowsum(O * dO), dO stored as bf16.
+int32_t precompute_d_mixed(hipStream_t st, float* d, const float* o, const bf16* g, int64_t rows, int64_t hd);
 
 // ---- Muon (ar_optim.hip) ----
 constexpr int kMuonMaxGroup = 48;

@@ -13,6 +13,15 @@
 //   * the token-id sort used by the deterministic embedding scatter is done
 //     once per backward and shared by the wte and value-embedding scatters;
 //   * all reductions are deterministic (fixed order, no float atomics).
+//
+// Precision AR_PREC_BF16 runs the bf16 step (forward_bf16 / backward_bf16):
+// GEMM and attention operands are stored as bf16 (a bf16 shadow of the
+// weights is refreshed at every forward), c_q / c_k / c_v run as one
+// [3C, C] GEMM (they are adjacent in the parameter arena), the residual add,
+// ReLU^2 and softcap are GEMM epilogues and the remaining element-wise steps
+// are the fused row kernels of ar_fused.hip.  The reference's operation order
+// and quirks are kept; only where each bf16 rounding happens moves (to the
+// producer instead of each consumer).
 #include <math.h>
 #include <stdio.h>
 #include <string.h>
@@ -39,6 +48,12 @@ struct LayerBufs {
     float *x, *xn_attn, *q, *k, *v, *lse, *attn_out, *xn_mlp, *mlp_hidden, *mlp_act, *rms_attn, *rms_mlp, *ve, *gate;
 };
 
+// Saved activations of one layer in the bf16 step.
+struct LayerBufsB {
+    float *x, *lse, *attn_out, *rms_attn, *rms_mlp, *gate, *xg;
+    ar::bf16 *xn, *q, *k, *v, *xn_mlp, *h, *act;
+};
+
 }  // namespace
 
 struct ar_gpt {
@@ -59,6 +74,14 @@ struct ar_gpt {
     // gradients of activations
     float *grad_x, *grad_x0, *grad_logits, *grad_attn_out, *grad_q, *grad_k, *grad_v, *grad_x_norm, *grad_tmp,
         *grad_mlp, *grad_ve, *grad_gate;
+    // bf16 step
+    ar::bf16* wb = nullptr;  // bf16 shadow of the parameter arena (same offsets)
+    std::vector<LayerBufsB> LB;
+    float* qkv = nullptr;  // [BT, 3C] q | k | v GEMM output
+    ar::bf16 *x_final_b = nullptr, *grad_logits_b = nullptr, *grad_xb = nullptr, *grad_h = nullptr,
+         *grad_attn_out_b = nullptr, *grad_qkv = nullptr;
+    float grad_logits_scale = 0.f;  // loss_scale baked into grad_logits_b
+    bool grad_logits_valid = false;
     // scratch (sequential users on one stream)
     float* scratch = nullptr;
     int64_t scratch_elems = 0;
@@ -108,6 +131,7 @@ int64_t add_tensor(ar_gpt* m, int64_t rows, int64_t cols, const std::string& nm)
 
 inline float* P(ar_gpt* m, int64_t i) { return m->params + m->t[i].offset; }
 inline float* G(ar_gpt* m, int64_t i) { return m->grads + m->t[i].offset; }
+inline const bf16* Wb(ar_gpt* m, int64_t i) { return m->wb + m->t[i].offset; }
 
 inline ar_stream_t AS(ar_gpt* m) { return reinterpret_cast<ar_stream_t>(m->st); }
 
@@ -161,14 +185,16 @@ double attn_keys(const ar_gpt* m, int64_t ws) {
     }
     return keys;
 }
-int32_t attention(ar_gpt* m, AttnOp op, float* o1, float* o2, const float* q, const float* k, const float* v,
-                  const float* dout, const float* lse, const float* dbuf, int64_t ws) {
+// fp32 operands: the fp32 step; bf16 operands: the bf16 step.
+template <typename TIN>
+int32_t attention(ar_gpt* m, AttnOp op, float* o1, float* o2, const TIN* q, const TIN* k, const TIN* v,
+                  const TIN* dout, const float* lse, const float* dbuf, int64_t ws) {
     const ar_gpt_config& c = m->c;
     const int e = prof_begin(m);
     int32_t r;
-    if (m->bf16)
-        r = attn_dispatch<true, float>(m->st, op, o1, o2, q, k, v, dout, lse, dbuf, m->B, m->T, c.n_head, c.head_dim,
-                                       ws);
+    if constexpr (sizeof(TIN) == 2)
+        r = attn_dispatch<true, bf16>(m->st, op, o1, o2, q, k, v, dout, lse, dbuf, m->B, m->T, c.n_head, c.head_dim,
+                                      ws);
     else
         r = attn_dispatch<false, float>(m->st, op, o1, o2, q, k, v, dout, lse, dbuf, m->B, m->T, c.n_head,
                                         c.head_dim, ws);
@@ -177,6 +203,22 @@ int32_t attention(ar_gpt* m, AttnOp op, float* o1, float* o2, const float* q, co
         const int cls = op == AttnOp::FWD ? 3 : (op == AttnOp::DQ ? 4 : 5);
         prof_end(m, e, cls, unit * (op == AttnOp::FWD ? 2.0 : (op == AttnOp::DQ ? 3.0 : 4.0)));
     }
+    return r;
+}
+// bf16-step GEMMs (operand storage per flag; profiling class cls).
+int32_t gemm_b(ar_gpt* m, int cls, int layout, void* C, bool cb, const void* X, bool xb, const void* W, bool wb,
+               int64_t M, int64_t N, int64_t K, bool accumulate) {
+    const int e = prof_begin(m);
+    const int32_t r = gemm_bf16io(m->st, layout, C, cb, X, xb, W, wb, M, N, K, accumulate, layout == 2 ? 0 : 1,
+                                  m->scratch);
+    prof_end(m, e, cls, 2.0 * M * N * K);
+    return r;
+}
+int32_t gemm_e(ar_gpt* m, int cls, int layout, int epi, void* C, bool cb, const void* X, bool xb, const bf16* W,
+               int64_t M, int64_t N, int64_t K, const void* aux, void* aux_out, float cap) {
+    const int e = prof_begin(m);
+    const int32_t r = gemm_epilogue(m->st, layout, epi, C, cb, X, xb, W, 1, M, N, K, aux, aux_out, cap);
+    prof_end(m, e, cls, 2.0 * M * N * K);
     return r;
 }
 int32_t rope_model(ar_gpt* m, float* x, bool inverse) {
@@ -230,56 +272,91 @@ static int32_t gpt_build(ar_gpt* m) {
     FALLOC(m->rope_cos, m->rope_rows * half);
     FALLOC(m->rope_sin, m->rope_rows * half);
 
+    // shared by both steps
     FALLOC(m->x0, BT * C);
     FALLOC(m->x, BT * C);
-    FALLOC(m->rms_qk, BT * H);
-    FALLOC(m->proj_out, BT * C);
-    FALLOC(m->mlp_out, BT * C);
     FALLOC(m->logits, BT * V);
     FALLOC(m->loss, BT);
     FALLOC(m->mean_loss, 64);
-    FALLOC(m->x_final, BT * C);
     FALLOC(m->rms_final, BT);
     FALLOC(m->d_buf, BT * H);
-    m->L.resize(Lr);
-    for (int64_t i = 0; i < Lr; ++i) {
-        LayerBufs& b = m->L[i];
-        FALLOC(b.x, BT * C);
-        FALLOC(b.xn_attn, BT * C);
-        FALLOC(b.q, BT * C);
-        FALLOC(b.k, BT * kv);
-        FALLOC(b.v, BT * kv);
-        FALLOC(b.lse, BT * H);
-        FALLOC(b.attn_out, BT * C);
-        FALLOC(b.xn_mlp, BT * C);
-        FALLOC(b.mlp_hidden, BT * F);
-        FALLOC(b.mlp_act, BT * F);
-        FALLOC(b.rms_attn, BT);
-        FALLOC(b.rms_mlp, BT);
-        if (has_ve(c, i)) {
-            FALLOC(b.ve, BT * kv);
-            FALLOC(b.gate, BT * H);
-        } else {
-            b.ve = b.gate = nullptr;
-        }
-    }
     FALLOC(m->grad_x, BT * C);
-    FALLOC(m->grad_x0, BT * C);
-    FALLOC(m->grad_logits, BT * V);
-    FALLOC(m->grad_attn_out, BT * C);
+    FALLOC(m->grad_x_norm, BT * C);
     FALLOC(m->grad_q, BT * C);
     FALLOC(m->grad_k, BT * kv);
     FALLOC(m->grad_v, BT * kv);
-    FALLOC(m->grad_x_norm, BT * C);
-    FALLOC(m->grad_tmp, BT * C);
-    FALLOC(m->grad_mlp, BT * F);
     FALLOC(m->grad_ve, BT * kv);
     FALLOC(m->grad_gate, BT * H);
+    auto balloc = [&](bf16** p, int64_t n) { return dalloc(m, (void**)p, (size_t)n * sizeof(bf16)); };
+    if (m->bf16) {
+        AR_TRY(balloc(&m->wb, m->nparams));
+        m->LB.resize(Lr);
+        for (int64_t i = 0; i < Lr; ++i) {
+            LayerBufsB& b = m->LB[i];
+            FALLOC(b.x, BT * C);
+            FALLOC(b.lse, BT * H);
+            FALLOC(b.attn_out, BT * C);
+            FALLOC(b.rms_attn, BT);
+            FALLOC(b.rms_mlp, BT);
+            AR_TRY(balloc(&b.xn, BT * C));
+            AR_TRY(balloc(&b.q, BT * C));
+            AR_TRY(balloc(&b.k, BT * kv));
+            AR_TRY(balloc(&b.v, BT * kv));
+            AR_TRY(balloc(&b.xn_mlp, BT * C));
+            AR_TRY(balloc(&b.h, BT * F));
+            AR_TRY(balloc(&b.act, BT * F));
+            if (has_ve(c, i)) {
+                FALLOC(b.gate, BT * H);
+                FALLOC(b.xg, BT * kGateChannels);
+            } else {
+                b.gate = b.xg = nullptr;
+            }
+        }
+        FALLOC(m->qkv, BT * 3 * C);
+        AR_TRY(balloc(&m->x_final_b, BT * C));
+        AR_TRY(balloc(&m->grad_logits_b, BT * V));
+        AR_TRY(balloc(&m->grad_xb, BT * C));
+        AR_TRY(balloc(&m->grad_h, BT * F));
+        AR_TRY(balloc(&m->grad_attn_out_b, BT * C));
+        AR_TRY(balloc(&m->grad_qkv, BT * 3 * C));
+    } else {
+        FALLOC(m->rms_qk, BT * H);
+        FALLOC(m->proj_out, BT * C);
+        FALLOC(m->mlp_out, BT * C);
+        FALLOC(m->x_final, BT * C);
+        m->L.resize(Lr);
+        for (int64_t i = 0; i < Lr; ++i) {
+            LayerBufs& b = m->L[i];
+            FALLOC(b.x, BT * C);
+            FALLOC(b.xn_attn, BT * C);
+            FALLOC(b.q, BT * C);
+            FALLOC(b.k, BT * kv);
+            FALLOC(b.v, BT * kv);
+            FALLOC(b.lse, BT * H);
+            FALLOC(b.attn_out, BT * C);
+            FALLOC(b.xn_mlp, BT * C);
+            FALLOC(b.mlp_hidden, BT * F);
+            FALLOC(b.mlp_act, BT * F);
+            FALLOC(b.rms_attn, BT);
+            FALLOC(b.rms_mlp, BT);
+            if (has_ve(c, i)) {
+                FALLOC(b.ve, BT * kv);
+                FALLOC(b.gate, BT * H);
+            } else {
+                b.ve = b.gate = nullptr;
+            }
+        }
+        FALLOC(m->grad_x0, BT * C);
+        FALLOC(m->grad_logits, BT * V);
+        FALLOC(m->grad_attn_out, BT * C);
+        FALLOC(m->grad_tmp, BT * C);
+        FALLOC(m->grad_mlp, BT * F);
+    }
 
     // Scratch: the largest of every sequential user.
     int64_t need = kSumBlocks + 64;
     auto upd = [&](int64_t n) { if (n > need) need = n; };
-    const int64_t dw_shapes[][2] = {{C, C}, {kv, C}, {F, C}, {C, F}, {V, C}};
+    const int64_t dw_shapes[][2] = {{C, C}, {kv, C}, {F, C}, {C, F}, {V, C}, {3 * C, C}};
     for (auto& s : dw_shapes)
         upd(gemm_partial_elems(2, BT, s[0], s[1], gemm_auto_splits(2, m->bf16, BT, s[0], s[1])));
     const int64_t groups = (4 * Lr + kMuonMaxGroup - 1) / kMuonMaxGroup;
@@ -289,6 +366,7 @@ static int32_t gpt_build(ar_gpt* m) {
     upd(muon_scratch_elems(C, F, m->bf16, Lr < kMuonMaxGroup ? Lr : kMuonMaxGroup));
     upd(BT * (C > kv ? C : kv));                  // embedding scatter partials
     upd((int64_t)kGateBlocks * H * kGateChannels);  // ve gate partials
+    upd(2 * (int64_t)kNormBwdWaves);                // learned-scalar gradient partials
     m->scratch_elems = need;
     FALLOC(m->scratch, need);
     int bits = 1;
@@ -313,6 +391,8 @@ extern "C" int32_t ar_gpt_create(ar_gpt** out, const ar_gpt_config* cfg, int64_t
     AR_CHECK_ARG(c.n_embd % 8 == 0 && c.vocab_size % 8 == 0 && (B * T) % 8 == 0,
                  "gpt_create: n_embd, vocab_size and B*T must be multiples of 8");
     AR_CHECK_ARG(c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128, "gpt_create: head_dim must be 32/64/128");
+    AR_CHECK_ARG(c.n_head <= kGateMaxH, "gpt_create: n_head must be <= %d (value-embedding gate)", kGateMaxH);
+    AR_CHECK_ARG(c.n_embd <= 4096, "gpt_create: n_embd must be <= 4096");
     AR_CHECK_ARG(precision == AR_PREC_FP32 || precision == AR_PREC_BF16, "gpt_create: bad precision");
     AR_CHECK_ARG(rope_period >= 0, "gpt_create: bad rope_period");
     ar_gpt* m = new ar_gpt();
@@ -385,9 +465,120 @@ extern "C" int32_t ar_gpt_init_weights(ar_gpt* m, uint64_t seed0) {
 // model.mojo:777-814
 extern "C" int32_t ar_gpt_zero_grads(ar_gpt* m) { return ar_zero_buffer(AS(m), m->grads, m->nparams); }
 
+// ------------------------------------------------------------------------
+// bf16 step: model.mojo:576-772 / 819-1037 with bf16 operand storage
+// ------------------------------------------------------------------------
+static int32_t forward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* targets) {
+    const ar_gpt_config& c = m->c;
+    const int64_t C = c.n_embd, V = c.vocab_size, BT = m->BT, H = c.n_head, hd = c.head_dim;
+    const int64_t F = kMlpExpansion * C;
+    hipStream_t st = m->st;
+    AR_TRY(to_bf16(st, m->wb, m->params, m->nparams));
+    for (int64_t i = 0; i < c.n_layer; ++i) {
+        LayerBufsB& b = m->LB[i];
+        const bool ve = has_ve(c, i);
+        // layer 0: x0 = norm(wte[idx]) (model.mojo:598-603); x = res*x_in + x0l*x0; xn = norm(x)
+        AR_TRY(resid_norm(st, i == 0 ? 0 : 1, m->x0, b.x, b.rms_attn, b.xn, ve ? b.xg : nullptr,
+                          ve ? b.gate : nullptr, m->x, m->x0, P(m, m->i_wte), inputs, P(m, m->i_res), P(m, m->i_x0),
+                          i, ve ? P(m, m->i_gate[i]) : nullptr, H, kGateChannels, BT, C));
+        // c_q | c_k | c_v: one [3C, C] weight
+        AR_TRY(gemm_b(m, 0, 0, m->qkv, false, b.xn, true, Wb(m, m->i_q[i]), true, BT, 3 * C, C, false));
+        AR_TRY(qkv_post(st, b.q, b.k, b.v, m->qkv, m->rope_cos, m->rope_sin, m->period, b.gate,
+                        ve ? P(m, m->i_ve[i]) : nullptr, inputs, BT, C, H, hd));
+        AR_TRY(attention<bf16>(m, AttnOp::FWD, b.attn_out, b.lse, b.q, b.k, b.v, nullptr, nullptr, nullptr,
+                               window_size(c, i)));
+        // x = x_layer + attn_out @ c_proj^T
+        AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_ADD, m->x, false, b.attn_out, false, Wb(m, m->i_proj[i]), BT, C, C, b.x,
+                      nullptr, 0.f));
+        AR_TRY(resid_norm(st, 2, nullptr, nullptr, b.rms_mlp, b.xn_mlp, nullptr, nullptr, m->x, nullptr, nullptr,
+                          nullptr, nullptr, nullptr, 0, nullptr, 0, 0, BT, C));
+        // h = xn @ c_fc^T, act = relu(h)^2; x += act @ mlp_proj^T
+        AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_RELU2, b.h, true, b.xn_mlp, true, Wb(m, m->i_fc[i]), BT, F, C, nullptr,
+                      b.act, 0.f));
+        AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_ADD, m->x, false, b.act, true, Wb(m, m->i_mlpp[i]), BT, C, F, m->x,
+                      nullptr, 0.f));
+    }
+    AR_TRY(resid_norm(st, 2, nullptr, nullptr, m->rms_final, m->x_final_b, nullptr, nullptr, m->x, nullptr, nullptr,
+                      nullptr, nullptr, nullptr, 0, nullptr, 0, 0, BT, C));
+    AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_SOFTCAP, m->logits, false, m->x_final_b, true, Wb(m, m->i_lm), BT, V, C, nullptr,
+                  nullptr, kSoftcap));
+    // loss, and the loss gradient for loss_scale 1 while the row is loaded
+    AR_TRY(ce_fused(st, m->loss, m->grad_logits_b, m->logits, targets, BT, V, 1.0f));
+    m->grad_logits_scale = 1.0f;
+    m->grad_logits_valid = true;
+    return fixed_sum(st, m->mean_loss, m->loss, nullptr, BT, 0, 0, 0, m->scratch);
+}
+
+static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* targets, float loss_scale) {
+    const ar_gpt_config& c = m->c;
+    const int64_t C = c.n_embd, V = c.vocab_size, BT = m->BT, H = c.n_head, hd = c.head_dim, kv = c.kv_dim;
+    const int64_t F = kMlpExpansion * C;
+    hipStream_t st = m->st;
+    AR_TRY(ar_embedding_sort(AS(m), m->sorted_ids, m->sorted_tok, inputs, BT, m->sort_bits, m->sort_scratch,
+                             m->sort_bytes, nullptr));
+    if (!m->grad_logits_valid || m->grad_logits_scale != loss_scale) {
+        AR_TRY(ce_fused(st, nullptr, m->grad_logits_b, m->logits, targets, BT, V, loss_scale));
+        m->grad_logits_scale = loss_scale;
+        m->grad_logits_valid = true;
+    }
+    AR_TRY(gemm_b(m, 1, 1, m->grad_x, false, m->grad_logits_b, true, Wb(m, m->i_lm), true, BT, V, C, false));
+    AR_TRY(gemm_b(m, 2, 2, G(m, m->i_lm), false, m->grad_logits_b, true, m->x_final_b, true, BT, V, C, true));
+    AR_TRY(norm_bwd(st, 0, m->grad_x, m->grad_xb, nullptr, m->x, m->rms_final, nullptr, nullptr, 0, nullptr, nullptr,
+                    nullptr, BT, C));
+    for (int64_t r = 0; r < c.n_layer; ++r) {
+        const int64_t i = c.n_layer - 1 - r;
+        LayerBufsB& b = m->LB[i];
+        const bool ve = has_ve(c, i);
+        // MLP: dh = relu2_bwd(grad_x @ mlp_proj, h)
+        AR_TRY(gemm_e(m, 1, 1, GEMM_EPI_RELU2_BWD, m->grad_h, true, m->grad_xb, true, Wb(m, m->i_mlpp[i]), BT, C, F,
+                      b.h, nullptr, 0.f));
+        AR_TRY(gemm_b(m, 2, 2, G(m, m->i_mlpp[i]), false, m->grad_xb, true, b.act, true, BT, C, F, true));
+        AR_TRY(gemm_b(m, 1, 1, m->grad_x_norm, false, m->grad_h, true, Wb(m, m->i_fc[i]), true, BT, F, C, false));
+        AR_TRY(gemm_b(m, 2, 2, G(m, m->i_fc[i]), false, m->grad_h, true, b.xn_mlp, true, BT, F, C, true));
+        AR_TRY(norm_bwd(st, 1, m->grad_x, m->grad_xb, m->grad_x_norm, b.x, b.rms_mlp, nullptr, nullptr, 0, nullptr,
+                        nullptr, nullptr, BT, C));  // Q7: saved x of the layer
+        // attention output projection
+        AR_TRY(gemm_b(m, 1, 1, m->grad_attn_out_b, true, m->grad_xb, true, Wb(m, m->i_proj[i]), true, BT, C, C,
+                      false));
+        AR_TRY(gemm_b(m, 2, 2, G(m, m->i_proj[i]), false, m->grad_xb, true, b.attn_out, false, BT, C, C, true));
+        const int64_t ws = window_size(c, i);
+        AR_TRY(precompute_d_mixed(st, m->d_buf, b.attn_out, m->grad_attn_out_b, BT * H, hd));
+        AR_TRY(attention<bf16>(m, AttnOp::DQ, m->grad_q, nullptr, b.q, b.k, b.v, m->grad_attn_out_b, b.lse, m->d_buf,
+                               ws));
+        AR_TRY(attention<bf16>(m, AttnOp::DKV, m->grad_k, m->grad_v, b.q, b.k, b.v, m->grad_attn_out_b, b.lse,
+                               m->d_buf, ws));
+        // Q6: q/k per-head norm backward skipped; rope_bwd, ve_apply_bwd, pack [dq | dk | dv]
+        AR_TRY(qkv_bwd_post(st, m->grad_qkv, m->grad_ve, m->grad_gate, m->grad_q, m->grad_k, m->grad_v, m->rope_cos,
+                            m->rope_sin, m->period, b.gate, ve ? P(m, m->i_ve[i]) : nullptr, inputs, BT, C, H, hd));
+        if (ve)
+            AR_TRY(ar_embedding_bwd_sorted(AS(m), G(m, m->i_ve[i]), m->grad_ve, m->sorted_ids, m->sorted_tok, BT, kv,
+                                           m->scratch));
+        AR_TRY(gemm_b(m, 1, 1, m->grad_x_norm, false, m->grad_qkv, true, Wb(m, m->i_q[i]), true, BT, 3 * C, C,
+                      false));
+        AR_TRY(gemm_b(m, 2, 2, G(m, m->i_q[i]), false, m->grad_qkv, true, b.xn, true, BT, 3 * C, C, true));
+        if (ve)
+            AR_TRY(ve_gate_bwd(st, m->grad_x_norm, G(m, m->i_gate[i]), m->grad_gate, b.gate, b.xg,
+                               P(m, m->i_gate[i]), BT, H, kGateChannels, C, kGateChannels, m->scratch));
+        // grad_x = res[i] * (grad_x + rmsnorm_bwd(.)), with the Q8 scalar dots (Q9: grad_x0 unused)
+        AR_TRY(norm_bwd(st, 2, m->grad_x, m->grad_xb, m->grad_x_norm, b.x, b.rms_attn, m->x0, P(m, m->i_res), i,
+                        G(m, m->i_res), G(m, m->i_x0), m->scratch, BT, C));
+    }
+    // Q10: embedding norm backward skipped
+    return ar_embedding_bwd_sorted(AS(m), G(m, m->i_wte), m->grad_x, m->sorted_ids, m->sorted_tok, BT, C, m->scratch);
+}
+
 // model.mojo:576-772
 extern "C" int32_t ar_gpt_forward(ar_gpt* m, const int64_t* inputs, const int64_t* targets, float* loss_host) {
     AR_CHECK_ARG(m && inputs && targets, "gpt_forward: null pointer");
+    if (m->bf16) {
+        AR_TRY(forward_bf16(m, inputs, targets));
+        if (loss_host) {
+            if (hipMemcpyAsync(loss_host, m->mean_loss, sizeof(float), hipMemcpyDeviceToHost, m->st) != hipSuccess ||
+                hipStreamSynchronize(m->st) != hipSuccess)
+                return set_error(AR_EHIP, "gpt_forward: loss copy failed");
+        }
+        return AR_OK;
+    }
     const ar_gpt_config& c = m->c;
     const int64_t C = c.n_embd, V = c.vocab_size, BT = m->BT, H = c.n_head, hd = c.head_dim;
     const int64_t kv = c.kv_dim, F = kMlpExpansion * C;
@@ -411,7 +602,7 @@ extern "C" int32_t ar_gpt_forward(ar_gpt* m, const int64_t* inputs, const int64_
         AR_TRY(rope_model(m, b.k, false));
         AR_TRY(ar_rmsnorm_fwd(st, b.q, m->rms_qk, b.q, BT * H, hd));
         AR_TRY(ar_rmsnorm_fwd(st, b.k, m->rms_qk, b.k, BT * H, hd));
-        AR_TRY(attention(m, AttnOp::FWD, b.attn_out, b.lse, b.q, b.k, b.v, nullptr, nullptr, nullptr,
+        AR_TRY(attention<float>(m, AttnOp::FWD, b.attn_out, b.lse, b.q, b.k, b.v, nullptr, nullptr, nullptr,
                          window_size(c, i)));
         AR_TRY(linear(m, m->proj_out, b.attn_out, P(m, m->i_proj[i]), BT, C, C));
         AR_TRY(ar_add_residual_fwd(st, m->x, b.x, m->proj_out, BT * C));
@@ -438,6 +629,7 @@ extern "C" int32_t ar_gpt_forward(ar_gpt* m, const int64_t* inputs, const int64_
 // model.mojo:819-1037 (quirks Q4-Q10 of the reference backward reproduced)
 extern "C" int32_t ar_gpt_backward(ar_gpt* m, const int64_t* inputs, const int64_t* targets, float loss_scale) {
     AR_CHECK_ARG(m && inputs && targets, "gpt_backward: null pointer");
+    if (m->bf16) return backward_bf16(m, inputs, targets, loss_scale);
     const ar_gpt_config& c = m->c;
     const int64_t C = c.n_embd, V = c.vocab_size, BT = m->BT, H = c.n_head, hd = c.head_dim;
     const int64_t kv = c.kv_dim, F = kMlpExpansion * C;
@@ -463,12 +655,9 @@ extern "C" int32_t ar_gpt_backward(ar_gpt* m, const int64_t* inputs, const int64
         AR_TRY(linear_dx(m, m->grad_attn_out, m->grad_x, P(m, m->i_proj[i]), BT, C, C));
         AR_TRY(linear_dw(m, G(m, m->i_proj[i]), m->grad_x, b.attn_out, BT, C, C));
         const int64_t ws = window_size(c, i);
-        if (m->bf16)
-            AR_TRY(ar_flash_attn_bwd_precompute_d_bf16(st, m->d_buf, b.attn_out, m->grad_attn_out, m->B, m->T, H, hd));
-        else
-            AR_TRY(ar_flash_attn_bwd_precompute_d(st, m->d_buf, b.attn_out, m->grad_attn_out, m->B, m->T, H, hd));
-        AR_TRY(attention(m, AttnOp::DQ, m->grad_q, nullptr, b.q, b.k, b.v, m->grad_attn_out, b.lse, m->d_buf, ws));
-        AR_TRY(attention(m, AttnOp::DKV, m->grad_k, m->grad_v, b.q, b.k, b.v, m->grad_attn_out, b.lse, m->d_buf,
+        AR_TRY(ar_flash_attn_bwd_precompute_d(st, m->d_buf, b.attn_out, m->grad_attn_out, m->B, m->T, H, hd));
+        AR_TRY(attention<float>(m, AttnOp::DQ, m->grad_q, nullptr, b.q, b.k, b.v, m->grad_attn_out, b.lse, m->d_buf, ws));
+        AR_TRY(attention<float>(m, AttnOp::DKV, m->grad_k, m->grad_v, b.q, b.k, b.v, m->grad_attn_out, b.lse, m->d_buf,
                          ws));
         // Q6: q/k per-head norm backward skipped
         if (has_ve(c, i)) {
@@ -488,7 +677,7 @@ extern "C" int32_t ar_gpt_backward(ar_gpt* m, const int64_t* inputs, const int64
         AR_TRY(linear_dw(m, G(m, m->i_v[i]), m->grad_v, b.xn_attn, BT, kv, C));
         if (has_ve(c, i))
             AR_TRY(ve_gate_bwd(m->st, m->grad_x_norm, G(m, m->i_gate[i]), m->grad_gate, b.gate, b.xn_attn,
-                               P(m, m->i_gate[i]), BT, H, kGateChannels, C, m->scratch));
+                               P(m, m->i_gate[i]), BT, H, kGateChannels, C, C, m->scratch));
         AR_TRY(ar_rmsnorm_bwd(st, m->grad_x_norm, m->grad_x_norm, b.x, b.rms_attn, BT, C));
         AR_TRY(ar_add_residual_fwd(st, m->grad_x, m->grad_x, m->grad_x_norm, BT * C));
         // Q8: post-scaled-add saved x; Q9: grad_x0 assigned and never consumed

@@ -116,7 +116,7 @@ __global__ void ce_fwd_k(float* loss, const float* logits, const int64_t* target
     if (threadIdx.x == 0) {
         const int64_t tg = targets[t];
         const float lse = m + logf(s);
-        loss[t] = tg >= 0 ? -row[tg] + lse : 0.f;
+        loss[t] = (tg >= 0 && tg < V) ? -row[tg] + lse : 0.f;  // out-of-range targets are ignored rows
     }
 }
 
@@ -126,7 +126,7 @@ __global__ void ce_bwd_k(float* grad, const float* logits, const int64_t* target
     const int64_t t = blockIdx.x;
     const int64_t tg = targets[t];
     float* g = grad + t * V;
-    if (tg < 0) {
+    if (tg < 0 || tg >= V) {
         for (int64_t i = threadIdx.x; i < V; i += blockDim.x) g[i] = 0.f;
         return;
     }
@@ -240,11 +240,9 @@ __global__ void ve_apply_bwd_k(float* gve, float* ggate, const float* gv, const 
 // Block b owns a fixed token range.  Thread (c = tid % 64, j = tid / 64):
 // gx[t,c] += sum_h dz[t,h] W[h,c] for its tokens (no conflicts), and a
 // per-block partial of gW[h,c] = sum_t dz[t,h] x[t,c] reduced over j in LDS.
-constexpr int kGateMaxH = 16;
-
 __global__ void ve_gate_bwd_partial_k(float* gx, float* partial, const float* ggate, const float* gate,
                                       const float* xn, const float* w, int64_t nt, int64_t nkv, int64_t gc,
-                                      int64_t C) {
+                                      int64_t C, int64_t ldx) {
     __shared__ float acc_s[4][kGateMaxH][64];
     const int c = threadIdx.x % 64, j = threadIdx.x / 64;
     const int64_t per = (nt + gridDim.x - 1) / gridDim.x;
@@ -254,7 +252,7 @@ __global__ void ve_gate_bwd_partial_k(float* gx, float* partial, const float* gg
     for (int h = 0; h < kGateMaxH; ++h) accw[h] = 0.f;
     if (c < gc) {
         for (int64_t t = t0 + j; t < t1; t += 4) {
-            const float x = xn[t * C + c];
+            const float x = xn[t * ldx + c];
             float ax = 0.f;
             for (int64_t h = 0; h < nkv; ++h) {
                 const float g = gate[t * nkv + h];
@@ -448,9 +446,9 @@ int32_t frob_normalize(hipStream_t st, float* data, int64_t n, float* scratch) {
 }
 
 int32_t ve_gate_bwd(hipStream_t st, float* gx, float* gw, const float* ggate, const float* gate, const float* xn,
-                    const float* w, int64_t nt, int64_t nkv, int64_t gc, int64_t C, float* partial) {
+                    const float* w, int64_t nt, int64_t nkv, int64_t gc, int64_t C, int64_t ldx, float* partial) {
     if (nt == 0) return AR_OK;
-    ve_gate_bwd_partial_k<<<kGateBlocks, 256, 0, st>>>(gx, partial, ggate, gate, xn, w, nt, nkv, gc, C);
+    ve_gate_bwd_partial_k<<<kGateBlocks, 256, 0, st>>>(gx, partial, ggate, gate, xn, w, nt, nkv, gc, C, ldx);
     ve_gate_bwd_finish_k<<<1, 256, 0, st>>>(gw, partial, kGateBlocks, nkv * gc);
     return check_launch("ve_gate_bwd");
 }
@@ -546,7 +544,7 @@ extern "C" int32_t ar_ve_gate_bwd(ar_stream_t stream, float* grad_x_norm_out, fl
     float* partial = (float*)workspace((size_t)kGateBlocks * n * sizeof(float), &st);
     if (!partial) return st;
     return ar::ve_gate_bwd(S(stream), grad_x_norm_out, grad_gate_weight, grad_gate, gate, x_norm, gate_weight,
-                           num_tokens, n_kv_head, gate_channels, embd_dim, partial);
+                           num_tokens, n_kv_head, gate_channels, embd_dim, embd_dim, partial);
 }
 
 // Sort workspace layout: keys, keys_sorted, vals, vals_sorted (n each), flag,

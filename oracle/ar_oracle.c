@@ -342,7 +342,7 @@ void orc_cross_entropy_fwd(float* loss, const float* logits, const int64_t* targ
         for (int64_t i = 0; i < V; ++i) s += exp((double)(row[i] - mx));
         float lse = mx + (float)log(s);
         int64_t tg = targets[t];
-        loss[t] = tg >= 0 ? -row[tg] + lse : 0.0f;
+        loss[t] = (tg >= 0 && tg < V) ? -row[tg] + lse : 0.0f;  /* tg >= V: ignored (the reference reads out of bounds) */
     }
 }
 
@@ -363,7 +363,7 @@ void orc_cross_entropy_softcap_bwd(float* grad, const float* logits, const int64
         const float* row = logits + t * V;
         float* g = grad + t * V;
         int64_t tg = targets[t];
-        if (tg < 0) {
+        if (tg < 0 || tg >= V) {
             for (int64_t i = 0; i < V; ++i) g[i] = 0.0f;
             continue;
         }
