@@ -591,13 +591,34 @@ extern "C" int32_t ar_flash_attn_fwd(ar_stream_t stream, float* output, float* l
     return ar::attn_dispatch<false, float>(S(stream), ar::AttnOp::FWD, output, lse_out, q, k, v, nullptr, nullptr,
                                            nullptr, B, T, num_heads, head_dim, window_size);
 }
+// bf16 compute: operands rounded to bf16 once (into the library workspace),
+// then the bf16-operand kernels of ar_flash.hip.
+namespace {
+int32_t to_bf16_ws(ar_stream_t stream, const float* const* src, int n, int64_t elems, ar::bf16** dst) {
+    int32_t st;
+    ar::bf16* w = (ar::bf16*)ar::workspace((size_t)n * (size_t)elems * sizeof(ar::bf16), &st);
+    if (!w) return st;
+    for (int i = 0; i < n; ++i) {
+        dst[i] = w + (int64_t)i * elems;
+        const int32_t r = ar::to_bf16(S(stream), dst[i], src[i], elems);
+        if (r) return r;
+    }
+    return AR_OK;
+}
+}  // namespace
+
 extern "C" int32_t ar_flash_attn_fwd_bf16(ar_stream_t stream, float* output, float* lse_out, const float* q,
                                           const float* k, const float* v, int64_t B, int64_t T, int64_t num_heads,
                                           int64_t head_dim, int64_t window_size) {
     AR_ATTN_PTRS(output, q, k, v);
     AR_CHECK_ARG(lse_out != nullptr, "flash_attn_fwd_bf16: null lse");
-    return ar::attn_dispatch<true, float>(S(stream), ar::AttnOp::FWD, output, lse_out, q, k, v, nullptr, nullptr,
-                                          nullptr, B, T, num_heads, head_dim, window_size);
+    AR_CHECK_ARG(B >= 0 && T >= 0 && num_heads >= 0 && head_dim % 32 == 0, "flash_attn_fwd_bf16: bad shape");
+    const float* src[3] = {q, k, v};
+    ar::bf16* b[3];
+    int32_t r = to_bf16_ws(stream, src, 3, B * T * num_heads * head_dim, b);
+    if (r) return r;
+    return ar::flash_attn_bf16(S(stream), ar::AttnOp::FWD, output, lse_out, nullptr, b[0], b[1], b[2], nullptr,
+                               nullptr, nullptr, B, T, num_heads, head_dim, window_size);
 }
 extern "C" int32_t ar_flash_attn_bwd_dq(ar_stream_t stream, float* grad_q, const float* q, const float* k,
                                         const float* v, const float* grad_output, const float* lse, const float* d_buf,
@@ -614,8 +635,13 @@ extern "C" int32_t ar_flash_attn_bwd_dq_bf16(ar_stream_t stream, float* grad_q, 
                                              int64_t head_dim, int64_t window_size) {
     AR_ATTN_PTRS(grad_q, q, k, v, grad_output);
     AR_CHECK_ARG(lse && d_buf, "flash_attn_bwd_dq_bf16: null lse / d_buf");
-    return ar::attn_dispatch<true, float>(S(stream), ar::AttnOp::DQ, grad_q, nullptr, q, k, v, grad_output, lse,
-                                          d_buf, B, T, num_heads, head_dim, window_size);
+    AR_CHECK_ARG(B >= 0 && T >= 0 && num_heads >= 0 && head_dim % 32 == 0, "flash_attn_bwd_dq_bf16: bad shape");
+    const float* src[4] = {q, k, v, grad_output};
+    ar::bf16* b[4];
+    int32_t r = to_bf16_ws(stream, src, 4, B * T * num_heads * head_dim, b);
+    if (r) return r;
+    return ar::flash_attn_bf16(S(stream), ar::AttnOp::DQ, grad_q, nullptr, nullptr, b[0], b[1], b[2], b[3], lse,
+                               d_buf, B, T, num_heads, head_dim, window_size);
 }
 extern "C" int32_t ar_flash_attn_bwd_dkv(ar_stream_t stream, float* grad_k, float* grad_v, const float* q,
                                          const float* k, const float* v, const float* grad_output, const float* lse,
@@ -632,16 +658,15 @@ extern "C" int32_t ar_flash_attn_bwd_dkv_bf16(ar_stream_t stream, float* grad_k,
                                               int64_t num_heads, int64_t head_dim, int64_t window_size) {
     AR_ATTN_PTRS(grad_k, grad_v, q, k, v, grad_output);
     AR_CHECK_ARG(lse && d_buf, "flash_attn_bwd_dkv_bf16: null lse / d_buf");
-    return ar::attn_dispatch<true, float>(S(stream), ar::AttnOp::DKV, grad_k, grad_v, q, k, v, grad_output, lse,
-                                          d_buf, B, T, num_heads, head_dim, window_size);
+    AR_CHECK_ARG(B >= 0 && T >= 0 && num_heads >= 0 && head_dim % 32 == 0, "flash_attn_bwd_dkv_bf16: bad shape");
+    const float* src[4] = {q, k, v, grad_output};
+    ar::bf16* b[4];
+    int32_t r = to_bf16_ws(stream, src, 4, B * T * num_heads * head_dim, b);
+    if (r) return r;
+    return ar::flash_attn_bf16(S(stream), ar::AttnOp::DKV, grad_k, grad_v, nullptr, b[0], b[1], b[2], b[3], lse,
+                               d_buf, B, T, num_heads, head_dim, window_size);
 }
 
 template int32_t ar::attn_dispatch<false, float>(hipStream_t, ar::AttnOp, float*, float*, const float*, const float*,
                                                  const float*, const float*, const float*, const float*, int64_t,
                                                  int64_t, int64_t, int64_t, int64_t);
-template int32_t ar::attn_dispatch<true, float>(hipStream_t, ar::AttnOp, float*, float*, const float*, const float*,
-                                                const float*, const float*, const float*, const float*, int64_t,
-                                                int64_t, int64_t, int64_t, int64_t);
-template int32_t ar::attn_dispatch<true, ar::bf16>(hipStream_t, ar::AttnOp, float*, float*, const ar::bf16*,
-                                                   const ar::bf16*, const ar::bf16*, const ar::bf16*, const float*,
-                                                   const float*, int64_t, int64_t, int64_t, int64_t, int64_t);

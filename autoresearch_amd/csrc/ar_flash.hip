@@ -1,0 +1,574 @@
+// ar_flash.hip -- flash attention for bf16-stored operands (the bf16 step):
+// forward (ops.mojo:244-323), dQ (ops.mojo:349-411) and dK/dV
+// (ops.mojo:414-480), same math and work split as ar_attention.hip, with the
+// data movement rebuilt around two gfx950 features:
+//
+//   * Natural tiles only.  Every streamed 64-row tile (K, V, Q, dO) sits in
+//     LDS in its natural [row][d] layout, 16-byte chunks XOR-swizzled per row
+//     (physical chunk = logical chunk ^ swz(row)).  Operands that the MFMA
+//     needs with the row index contiguous (V^T for O^T += V^T P^T, K^T for
+//     dQ, Q^T / dO^T for dK / dV) are read with ds_read_b64_tr_b16: inside
+//     each group of 16 lanes, lane 4k+q supplies the address of row k,
+//     columns 4q..4q+3, and lane i receives rows 0..3 of column i.  Two such
+//     reads give a lane the 8 rows {16s + 4g + 0..3, 16s + 8 + 4g + 0..3}
+//     (g = lane / 32) that the accumulator-fed B operand holds, so no
+//     transposed LDS copy is ever written.
+//   * swz(r) = 4 (r mod 4) + (r / 4) mod 4 (mod chunks per row) keeps both
+//     access patterns spread over the banks: 16 consecutive rows read at one
+//     logical chunk hit 16 different chunks (row fragments), and 4
+//     consecutive rows x 4 consecutive chunks hit 16 different chunks
+//     (transposed reads).
+//   * Double-buffered tiles: the next tile's global loads are issued into
+//     registers before the current tile's MFMAs and written to the other LDS
+//     stage after them (one barrier per tile).
+//   * Blocks of one (batch, head) run on one XCD (K / V stay in its L2), and
+//     the causal work is issued heavy-first.
+//
+// Layout: q, k, v, dO [B, T, H, hd] bf16 (row stride H*hd); O, dQ, dK, dV
+// fp32 (plus an optional bf16 copy of O); LSE, D [B, T, H] fp32.
+#include "ar_internal.hpp"
+
+namespace ar {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kOwn = 128;  // rows owned by a workgroup (4 waves x 32)
+constexpr int kTile = 64;  // rows per streamed tile
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+__device__ __forceinline__ int acc_row(int v, int lane) { return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); }
+
+template <int HD>
+struct Geo {
+    static constexpr int NCH = HD / 8;            // 16-byte chunks per row
+    static constexpr int TILE = kTile * HD;       // bf16 elements per tile
+    static constexpr int PER = TILE / 8 / kThreads;  // chunks per thread per tile
+    static constexpr int KSTEPS = HD / 16;
+    static constexpr int DT = HD / 32;
+    __device__ static int swz(int r) { return (4 * (r & 3) + ((r >> 2) & 3)) & (NCH - 1); }
+    // element offset of logical (row, chunk) + e (e < 8) in a tile
+    __device__ static int off(int r, int c) { return r * HD + ((c ^ swz(r)) << 3); }
+};
+
+__device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Row fragment: row r, k-step ks (lane holds d = 16 ks + 8 (lane / 32) .. +8).
+template <int HD>
+__device__ __forceinline__ bf16x8 rowfrag(const bf16* tile, int r, int ks, int lane) {
+    return *reinterpret_cast<const bf16x8*>(tile + Geo<HD>::off(r, 2 * ks + (lane >> 5)));
+}
+
+// Transposed fragment of a natural tile for 32-row block rb, k-step s and
+// column block ct: lane l gets column 32 ct + l % 32, rows
+// {32 rb + 16 s + 4 g + 0..3, 32 rb + 16 s + 8 + 4 g + 0..3}, g = l / 32.
+template <int HD>
+__device__ __forceinline__ bf16x8 trfrag(const bf16* tile, int rb, int s, int ct, int lane) {
+    const int g = lane >> 4, src = lane & 15;
+    const int row = 32 * rb + 16 * s + 4 * (g >> 1) + (src >> 2);
+    const int col = 32 * ct + 16 * (g & 1) + 4 * (src & 3);
+    const bf16* p0 = tile + Geo<HD>::off(row, col >> 3) + (col & 7);
+    const bf16* p1 = tile + Geo<HD>::off(row + 8, col >> 3) + (col & 7);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1));
+    const s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(bf16x8, both);
+}
+
+// B fragment (bf16x8) of the lane's own accumulator values, k-step s.
+__device__ __forceinline__ bf16x8 accfrag(const f32x16& a, int s) {
+    bf16x8 f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (bf16)a[8 * s + e];
+    return f;
+}
+// Rounding residual of accfrag (accfrag + accfrag_lo ~ 16 significant bits).
+__device__ __forceinline__ bf16x8 accfrag_lo(const f32x16& a, int s) {
+    bf16x8 f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float x = a[8 * s + e];
+        f[e] = (bf16)(x - (float)(bf16)x);
+    }
+    return f;
+}
+
+// Global -> register prefetch of one 64-row tile (rows >= T read as zero).
+template <int HD>
+struct TilePrefetch {
+    uint4 v[Geo<HD>::PER];
+    __device__ __forceinline__ void load(const bf16* base, int64_t rs, int row0, int T) {
+#pragma unroll
+        for (int i = 0; i < Geo<HD>::PER; ++i) {
+            const int id = i * kThreads + threadIdx.x;
+            const int r = id / Geo<HD>::NCH, pos = id % Geo<HD>::NCH;
+            const int c = pos ^ Geo<HD>::swz(r);
+            v[i] = row0 + r < T ? *reinterpret_cast<const uint4*>(base + (int64_t)(row0 + r) * rs + c * 8)
+                                : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    __device__ __forceinline__ void store(bf16* tile) const {
+#pragma unroll
+        for (int i = 0; i < Geo<HD>::PER; ++i) {
+            const int id = i * kThreads + threadIdx.x;
+            *reinterpret_cast<uint4*>(tile + id * 8) = v[i];  // physical chunk order
+        }
+    }
+};
+
+// B fragments of 32 own rows (row = row0 + lane % 32), read from global.
+template <int HD>
+__device__ __forceinline__ void own_frags(bf16x8 (&f)[HD / 16], const bf16* base, int64_t rs, int row, int T,
+                                          int lane) {
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) {
+        if (row < T) {
+            f[ks] = *reinterpret_cast<const bf16x8*>(base + (int64_t)row * rs + ks * 16 + (lane >> 5) * 8);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[ks][e] = (bf16)0.0f;
+        }
+    }
+}
+
+// Block -> (bh, row block): the nrb blocks of one (b, h) are contiguous in a
+// per-XCD run (workgroups are dispatched round-robin over the 8 XCDs), and
+// with heavy_first the block index runs from the last row block down.
+__device__ __forceinline__ void block_coords(int nrb, int nbh, bool heavy_first, int& bh, int& rb) {
+    const int total = nrb * nbh;
+    int id = blockIdx.x;
+    if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
+    bh = id / nrb;
+    rb = id % nrb;
+    if (heavy_first) rb = nrb - 1 - rb;
+}
+
+// Write a wave's transposed accumulators (rows d, columns = its 32 rows) as
+// [row][d] rows of `out` (fp32) and optionally `outb` (bf16), scaled per
+// column by colscale (one value per lane column), via wave-private LDS.
+template <int HD>
+__device__ __forceinline__ void store_T(float* out, bf16* outb, int64_t rs, int row_base, int T,
+                                        const f32x16 (&acc)[HD / 32], float colscale, float* scratch, int lane) {
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) scratch[(lane & 31) * 36 + acc_row(v, lane)] = acc[dt][v] * colscale;
+        __syncthreads();
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass) {
+            const int r = pass * 8 + lane / 8, c4 = (lane % 8) * 4;
+            const int row = row_base + r;
+            if (row < T) {
+                const float4 x = *reinterpret_cast<const float4*>(scratch + r * 36 + c4);
+                *reinterpret_cast<float4*>(out + (int64_t)row * rs + dt * 32 + c4) = x;
+                if (outb) {
+                    bf16x4 y;
+                    y[0] = (bf16)x.x;
+                    y[1] = (bf16)x.y;
+                    y[2] = (bf16)x.z;
+                    y[3] = (bf16)x.w;
+                    *reinterpret_cast<bf16x4*>(outb + (int64_t)row * rs + dt * 32 + c4) = y;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// visibility of key kp from query qp
+__device__ __forceinline__ bool visible(int kp, int qp, int T, int window) {
+    return kp <= qp && qp < T && (window <= 0 || kp >= qp - window);
+}
+
+// ============================ forward ============================
+template <int HD>
+__global__ __launch_bounds__(kThreads) void fa2_fwd_k(float* out, bf16* outb, float* lse, const bf16* q,
+                                                      const bf16* k, const bf16* v, int B, int T, int H, int window,
+                                                      float scale_log2) {
+    using G = Geo<HD>;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    bf16* const lds = reinterpret_cast<bf16*>(smem_raw);  // stage s: K at 2 s TILE, V at (2 s + 1) TILE
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int nqb = (T + kOwn - 1) / kOwn;
+    int bh, qb;
+    block_coords(nqb, B * H, true, bh, qb);
+    const int b = bh / H, h = bh % H;
+    const int q0 = qb * kOwn, qw = q0 + wave * 32, my_q = qw + (lane & 31);
+    const int64_t rs = (int64_t)H * HD;
+    const int64_t boff = (int64_t)b * T * rs + (int64_t)h * HD;
+
+    bf16x8 qf[G::KSTEPS];
+    own_frags<HD>(qf, q + boff, rs, my_q, T, lane);
+    f32x16 o[G::DT];
+#pragma unroll
+    for (int dt = 0; dt < G::DT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+    float m = -INFINITY, l = 0.f;
+
+    int kstart = 0;
+    if (window > 0) kstart = q0 - window > 0 ? q0 - window : 0;
+    kstart = (kstart / kTile) * kTile;
+    const int kend = (q0 + kOwn < T) ? q0 + kOwn : T;
+    const int ntiles = kend > kstart ? (kend - kstart + kTile - 1) / kTile : 0;
+
+    TilePrefetch<HD> pk, pv;
+    if (ntiles > 0) {
+        pk.load(k + boff, rs, kstart, T);
+        pv.load(v + boff, rs, kstart, T);
+        pk.store(lds);
+        pv.store(lds + G::TILE);
+    }
+    __syncthreads();
+    for (int it = 0; it < ntiles; ++it) {
+        const int kv0 = kstart + it * kTile;
+        const int cur = it & 1;
+        const bool more = it + 1 < ntiles;
+        if (more) {
+            pk.load(k + boff, rs, kv0 + kTile, T);
+            pv.load(v + boff, rs, kv0 + kTile, T);
+        }
+        const bf16* sK = lds + (2 * cur) * G::TILE;
+        const bf16* sV = lds + (2 * cur + 1) * G::TILE;
+        const bool skip = kv0 > qw + 31 || (window > 0 && kv0 + kTile - 1 < qw - window) || qw >= T;
+        if (!skip) {
+            // every (key, query) of the tile visible: no per-element mask
+            const bool full = kv0 + kTile - 1 <= qw && qw + 31 < T && (window <= 0 || kv0 >= qw + 31 - window);
+            f32x16 s[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
+#pragma unroll
+                for (int ks = 0; ks < G::KSTEPS; ++ks)
+                    s[kb] = mma(rowfrag<HD>(sK, kb * 32 + (lane & 31), ks, lane), qf[ks], s[kb]);
+            }
+            float mt = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    float x = s[kb][e] * scale_log2;
+                    if (!full && !visible(kv0 + kb * 32 + acc_row(e, lane), my_q, T, window)) x = -INFINITY;
+                    s[kb][e] = x;
+                    mt = fmaxf(mt, x);
+                }
+            mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+            const float m_new = fmaxf(m, mt);
+            const float m_use = m_new == -INFINITY ? 0.f : m_new;
+            const float alpha = exp2f(m - m_use);
+            float rsum = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float p = exp2f(s[kb][e] - m_use);
+                    s[kb][e] = p;
+                    rsum += p;
+                }
+            rsum += __shfl_xor(rsum, 32, kWave);
+            l = l * alpha + rsum;
+            m = m_new;
+#pragma unroll
+            for (int dt = 0; dt < G::DT; ++dt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+            // O^T += V^T P^T with P as a two-term bf16 split (hi + lo): the
+            // backward's D = rowsum(dO * O) must equal sum_j P_j dP_j.
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    const bf16x8 ph = accfrag(s[kb], st);
+                    const bf16x8 pl = accfrag_lo(s[kb], st);
+#pragma unroll
+                    for (int dt = 0; dt < G::DT; ++dt) {
+                        const bf16x8 va = trfrag<HD>(sV, kb, st, dt, lane);
+                        o[dt] = mma(va, ph, o[dt]);
+                        o[dt] = mma(va, pl, o[dt]);
+                    }
+                }
+        }
+        if (more) {
+            pk.store(lds + (2 * (cur ^ 1)) * G::TILE);
+            pv.store(lds + (2 * (cur ^ 1) + 1) * G::TILE);
+        }
+        __syncthreads();
+    }
+    const float inv_l = l > 0.f ? 1.0f / l : 0.f;
+    if (lane < 32 && my_q < T) lse[((int64_t)b * T + my_q) * H + h] = l > 0.f ? (m + log2f(l)) * kLn2 : -INFINITY;
+    float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 36;
+    store_T<HD>(out + boff, outb ? outb + boff : nullptr, rs, qw, T, o, inv_l, scratch, lane);
+}
+
+// ============================ backward: dQ ============================
+template <int HD>
+__global__ __launch_bounds__(kThreads) void fa2_dq_k(float* dq, const bf16* q, const bf16* k, const bf16* v,
+                                                     const bf16* dout, const float* lse, const float* dbuf, int B,
+                                                     int T, int H, int window, float scale_log2, float scale) {
+    using G = Geo<HD>;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    bf16* const lds = reinterpret_cast<bf16*>(smem_raw);  // stage s: K at 2 s TILE, V at (2 s + 1) TILE
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int nqb = (T + kOwn - 1) / kOwn;
+    int bh, qb;
+    block_coords(nqb, B * H, true, bh, qb);
+    const int b = bh / H, h = bh % H;
+    const int q0 = qb * kOwn, qw = q0 + wave * 32, my_q = qw + (lane & 31);
+    const int64_t rs = (int64_t)H * HD;
+    const int64_t boff = (int64_t)b * T * rs + (int64_t)h * HD;
+
+    bf16x8 qf[G::KSTEPS], df[G::KSTEPS];
+    own_frags<HD>(qf, q + boff, rs, my_q, T, lane);
+    own_frags<HD>(df, dout + boff, rs, my_q, T, lane);
+    const int64_t bth = ((int64_t)b * T + (my_q < T ? my_q : 0)) * H + h;
+    const float my_lse2 = lse[bth] * kLog2e;
+    const float my_D = dbuf[bth];
+
+    f32x16 acc[G::DT];
+#pragma unroll
+    for (int dt = 0; dt < G::DT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[dt][e] = 0.f;
+
+    int kstart = 0;
+    if (window > 0) kstart = q0 - window > 0 ? q0 - window : 0;
+    kstart = (kstart / kTile) * kTile;
+    const int kend = (q0 + kOwn < T) ? q0 + kOwn : T;
+    const int ntiles = kend > kstart ? (kend - kstart + kTile - 1) / kTile : 0;
+
+    TilePrefetch<HD> pk, pv;
+    if (ntiles > 0) {
+        pk.load(k + boff, rs, kstart, T);
+        pv.load(v + boff, rs, kstart, T);
+        pk.store(lds);
+        pv.store(lds + G::TILE);
+    }
+    __syncthreads();
+    for (int it = 0; it < ntiles; ++it) {
+        const int kv0 = kstart + it * kTile;
+        const int cur = it & 1;
+        const bool more = it + 1 < ntiles;
+        if (more) {
+            pk.load(k + boff, rs, kv0 + kTile, T);
+            pv.load(v + boff, rs, kv0 + kTile, T);
+        }
+        const bf16* sK = lds + (2 * cur) * G::TILE;
+        const bf16* sV = lds + (2 * cur + 1) * G::TILE;
+        const bool skip = kv0 > qw + 31 || (window > 0 && kv0 + kTile - 1 < qw - window) || qw >= T;
+        if (!skip) {
+            const bool full = kv0 + kTile - 1 <= qw && qw + 31 < T && (window <= 0 || kv0 >= qw + 31 - window);
+            f32x16 s[2], dp[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) s[kb][e] = dp[kb][e] = 0.f;
+#pragma unroll
+                for (int ks = 0; ks < G::KSTEPS; ++ks) {
+                    s[kb] = mma(rowfrag<HD>(sK, kb * 32 + (lane & 31), ks, lane), qf[ks], s[kb]);
+                    dp[kb] = mma(rowfrag<HD>(sV, kb * 32 + (lane & 31), ks, lane), df[ks], dp[kb]);
+                }
+            }
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const bool ok = full || visible(kv0 + kb * 32 + acc_row(e, lane), my_q, T, window);
+                    const float p = ok ? exp2f(s[kb][e] * scale_log2 - my_lse2) : 0.f;
+                    s[kb][e] = p * (dp[kb][e] - my_D);
+                }
+            // dQ^T += K^T dS^T
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    const bf16x8 db = accfrag(s[kb], st);
+#pragma unroll
+                    for (int dt = 0; dt < G::DT; ++dt) acc[dt] = mma(trfrag<HD>(sK, kb, st, dt, lane), db, acc[dt]);
+                }
+        }
+        if (more) {
+            pk.store(lds + (2 * (cur ^ 1)) * G::TILE);
+            pv.store(lds + (2 * (cur ^ 1) + 1) * G::TILE);
+        }
+        __syncthreads();
+    }
+    float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 36;
+    store_T<HD>(dq + boff, nullptr, rs, qw, T, acc, scale, scratch, lane);
+}
+
+// ============================ backward: dK, dV ============================
+template <int HD>
+__global__ __launch_bounds__(kThreads) void fa2_dkv_k(float* dk, float* dv, const bf16* q, const bf16* k,
+                                                      const bf16* v, const bf16* dout, const float* lse,
+                                                      const float* dbuf, int B, int T, int H, int window,
+                                                      float scale_log2, float scale) {
+    using G = Geo<HD>;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    // stage s: Q at 2 s TILE, dO at (2 s + 1) TILE; then per stage 64 LSE + 64 D floats
+    bf16* const lds = reinterpret_cast<bf16*>(smem_raw);
+    float* const sLD = reinterpret_cast<float*>(lds + 4 * G::TILE);
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int nkb = (T + kOwn - 1) / kOwn;
+    int bh, kblk;
+    block_coords(nkb, B * H, false, bh, kblk);
+    const int b = bh / H, h = bh % H;
+    const int k0 = kblk * kOwn, kw = k0 + wave * 32, my_k = kw + (lane & 31);
+    const int64_t rs = (int64_t)H * HD;
+    const int64_t boff = (int64_t)b * T * rs + (int64_t)h * HD;
+
+    bf16x8 kf[G::KSTEPS], vf[G::KSTEPS];
+    own_frags<HD>(kf, k + boff, rs, my_k, T, lane);
+    own_frags<HD>(vf, v + boff, rs, my_k, T, lane);
+
+    f32x16 dka[G::DT], dva[G::DT];
+#pragma unroll
+    for (int dt = 0; dt < G::DT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) dka[dt][e] = dva[dt][e] = 0.f;
+
+    const int qstart = (k0 / kTile) * kTile;
+    int qend = T;
+    if (window > 0 && k0 + kOwn - 1 + window + 1 < T) qend = k0 + kOwn - 1 + window + 1;
+    const int ntiles = qend > qstart ? (qend - qstart + kTile - 1) / kTile : 0;
+
+    TilePrefetch<HD> pq, pd;
+    float lv = 0.f, dl = 0.f;  // this thread's LSE / D prefetch (threads < 64)
+    auto load_ld = [&](int qt0) {
+        if (threadIdx.x < kTile) {
+            const int qq = qt0 + threadIdx.x;
+            const int64_t i = ((int64_t)b * T + (qq < T ? qq : 0)) * H + h;
+            lv = lse[i] * kLog2e;
+            dl = dbuf[i];
+        }
+    };
+    auto store_ld = [&](int stage) {
+        if (threadIdx.x < kTile) {
+            sLD[stage * 2 * kTile + threadIdx.x] = lv;
+            sLD[stage * 2 * kTile + kTile + threadIdx.x] = dl;
+        }
+    };
+    if (ntiles > 0) {
+        pq.load(q + boff, rs, qstart, T);
+        pd.load(dout + boff, rs, qstart, T);
+        load_ld(qstart);
+        pq.store(lds);
+        pd.store(lds + G::TILE);
+        store_ld(0);
+    }
+    __syncthreads();
+    for (int it = 0; it < ntiles; ++it) {
+        const int qt0 = qstart + it * kTile;
+        const int cur = it & 1;
+        const bool more = it + 1 < ntiles;
+        if (more) {
+            pq.load(q + boff, rs, qt0 + kTile, T);
+            pd.load(dout + boff, rs, qt0 + kTile, T);
+            load_ld(qt0 + kTile);
+        }
+        const bf16* sQ = lds + (2 * cur) * G::TILE;
+        const bf16* sD = lds + (2 * cur + 1) * G::TILE;
+        const float* sL = sLD + cur * 2 * kTile;
+        const float* sDl = sL + kTile;
+        const bool skip = qt0 + kTile - 1 < kw || (window > 0 && qt0 > kw + 31 + window) || kw >= T;
+        if (!skip) {
+            // every (key, query) of the tile visible
+            const bool full = qt0 >= kw + 31 && qt0 + kTile <= T && kw + 31 < T &&
+                              (window <= 0 || kw >= qt0 + kTile - 1 - window);
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                f32x16 s, dp;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.f;
+#pragma unroll
+                for (int ks = 0; ks < G::KSTEPS; ++ks) {
+                    s = mma(rowfrag<HD>(sQ, qb * 32 + (lane & 31), ks, lane), kf[ks], s);
+                    dp = mma(rowfrag<HD>(sD, qb * 32 + (lane & 31), ks, lane), vf[ks], dp);
+                }
+                // lane: key my_k; rows: queries qt0 + 32 qb + acc_row(e)
+                f32x16 p, ds;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int qr = qb * 32 + acc_row(e, lane);
+                    const bool ok = full || (my_k < T && visible(my_k, qt0 + qr, T, window));
+                    const float pv = ok ? exp2f(s[e] * scale_log2 - sL[qr]) : 0.f;
+                    p[e] = pv;
+                    ds[e] = pv * (dp[e] - sDl[qr]);
+                }
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    const bf16x8 pb = accfrag(p, st);
+                    const bf16x8 db = accfrag(ds, st);
+#pragma unroll
+                    for (int dt = 0; dt < G::DT; ++dt) {
+                        dva[dt] = mma(trfrag<HD>(sD, qb, st, dt, lane), pb, dva[dt]);
+                        dka[dt] = mma(trfrag<HD>(sQ, qb, st, dt, lane), db, dka[dt]);
+                    }
+                }
+            }
+        }
+        if (more) {
+            pq.store(lds + (2 * (cur ^ 1)) * G::TILE);
+            pd.store(lds + (2 * (cur ^ 1) + 1) * G::TILE);
+            store_ld(cur ^ 1);
+        }
+        __syncthreads();
+    }
+    float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 36;
+    store_T<HD>(dk + boff, nullptr, rs, kw, T, dka, scale, scratch, lane);
+    store_T<HD>(dv + boff, nullptr, rs, kw, T, dva, 1.0f, scratch, lane);
+}
+
+template <int HD>
+constexpr size_t fa2_lds(bool with_ld) {
+    const size_t tiles = 4 * (size_t)Geo<HD>::TILE * sizeof(bf16) + (with_ld ? 4 * kTile * sizeof(float) : 0);
+    const size_t stage = 4 * 32 * 36 * sizeof(float);
+    return tiles > stage ? tiles : stage;
+}
+
+template <int HD>
+int32_t flash_hd(hipStream_t st, AttnOp op, float* o1, float* o2, bf16* ob, const bf16* q, const bf16* k,
+                 const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int B, int T, int H,
+                 int window) {
+    const float scale = 1.0f / sqrtf((float)HD);
+    const float scale_log2 = scale * kLog2e;
+    const unsigned grid = (unsigned)(((T + kOwn - 1) / kOwn) * B * H);
+    if (op == AttnOp::FWD) {
+        fa2_fwd_k<HD><<<grid, kThreads, fa2_lds<HD>(false), st>>>(o1, ob, o2, q, k, v, B, T, H, window,
+                                                                  scale_log2);
+        return check_launch("flash_attn_fwd (bf16 operands)");
+    }
+    if (op == AttnOp::DQ) {
+        fa2_dq_k<HD><<<grid, kThreads, fa2_lds<HD>(false), st>>>(o1, q, k, v, dout, lse, dbuf, B, T, H, window,
+                                                                 scale_log2, scale);
+        return check_launch("flash_attn_bwd_dq (bf16 operands)");
+    }
+    fa2_dkv_k<HD><<<grid, kThreads, fa2_lds<HD>(true), st>>>(o1, o2, q, k, v, dout, lse, dbuf, B, T, H, window,
+                                                             scale_log2, scale);
+    return check_launch("flash_attn_bwd_dkv (bf16 operands)");
+}
+
+}  // namespace
+
+int32_t flash_attn_bf16(hipStream_t st, AttnOp op, float* o1, float* o2, bf16* ob, const bf16* q, const bf16* k,
+                        const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int64_t B, int64_t T,
+                        int64_t H, int64_t HD, int64_t window) {
+    if (B <= 0 || T <= 0 || H <= 0) return B == 0 || T == 0 ? AR_OK : set_error(AR_EINVAL, "flash attention: bad shape");
+    if (((T + kOwn - 1) / kOwn) * B * H > 0x7fffffff || T > (1 << 30))
+        return set_error(AR_EINVAL, "flash attention: shape too large");
+    const int w = window > T ? (int)T : (int)window;  // a window >= T is full causal
+    switch (HD) {
+        case 32: return flash_hd<32>(st, op, o1, o2, ob, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
+        case 64: return flash_hd<64>(st, op, o1, o2, ob, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
+        case 128: return flash_hd<128>(st, op, o1, o2, ob, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
+        default: return set_error(AR_EUNSUPPORTED, "flash attention: head_dim %lld not in {32, 64, 128}", (long long)HD);
+    }
+}
+
+}  // namespace ar

@@ -58,6 +58,13 @@ int32_t attn_dispatch(hipStream_t st, AttnOp op, float* o1, float* o2, const TIN
                       const TIN* dout, const float* lse, const float* dbuf, int64_t B, int64_t T, int64_t H,
                       int64_t HD, int64_t window);
 
+// bf16-stored operands (ar_flash.hip): q, k, v, dout bf16; FWD writes
+// o1 = O (fp32), o2 = LSE and, if ob is set, a bf16 copy of O; DQ writes
+// o1 = dQ; DKV writes o1 = dK, o2 = dV (fp32).
+int32_t flash_attn_bf16(hipStream_t st, AttnOp op, float* o1, float* o2, bf16* ob, const bf16* q, const bf16* k,
+                        const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int64_t B, int64_t T,
+                        int64_t H, int64_t HD, int64_t window);
+
 // ---- element-wise (ar_elementwise.hip) ----
 int32_t rope(hipStream_t st, float* out, const float* in, const float* cos_t, const float* sin_t, int64_t nt,
              int64_t nh, int64_t hd, int64_t period, bool inverse);

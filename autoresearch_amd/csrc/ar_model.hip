@@ -51,7 +51,7 @@ struct LayerBufs {
 // Saved activations of one layer in the bf16 step.
 struct LayerBufsB {
     float *x, *lse, *attn_out, *rms_attn, *rms_mlp, *gate, *xg;
-    ar::bf16 *xn, *q, *k, *v, *xn_mlp, *h, *act;
+    ar::bf16 *xn, *q, *k, *v, *attn_out_b, *xn_mlp, *h, *act;
 };
 
 }  // namespace
@@ -185,24 +185,27 @@ double attn_keys(const ar_gpt* m, int64_t ws) {
     }
     return keys;
 }
-// fp32 operands: the fp32 step; bf16 operands: the bf16 step.
-template <typename TIN>
-int32_t attention(ar_gpt* m, AttnOp op, float* o1, float* o2, const TIN* q, const TIN* k, const TIN* v,
-                  const TIN* dout, const float* lse, const float* dbuf, int64_t ws) {
+void attn_prof_end(ar_gpt* m, int e, AttnOp op, int64_t ws) {
+    if (e < 0) return;
     const ar_gpt_config& c = m->c;
+    const double unit = 2.0 * m->B * c.n_head * c.head_dim * attn_keys(m, ws);
+    const int cls = op == AttnOp::FWD ? 3 : (op == AttnOp::DQ ? 4 : 5);
+    prof_end(m, e, cls, unit * (op == AttnOp::FWD ? 2.0 : (op == AttnOp::DQ ? 3.0 : 4.0)));
+}
+int32_t attention(ar_gpt* m, AttnOp op, float* o1, float* o2, const float* q, const float* k, const float* v,
+                  const float* dout, const float* lse, const float* dbuf, int64_t ws) {
     const int e = prof_begin(m);
-    int32_t r;
-    if constexpr (sizeof(TIN) == 2)
-        r = attn_dispatch<true, bf16>(m->st, op, o1, o2, q, k, v, dout, lse, dbuf, m->B, m->T, c.n_head, c.head_dim,
-                                      ws);
-    else
-        r = attn_dispatch<false, float>(m->st, op, o1, o2, q, k, v, dout, lse, dbuf, m->B, m->T, c.n_head,
-                                        c.head_dim, ws);
-    if (e >= 0) {
-        const double unit = 2.0 * m->B * c.n_head * c.head_dim * attn_keys(m, ws);
-        const int cls = op == AttnOp::FWD ? 3 : (op == AttnOp::DQ ? 4 : 5);
-        prof_end(m, e, cls, unit * (op == AttnOp::FWD ? 2.0 : (op == AttnOp::DQ ? 3.0 : 4.0)));
-    }
+    const int32_t r = attn_dispatch<false, float>(m->st, op, o1, o2, q, k, v, dout, lse, dbuf, m->B, m->T,
+                                                  m->c.n_head, m->c.head_dim, ws);
+    attn_prof_end(m, e, op, ws);
+    return r;
+}
+int32_t attention_b(ar_gpt* m, AttnOp op, float* o1, float* o2, bf16* ob, const bf16* q, const bf16* k,
+                    const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int64_t ws) {
+    const int e = prof_begin(m);
+    const int32_t r = flash_attn_bf16(m->st, op, o1, o2, ob, q, k, v, dout, lse, dbuf, m->B, m->T, m->c.n_head,
+                                      m->c.head_dim, ws);
+    attn_prof_end(m, e, op, ws);
     return r;
 }
 // bf16-step GEMMs (operand storage per flag; profiling class cls).
@@ -302,6 +305,7 @@ static int32_t gpt_build(ar_gpt* m) {
             AR_TRY(balloc(&b.q, BT * C));
             AR_TRY(balloc(&b.k, BT * kv));
             AR_TRY(balloc(&b.v, BT * kv));
+            AR_TRY(balloc(&b.attn_out_b, BT * C));
             AR_TRY(balloc(&b.xn_mlp, BT * C));
             AR_TRY(balloc(&b.h, BT * F));
             AR_TRY(balloc(&b.act, BT * F));
@@ -485,10 +489,10 @@ static int32_t forward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* tar
         AR_TRY(gemm_b(m, 0, 0, m->qkv, false, b.xn, true, Wb(m, m->i_q[i]), true, BT, 3 * C, C, false));
         AR_TRY(qkv_post(st, b.q, b.k, b.v, m->qkv, m->rope_cos, m->rope_sin, m->period, b.gate,
                         ve ? P(m, m->i_ve[i]) : nullptr, inputs, BT, C, H, hd));
-        AR_TRY(attention<bf16>(m, AttnOp::FWD, b.attn_out, b.lse, b.q, b.k, b.v, nullptr, nullptr, nullptr,
-                               window_size(c, i)));
+        AR_TRY(attention_b(m, AttnOp::FWD, b.attn_out, b.lse, b.attn_out_b, b.q, b.k, b.v, nullptr, nullptr, nullptr,
+                           window_size(c, i)));
         // x = x_layer + attn_out @ c_proj^T
-        AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_ADD, m->x, false, b.attn_out, false, Wb(m, m->i_proj[i]), BT, C, C, b.x,
+        AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_ADD, m->x, false, b.attn_out_b, true, Wb(m, m->i_proj[i]), BT, C, C, b.x,
                       nullptr, 0.f));
         AR_TRY(resid_norm(st, 2, nullptr, nullptr, b.rms_mlp, b.xn_mlp, nullptr, nullptr, m->x, nullptr, nullptr,
                           nullptr, nullptr, nullptr, 0, nullptr, 0, 0, BT, C));
@@ -540,13 +544,13 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
         // attention output projection
         AR_TRY(gemm_b(m, 1, 1, m->grad_attn_out_b, true, m->grad_xb, true, Wb(m, m->i_proj[i]), true, BT, C, C,
                       false));
-        AR_TRY(gemm_b(m, 2, 2, G(m, m->i_proj[i]), false, m->grad_xb, true, b.attn_out, false, BT, C, C, true));
+        AR_TRY(gemm_b(m, 2, 2, G(m, m->i_proj[i]), false, m->grad_xb, true, b.attn_out_b, true, BT, C, C, true));
         const int64_t ws = window_size(c, i);
         AR_TRY(precompute_d_mixed(st, m->d_buf, b.attn_out, m->grad_attn_out_b, BT * H, hd));
-        AR_TRY(attention<bf16>(m, AttnOp::DQ, m->grad_q, nullptr, b.q, b.k, b.v, m->grad_attn_out_b, b.lse, m->d_buf,
-                               ws));
-        AR_TRY(attention<bf16>(m, AttnOp::DKV, m->grad_k, m->grad_v, b.q, b.k, b.v, m->grad_attn_out_b, b.lse,
-                               m->d_buf, ws));
+        AR_TRY(attention_b(m, AttnOp::DQ, m->grad_q, nullptr, nullptr, b.q, b.k, b.v, m->grad_attn_out_b, b.lse,
+                           m->d_buf, ws));
+        AR_TRY(attention_b(m, AttnOp::DKV, m->grad_k, m->grad_v, nullptr, b.q, b.k, b.v, m->grad_attn_out_b, b.lse,
+                           m->d_buf, ws));
         // Q6: q/k per-head norm backward skipped; rope_bwd, ve_apply_bwd, pack [dq | dk | dv]
         AR_TRY(qkv_bwd_post(st, m->grad_qkv, m->grad_ve, m->grad_gate, m->grad_q, m->grad_k, m->grad_v, m->rope_cos,
                             m->rope_sin, m->period, b.gate, ve ? P(m, m->i_ve[i]) : nullptr, inputs, BT, C, H, hd));
@@ -602,7 +606,7 @@ extern "C" int32_t ar_gpt_forward(ar_gpt* m, const int64_t* inputs, const int64_
         AR_TRY(rope_model(m, b.k, false));
         AR_TRY(ar_rmsnorm_fwd(st, b.q, m->rms_qk, b.q, BT * H, hd));
         AR_TRY(ar_rmsnorm_fwd(st, b.k, m->rms_qk, b.k, BT * H, hd));
-        AR_TRY(attention<float>(m, AttnOp::FWD, b.attn_out, b.lse, b.q, b.k, b.v, nullptr, nullptr, nullptr,
+        AR_TRY(attention(m, AttnOp::FWD, b.attn_out, b.lse, b.q, b.k, b.v, nullptr, nullptr, nullptr,
                          window_size(c, i)));
         AR_TRY(linear(m, m->proj_out, b.attn_out, P(m, m->i_proj[i]), BT, C, C));
         AR_TRY(ar_add_residual_fwd(st, m->x, b.x, m->proj_out, BT * C));
@@ -656,8 +660,8 @@ extern "C" int32_t ar_gpt_backward(ar_gpt* m, const int64_t* inputs, const int64
         AR_TRY(linear_dw(m, G(m, m->i_proj[i]), m->grad_x, b.attn_out, BT, C, C));
         const int64_t ws = window_size(c, i);
         AR_TRY(ar_flash_attn_bwd_precompute_d(st, m->d_buf, b.attn_out, m->grad_attn_out, m->B, m->T, H, hd));
-        AR_TRY(attention<float>(m, AttnOp::DQ, m->grad_q, nullptr, b.q, b.k, b.v, m->grad_attn_out, b.lse, m->d_buf, ws));
-        AR_TRY(attention<float>(m, AttnOp::DKV, m->grad_k, m->grad_v, b.q, b.k, b.v, m->grad_attn_out, b.lse, m->d_buf,
+        AR_TRY(attention(m, AttnOp::DQ, m->grad_q, nullptr, b.q, b.k, b.v, m->grad_attn_out, b.lse, m->d_buf, ws));
+        AR_TRY(attention(m, AttnOp::DKV, m->grad_k, m->grad_v, b.q, b.k, b.v, m->grad_attn_out, b.lse, m->d_buf,
                          ws));
         // Q6: q/k per-head norm backward skipped
         if (has_ve(c, i)) {
