@@ -15,11 +15,15 @@
 //   * 256 threads = 4 wave64s, block tile 128x128, each wave a 64x64 quadrant
 //     computed as 2x2 MFMA 32x32 tiles (v_mfma_f32_32x32x16_bf16 for bf16
 //     compute, v_mfma_f32_32x32x2_f32 for exact fp32 compute).
-//   * Operands are staged through LDS in [row][k] layout (k contiguous,
-//     16-byte padded rows) so every MFMA fragment is one ds_read_b128 (bf16)
-//     or ds_read_b32 (fp32).  MN-major operands are transposed on the way in:
-//     a thread loads a (k x 4-row) block with 4-wide vector loads and writes
-//     it as 4 k-contiguous 16-byte LDS chunks.
+//   * K-major operands are staged through LDS in [row][k] layout (k
+//     contiguous, 16-byte padded rows) so every MFMA fragment is one
+//     ds_read_b128 (bf16) or ds_read_b32 (fp32).  With bf16 compute an
+//     MN-major operand stays in its natural [k][row] layout (16-byte loads
+//     and stores, chunks XOR-swizzled by k) and each fragment is two
+//     ds_read_b64_tr_b16 transpose reads; with fp32 compute it is transposed
+//     in registers on the way in.
+//   * The epilogue stages each wave's accumulators through LDS and writes C
+//     (and reads the epilogue operand) as row-contiguous 4-wide vectors.
 //   * Two LDS stages; the next k-tile's global loads are issued before the
 //     current tile's MFMAs, one barrier per k-tile.
 //   * 1-D grid, remapped so each XCD (8 per MI355X, workgroups dispatched
@@ -89,6 +93,25 @@ template <> struct Mfma<false> {
 // its column is lane % 32.
 __device__ __forceinline__ int acc_row(int v, int lane) { return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); }
 
+// 4-wide fp32 <-> storage-type vector access (16 B fp32, 8 B bf16).
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 ld4(const bf16* p) {
+    const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+    return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
+}
+__device__ __forceinline__ void st4(float* p, float4 x) { *reinterpret_cast<float4*>(p) = x; }
+__device__ __forceinline__ void st4(bf16* p, float4 x) {
+    bf16x4 v;
+    v[0] = (bf16)x.x;
+    v[1] = (bf16)x.y;
+    v[2] = (bf16)x.z;
+    v[3] = (bf16)x.w;
+    *reinterpret_cast<bf16x4*>(p) = v;
+}
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
 template <typename T, int N>
 __device__ __forceinline__ void vload(T (&dst)[N], const T* src) {
     constexpr int BYTES = N * (int)sizeof(T);
@@ -110,12 +133,23 @@ __device__ __forceinline__ void vzero(T (&dst)[N]) {
 }
 
 // Global -> register -> LDS tile loader for one operand (ROWS x BK tile).
+//   K-major (KMAJ): LDS [row][k], rows padded to ldk, one 16-byte chunk of
+//     CW k-values per item.
+//   MN-major, bf16 compute (TR): LDS holds the natural [k][row] tile (ROWS
+//     bf16 per k, 16-byte chunks XOR-swizzled by tr_swz(k)); the MFMA
+//     fragments are read with ds_read_b64_tr_b16 (tr_frag).
+//   MN-major, fp32 compute: (k x 4-row) blocks transposed in registers into
+//     the [row][k] layout.
+__device__ __forceinline__ int tr_swz(int k) { return 4 * (k & 3); }
+
 template <typename TG, typename LT, bool KMAJ, int ROWS, int BK, int CW, int kThreads>
 struct TileLoader {
-    static constexpr int MW = 4;  // rows per MN-major item
-    static constexpr int NPASS = KMAJ ? (ROWS * BK / CW) / kThreads : ((BK / CW) * (ROWS / MW)) / kThreads;
+    static constexpr bool TR = !KMAJ && sizeof(LT) == 2;
+    static constexpr int MW = 4;  // rows per MN-major item (fp32 compute)
+    static constexpr int NPASS = KMAJ ? (ROWS * BK / CW) / kThreads
+                                      : (TR ? (BK * ROWS / 8) / kThreads : ((BK / CW) * (ROWS / MW)) / kThreads);
     static_assert(NPASS >= 1, "tile too small for the block");
-    static constexpr int PER = KMAJ ? CW : CW * MW;  // TG values per pass
+    static constexpr int PER = KMAJ ? CW : (TR ? 8 : CW * MW);  // TG values per pass
     TG v[NPASS][PER];
 
     // g: operand base; ld: row stride of the stored matrix; rows: extent of
@@ -137,6 +171,13 @@ struct TileLoader {
                 } else {
                     vzero(v[p]);
                 }
+            } else if constexpr (TR) {
+                const int item = p * kThreads + tid;
+                const int k = item / (ROWS / 8), c = item % (ROWS / 8);
+                const int lc = c ^ tr_swz(k);
+                const int64_t gk = k0 + k, gr = row0 + lc * 8;
+                if (gr < rows && gk < kend) vload(v[p], g + gk * ld + gr);
+                else vzero(v[p]);
             } else {
                 const int item = p * kThreads + tid;
                 const int mg = item % (ROWS / MW), kg = item / (ROWS / MW);
@@ -165,6 +206,12 @@ struct TileLoader {
 #pragma unroll
                 for (int i = 0; i < CW; ++i) out[i] = (LT)to_f32(v[p][i]);
                 *reinterpret_cast<uint4*>(lds + r * ldk + kc) = *reinterpret_cast<const uint4*>(out);
+            } else if constexpr (TR) {
+                const int item = p * kThreads + tid;
+                LT out[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) out[i] = (LT)to_f32(v[p][i]);
+                *reinterpret_cast<uint4*>(lds + item * 8) = *reinterpret_cast<const uint4*>(out);
             } else {
                 const int item = p * kThreads + tid;
                 const int mg = item % (ROWS / MW), kg = item / (ROWS / MW);
@@ -179,7 +226,28 @@ struct TileLoader {
             }
         }
     }
+    // LDS elements of one stage of this operand.
+    static constexpr int elems(int ldk) { return TR ? BK * ROWS : ROWS * ldk; }
 };
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// MFMA fragment (32 rows from mn0, k-step ks) of a TR tile with ROWS bf16 per
+// k: inside each 16-lane group, lane 4k+q supplies the address of k-row k,
+// columns 4q..4q+3, and lane i receives k-rows 0..3 of column i; two reads
+// give lane l the k-values 16 ks + 8 (l / 32) + 0..7 of column mn0 + l % 32.
+template <int ROWS>
+__device__ __forceinline__ bf16x8 tr_frag(const bf16* tile, int mn0, int ks, int lane) {
+    const int g = lane >> 4, src = lane & 15;
+    const int k = 16 * ks + 8 * (g >> 1) + (src >> 2);
+    const int col = mn0 + 16 * (g & 1) + 4 * (src & 3);
+    const int co = (((col >> 3) ^ tr_swz(k)) << 3) + (col & 7);  // k and k + 4 share tr_swz
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + k * ROWS + co));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + (k + 4) * ROWS + co));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
 
 // Linear block id -> (batch, split, tile_m, tile_n) with an XCD-contiguous
 // order: each of the 8 XCDs owns a contiguous run of (batch, split, m, n).
@@ -206,11 +274,13 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
     constexpr int BM = TL::BM, BN = TL::BN, TM = TL::TM, TN = TL::TN;
     constexpr int BK = MM::BK, LDK = MM::LDK, CW = MM::CW;
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    // Stage s occupies [s*(BM+BN)*LDK, (s+1)*(BM+BN)*LDK): A rows then B rows.
+    // Stage s occupies [s*STAGE, (s+1)*STAGE): the A tile then the B tile.
     // Stage addresses are formed by arithmetic on the __shared__ base (never
     // through a pointer array), so every access stays a ds_read / ds_write.
     LT* const lds = reinterpret_cast<LT*>(smem_raw);
-    constexpr int STAGE = (BM + BN) * LDK;
+    using LA = TileLoader<TA, LT, AK, BM, BK, CW, TL::THREADS>;
+    using LB = TileLoader<TB, LT, BKM, BN, BK, CW, TL::THREADS>;
+    constexpr int AEL = LA::elems(LDK), STAGE = AEL + LB::elems(LDK);
 
     const int64_t tiles_n = (N + BN - 1) / BN, tiles_m = (M + BM - 1) / BM;
     const int64_t tiles_mn = tiles_m * tiles_n;
@@ -228,8 +298,8 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int wm = wave / TL::NWN, wn = wave % TL::NWN;
 
-    TileLoader<TA, LT, AK, BM, BK, CW, TL::THREADS> la;
-    TileLoader<TB, LT, BKM, BN, BK, CW, TL::THREADS> lb;
+    LA la;
+    LB lb;
 
     f32x16 acc[TM][TN];
 #pragma unroll
@@ -244,7 +314,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
         la.load(A, lda, m0, M, kbeg, kend);
         lb.load(B, ldb, n0, N, kbeg, kend);
         la.store(lds, LDK);
-        lb.store(lds + BM * LDK, LDK);
+        lb.store(lds + AEL, LDK);
     }
     __syncthreads();
     for (int64_t kt = 0; kt < nk; ++kt) {
@@ -254,15 +324,23 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
             la.load(A, lda, m0, M, kbeg + (kt + 1) * BK, kend);
             lb.load(B, ldb, n0, N, kbeg + (kt + 1) * BK, kend);
         }
-        const LT* a_base = lds + cur * STAGE + (wm * TL::WM + (lane & 31)) * LDK + MM::lane_k(lane);
-        const LT* b_base = lds + cur * STAGE + (BM + wn * TL::WN + (lane & 31)) * LDK + MM::lane_k(lane);
+        const LT* sa = lds + cur * STAGE;
+        const LT* sb = sa + AEL;
+        const LT* a_base = sa + (wm * TL::WM + (lane & 31)) * LDK + MM::lane_k(lane);
+        const LT* b_base = sb + (wn * TL::WN + (lane & 31)) * LDK + MM::lane_k(lane);
 #pragma unroll
         for (int ks = 0; ks < BK / MM::KS; ++ks) {
             typename MM::Frag fa[TM], fb[TN];
 #pragma unroll
-            for (int i = 0; i < TM; ++i) fa[i] = MM::frag(a_base + i * 32 * LDK + ks * MM::KS);
+            for (int i = 0; i < TM; ++i) {
+                if constexpr (LA::TR) fa[i] = tr_frag<BM>(sa, wm * TL::WM + i * 32, ks, lane);
+                else fa[i] = MM::frag(a_base + i * 32 * LDK + ks * MM::KS);
+            }
 #pragma unroll
-            for (int j = 0; j < TN; ++j) fb[j] = MM::frag(b_base + j * 32 * LDK + ks * MM::KS);
+            for (int j = 0; j < TN; ++j) {
+                if constexpr (LB::TR) fb[j] = tr_frag<BN>(sb, wn * TL::WN + j * 32, ks, lane);
+                else fb[j] = MM::frag(b_base + j * 32 * LDK + ks * MM::KS);
+            }
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -270,44 +348,54 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
         }
         if (more) {
             la.store(lds + (cur ^ 1) * STAGE, LDK);
-            lb.store(lds + (cur ^ 1) * STAGE + BM * LDK, LDK);
+            lb.store(lds + (cur ^ 1) * STAGE + AEL, LDK);
         }
         __syncthreads();
     }
 
-    // Epilogue.
+    // Epilogue through LDS: each wave stages a 32 x WN strip of its tile
+    // (fp32, row stride SLD) and writes it back as row-contiguous 4-wide
+    // vectors, so every global access (C, aux, partials) is coalesced.
+    constexpr int WN = TL::WN, SLD = WN + 8, VPR = WN / 4, RPI = kWave / VPR;
+    float* const strip = reinterpret_cast<float*>(smem_raw) + wave * 32 * SLD;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int64_t col = n0 + wn * TL::WN + j * 32 + (lane & 31);
-            if (col >= N) continue;
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int64_t row = m0 + wm * TL::WM + i * 32 + acc_row(v, lane);
-                if (row >= M) continue;
-                const float x = acc[i][j][v];
-                const int64_t o = row * ldc + col;
-                if constexpr (EPI == EPI_STORE) {
-                    C[o] = from_f32<TC>(x);
-                } else if constexpr (EPI == EPI_ACCUM) {
-                    C[o] = from_f32<TC>(to_f32(C[o]) + x);
-                } else if constexpr (EPI == EPI_ADD) {
-                    C[o] = from_f32<TC>(static_cast<const float*>(aux)[o] + x);
-                } else if constexpr (EPI == EPI_RELU2) {
-                    const float r = x > 0.f ? x : 0.f;
-                    C[o] = from_f32<TC>(x);
-                    static_cast<TC*>(aux_out)[o] = from_f32<TC>(r * r);
-                } else if constexpr (EPI == EPI_SOFTCAP) {
-                    C[o] = from_f32<TC>(cap * tanhf(x / cap));
-                } else if constexpr (EPI == EPI_RELU2_BWD) {
-                    const float h = to_f32(static_cast<const TC*>(aux)[o]);
-                    C[o] = from_f32<TC>(h > 0.f ? 2.f * h * x : 0.f);
-                } else {
-                    partial[(z * M + row) * N + col] = x;
-                }
+            for (int v = 0; v < 16; ++v) strip[acc_row(v, lane) * SLD + j * 32 + (lane & 31)] = acc[i][j][v];
+        __syncthreads();
+#pragma unroll
+        for (int rr = 0; rr < 32; rr += RPI) {
+            const int r = rr + lane / VPR, c4 = (lane % VPR) * 4;
+            const int64_t row = m0 + wm * TL::WM + i * 32 + r, col = n0 + wn * WN + c4;
+            if (row >= M || col >= N) continue;  // N % 4 == 0: col < N covers col + 3
+            const float4 x = *reinterpret_cast<const float4*>(strip + r * SLD + c4);
+            const int64_t o = row * ldc + col;
+            if constexpr (EPI == EPI_PARTIAL) {
+                *reinterpret_cast<float4*>(partial + (z * M + row) * N + col) = x;
+            } else if constexpr (EPI == EPI_STORE) {
+                st4(C + o, x);
+            } else if constexpr (EPI == EPI_ACCUM) {
+                st4(C + o, add4(ld4(C + o), x));
+            } else if constexpr (EPI == EPI_ADD) {
+                st4(C + o, add4(ld4(static_cast<const float*>(aux) + o), x));
+            } else if constexpr (EPI == EPI_RELU2) {
+                const float4 r2 = make_float4(x.x > 0.f ? x.x * x.x : 0.f, x.y > 0.f ? x.y * x.y : 0.f,
+                                              x.z > 0.f ? x.z * x.z : 0.f, x.w > 0.f ? x.w * x.w : 0.f);
+                st4(C + o, x);
+                st4(static_cast<TC*>(aux_out) + o, r2);
+            } else if constexpr (EPI == EPI_SOFTCAP) {
+                st4(C + o, make_float4(cap * tanhf(x.x / cap), cap * tanhf(x.y / cap), cap * tanhf(x.z / cap),
+                                       cap * tanhf(x.w / cap)));
+            } else if constexpr (EPI == EPI_RELU2_BWD) {
+                const float4 h = ld4(static_cast<const TC*>(aux) + o);
+                st4(C + o, make_float4(h.x > 0.f ? 2.f * h.x * x.x : 0.f, h.y > 0.f ? 2.f * h.y * x.y : 0.f,
+                                       h.z > 0.f ? 2.f * h.z * x.z : 0.f, h.w > 0.f ? 2.f * h.w * x.w : 0.f));
             }
         }
+        __syncthreads();
+    }
 }
 
 // C[b][i] (+)= sum_z partial[b][z][i], z in order (row stride ldc for C).
@@ -330,7 +418,10 @@ __global__ void splitk_reduce_k(TC* C, const float* partial, int64_t M, int64_t 
 template <bool BF16, typename TL>
 constexpr size_t lds_bytes() {
     using MM = Mfma<BF16>;
-    return (size_t)2 * (TL::BM + TL::BN) * MM::LDK * sizeof(typename MM::LT);
+    // K-major tiles are the larger layout (padded rows); TR tiles fit inside.
+    const size_t stages = (size_t)2 * (TL::BM + TL::BN) * MM::LDK * sizeof(typename MM::LT);
+    const size_t strips = (size_t)(TL::THREADS / 64) * 32 * (TL::WN + 8) * sizeof(float);
+    return stages > strips ? stages : strips;
 }
 
 }  // namespace
