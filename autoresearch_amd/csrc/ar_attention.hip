@@ -617,7 +617,7 @@ extern "C" int32_t ar_flash_attn_fwd_bf16(ar_stream_t stream, float* output, flo
     ar::bf16* b[3];
     int32_t r = to_bf16_ws(stream, src, 3, B * T * num_heads * head_dim, b);
     if (r) return r;
-    return ar::flash_attn_bf16(S(stream), ar::AttnOp::FWD, output, lse_out, nullptr, b[0], b[1], b[2], nullptr,
+    return ar::flash_attn_bf16(S(stream), ar::AttnOp::FWD, output, lse_out, ar::FlashOut{}, b[0], b[1], b[2], nullptr,
                                nullptr, nullptr, B, T, num_heads, head_dim, window_size);
 }
 extern "C" int32_t ar_flash_attn_bwd_dq(ar_stream_t stream, float* grad_q, const float* q, const float* k,
@@ -640,7 +640,7 @@ extern "C" int32_t ar_flash_attn_bwd_dq_bf16(ar_stream_t stream, float* grad_q, 
     ar::bf16* b[4];
     int32_t r = to_bf16_ws(stream, src, 4, B * T * num_heads * head_dim, b);
     if (r) return r;
-    return ar::flash_attn_bf16(S(stream), ar::AttnOp::DQ, grad_q, nullptr, nullptr, b[0], b[1], b[2], b[3], lse,
+    return ar::flash_attn_bf16(S(stream), ar::AttnOp::DQ, grad_q, nullptr, ar::FlashOut{}, b[0], b[1], b[2], b[3], lse,
                                d_buf, B, T, num_heads, head_dim, window_size);
 }
 extern "C" int32_t ar_flash_attn_bwd_dkv(ar_stream_t stream, float* grad_k, float* grad_v, const float* q,
@@ -663,7 +663,7 @@ extern "C" int32_t ar_flash_attn_bwd_dkv_bf16(ar_stream_t stream, float* grad_k,
     ar::bf16* b[4];
     int32_t r = to_bf16_ws(stream, src, 4, B * T * num_heads * head_dim, b);
     if (r) return r;
-    return ar::flash_attn_bf16(S(stream), ar::AttnOp::DKV, grad_k, grad_v, nullptr, b[0], b[1], b[2], b[3], lse,
+    return ar::flash_attn_bf16(S(stream), ar::AttnOp::DKV, grad_k, grad_v, ar::FlashOut{}, b[0], b[1], b[2], b[3], lse,
                                d_buf, B, T, num_heads, head_dim, window_size);
 }
 

@@ -24,8 +24,10 @@
 //   * Blocks of one (batch, head) run on one XCD (K / V stay in its L2), and
 //     the causal work is issued heavy-first.
 //
-// Layout: q, k, v, dO [B, T, H, hd] bf16 (row stride H*hd); O, dQ, dK, dV
-// fp32 (plus an optional bf16 copy of O); LSE, D [B, T, H] fp32.
+// Layout: q, k, v, dO [B, T, H, hd] bf16 (row stride H*hd); LSE, D
+// [B, T, H] fp32; outputs O, dQ, dK, dV in fp32 and / or bf16 (any row
+// stride: the bf16 step writes dQ | dK | dV into one [B*T, 3C] buffer, dQ and
+// dK already rotated back by the inverse rope).
 #include "ar_internal.hpp"
 
 namespace ar {
@@ -149,36 +151,80 @@ __device__ __forceinline__ void block_coords(int nrb, int nbh, bool heavy_first,
     if (heavy_first) rb = nrb - 1 - rb;
 }
 
-// Write a wave's transposed accumulators (rows d, columns = its 32 rows) as
-// [row][d] rows of `out` (fp32) and optionally `outb` (bf16), scaled per
-// column by colscale (one value per lane column), via wave-private LDS.
+// Write a wave's transposed accumulators (rows d, columns = its 32 rows r)
+// as [r][d] rows, scaled per column (colscale: one value per lane column):
+// fp32 to `of` (row stride rsf) and / or bf16 to `ob` (row stride rsb), the
+// bf16 copy optionally rotated by the inverse rope of its token
+// (tok = tok0 + r, table row tok % period; rope_bwd, ops.mojo:1088-1123).
+// Pairs (d, d + HD/2) are staged together through wave-private LDS (32 x 68
+// floats per wave).
+struct RowOut {
+    float* of;
+    bf16* ob;
+    int64_t rsf, rsb;
+    const float *cos_t, *sin_t;
+    int64_t tok0, period;
+};
+
 template <int HD>
-__device__ __forceinline__ void store_T(float* out, bf16* outb, int64_t rs, int row_base, int T,
-                                        const f32x16 (&acc)[HD / 32], float colscale, float* scratch, int lane) {
+__device__ __forceinline__ void store_rows(const RowOut& o, int row_base, int T, const f32x16 (&acc)[HD / 32],
+                                           float colscale, float* scratch, int lane) {
+    constexpr int DT = HD / 32, HALF = HD / 2;
+    constexpr int NPAIR = DT >= 2 ? DT / 2 : 1;  // staged (block, block + DT/2) pairs
+    constexpr int PW = DT >= 2 ? 32 : 16;        // pair columns per staged block
+    constexpr int LDS_ = 68;
 #pragma unroll
-    for (int dt = 0; dt < HD / 32; ++dt) {
+    for (int p = 0; p < NPAIR; ++p) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) scratch[(lane & 31) * 36 + acc_row(v, lane)] = acc[dt][v] * colscale;
+        for (int v = 0; v < 16; ++v) {
+            scratch[(lane & 31) * LDS_ + acc_row(v, lane)] = acc[p][v] * colscale;
+            if constexpr (DT >= 2) scratch[(lane & 31) * LDS_ + 32 + acc_row(v, lane)] = acc[p + DT / 2][v] * colscale;
+        }
         __syncthreads();
+        // items: 32 rows x (PW / 4) groups of 4 columns
 #pragma unroll
-        for (int pass = 0; pass < 4; ++pass) {
-            const int r = pass * 8 + lane / 8, c4 = (lane % 8) * 4;
+        for (int it = 0; it < 32 * (PW / 4) / kWave; ++it) {
+            const int item = it * kWave + lane;
+            const int r = item / (PW / 4), c4 = (item % (PW / 4)) * 4;
             const int row = row_base + r;
-            if (row < T) {
-                const float4 x = *reinterpret_cast<const float4*>(scratch + r * 36 + c4);
-                *reinterpret_cast<float4*>(out + (int64_t)row * rs + dt * 32 + c4) = x;
-                if (outb) {
-                    bf16x4 y;
-                    y[0] = (bf16)x.x;
-                    y[1] = (bf16)x.y;
-                    y[2] = (bf16)x.z;
-                    y[3] = (bf16)x.w;
-                    *reinterpret_cast<bf16x4*>(outb + (int64_t)row * rs + dt * 32 + c4) = y;
+            if (row >= T) continue;
+            float4 x1 = *reinterpret_cast<const float4*>(scratch + r * LDS_ + c4);
+            float4 x2 = *reinterpret_cast<const float4*>(scratch + r * LDS_ + (DT >= 2 ? 32 : 16) + c4);
+            const int d1 = (DT >= 2 ? p * 32 : 0) + c4, d2 = d1 + HALF;
+            if (o.of) {
+                *reinterpret_cast<float4*>(o.of + (int64_t)row * o.rsf + d1) = x1;
+                *reinterpret_cast<float4*>(o.of + (int64_t)row * o.rsf + d2) = x2;
+            }
+            if (o.ob) {
+                if (o.cos_t) {
+                    const int64_t tr = ((o.tok0 + row) % o.period) * HALF + d1;
+                    const float4 c = *reinterpret_cast<const float4*>(o.cos_t + tr);
+                    const float4 sn = *reinterpret_cast<const float4*>(o.sin_t + tr);
+                    // inverse rotation: s' = -sin; y1 = x1 c + x2 s', y2 = -x1 s' + x2 c
+                    const float4 y1 = make_float4(x1.x * c.x - x2.x * sn.x, x1.y * c.y - x2.y * sn.y,
+                                                  x1.z * c.z - x2.z * sn.z, x1.w * c.w - x2.w * sn.w);
+                    const float4 y2 = make_float4(x1.x * sn.x + x2.x * c.x, x1.y * sn.y + x2.y * c.y,
+                                                  x1.z * sn.z + x2.z * c.z, x1.w * sn.w + x2.w * c.w);
+                    x1 = y1;
+                    x2 = y2;
                 }
+                bf16x4 b1, b2;
+                b1[0] = (bf16)x1.x; b1[1] = (bf16)x1.y; b1[2] = (bf16)x1.z; b1[3] = (bf16)x1.w;
+                b2[0] = (bf16)x2.x; b2[1] = (bf16)x2.y; b2[2] = (bf16)x2.z; b2[3] = (bf16)x2.w;
+                *reinterpret_cast<bf16x4*>(o.ob + (int64_t)row * o.rsb + d1) = b1;
+                *reinterpret_cast<bf16x4*>(o.ob + (int64_t)row * o.rsb + d2) = b2;
             }
         }
         __syncthreads();
     }
+}
+
+// RowOut advanced to sequence b, head h (rows = tokens of sequence b).
+__device__ __forceinline__ RowOut at_head(RowOut o, int b, int h, int T, int HD) {
+    if (o.of) o.of += (int64_t)b * T * o.rsf + (int64_t)h * HD;
+    if (o.ob) o.ob += (int64_t)b * T * o.rsb + (int64_t)h * HD;
+    o.tok0 = (int64_t)b * T;
+    return o;
 }
 
 // visibility of key kp from query qp
@@ -187,10 +233,11 @@ __device__ __forceinline__ bool visible(int kp, int qp, int T, int window) {
 }
 
 // ============================ forward ============================
+// Two workgroups per CU (2 waves per SIMD): registers are capped at 256.
 template <int HD>
-__global__ __launch_bounds__(kThreads) void fa2_fwd_k(float* out, bf16* outb, float* lse, const bf16* q,
-                                                      const bf16* k, const bf16* v, int B, int T, int H, int window,
-                                                      float scale_log2) {
+__global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse, const bf16* q, const bf16* k,
+                                                         const bf16* v, int B, int T, int H, int window,
+                                                         float scale_log2) {
     using G = Geo<HD>;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     bf16* const lds = reinterpret_cast<bf16*>(smem_raw);  // stage s: K at 2 s TILE, V at (2 s + 1) TILE
@@ -303,13 +350,13 @@ __global__ __launch_bounds__(kThreads) void fa2_fwd_k(float* out, bf16* outb, fl
     }
     const float inv_l = l > 0.f ? 1.0f / l : 0.f;
     if (lane < 32 && my_q < T) lse[((int64_t)b * T + my_q) * H + h] = l > 0.f ? (m + log2f(l)) * kLn2 : -INFINITY;
-    float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 36;
-    store_T<HD>(out + boff, outb ? outb + boff : nullptr, rs, qw, T, o, inv_l, scratch, lane);
+    float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 68;
+    store_rows<HD>(at_head(out, b, h, T, HD), qw, T, o, inv_l, scratch, lane);
 }
 
 // ============================ backward: dQ ============================
 template <int HD>
-__global__ __launch_bounds__(kThreads) void fa2_dq_k(float* dq, const bf16* q, const bf16* k, const bf16* v,
+__global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q, const bf16* k, const bf16* v,
                                                      const bf16* dout, const float* lse, const float* dbuf, int B,
                                                      int T, int H, int window, float scale_log2, float scale) {
     using G = Geo<HD>;
@@ -399,16 +446,21 @@ __global__ __launch_bounds__(kThreads) void fa2_dq_k(float* dq, const bf16* q, c
         }
         __syncthreads();
     }
-    float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 36;
-    store_T<HD>(dq + boff, nullptr, rs, qw, T, acc, scale, scratch, lane);
+    float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 68;
+    store_rows<HD>(at_head(dq, b, h, T, HD), qw, T, acc, scale, scratch, lane);
 }
 
 // ============================ backward: dK, dV ============================
-template <int HD>
-__global__ __launch_bounds__(kThreads) void fa2_dkv_k(float* dk, float* dv, const bf16* q, const bf16* k,
-                                                      const bf16* v, const bf16* dout, const float* lse,
-                                                      const float* dbuf, int B, int T, int H, int window,
-                                                      float scale_log2, float scale) {
+// WHAT = kDV: S -> P -> dV^T += dO^T P; WHAT = kDK: S, dP -> dS ->
+// dK^T += Q^T dS.  Two kernels (each recomputing S) instead of one keep the
+// accumulators of each within 256 registers, so two workgroups share a CU.
+constexpr int kDV = 1, kDK = 2;
+template <int HD, int WHAT>
+__global__ __launch_bounds__(kThreads, 2) void fa2_dkv_k(RowOut out, const bf16* q, const bf16* k,
+                                                         const bf16* v, const bf16* dout, const float* lse,
+                                                         const float* dbuf, int B, int T, int H, int window,
+                                                         float scale_log2, float scale) {
+    constexpr bool DO_DV = (WHAT & kDV) != 0, DO_DK = (WHAT & kDK) != 0;
     using G = Geo<HD>;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     // stage s: Q at 2 s TILE, dO at (2 s + 1) TILE; then per stage 64 LSE + 64 D floats
@@ -423,15 +475,15 @@ __global__ __launch_bounds__(kThreads) void fa2_dkv_k(float* dk, float* dv, cons
     const int64_t rs = (int64_t)H * HD;
     const int64_t boff = (int64_t)b * T * rs + (int64_t)h * HD;
 
-    bf16x8 kf[G::KSTEPS], vf[G::KSTEPS];
+    bf16x8 kf[G::KSTEPS], vf[DO_DK ? G::KSTEPS : 1];
     own_frags<HD>(kf, k + boff, rs, my_k, T, lane);
-    own_frags<HD>(vf, v + boff, rs, my_k, T, lane);
+    if constexpr (DO_DK) own_frags<HD>(vf, v + boff, rs, my_k, T, lane);
 
-    f32x16 dka[G::DT], dva[G::DT];
+    f32x16 acc[G::DT];
 #pragma unroll
     for (int dt = 0; dt < G::DT; ++dt)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) dka[dt][e] = dva[dt][e] = 0.f;
+        for (int e = 0; e < 16; ++e) acc[dt][e] = 0.f;
 
     const int qstart = (k0 / kTile) * kTile;
     int qend = T;
@@ -489,27 +541,22 @@ __global__ __launch_bounds__(kThreads) void fa2_dkv_k(float* dk, float* dv, cons
 #pragma unroll
                 for (int ks = 0; ks < G::KSTEPS; ++ks) {
                     s = mma(rowfrag<HD>(sQ, qb * 32 + (lane & 31), ks, lane), kf[ks], s);
-                    dp = mma(rowfrag<HD>(sD, qb * 32 + (lane & 31), ks, lane), vf[ks], dp);
+                    if constexpr (DO_DK) dp = mma(rowfrag<HD>(sD, qb * 32 + (lane & 31), ks, lane), vf[ks], dp);
                 }
-                // lane: key my_k; rows: queries qt0 + 32 qb + acc_row(e)
-                f32x16 p, ds;
+                // lane: key my_k; rows: queries qt0 + 32 qb + acc_row(e); s becomes P or dS
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int qr = qb * 32 + acc_row(e, lane);
                     const bool ok = full || (my_k < T && visible(my_k, qt0 + qr, T, window));
                     const float pv = ok ? exp2f(s[e] * scale_log2 - sL[qr]) : 0.f;
-                    p[e] = pv;
-                    ds[e] = pv * (dp[e] - sDl[qr]);
+                    s[e] = DO_DK ? pv * (dp[e] - sDl[qr]) : pv;
                 }
 #pragma unroll
                 for (int st = 0; st < 2; ++st) {
-                    const bf16x8 pb = accfrag(p, st);
-                    const bf16x8 db = accfrag(ds, st);
+                    const bf16x8 fb = accfrag(s, st);
 #pragma unroll
-                    for (int dt = 0; dt < G::DT; ++dt) {
-                        dva[dt] = mma(trfrag<HD>(sD, qb, st, dt, lane), pb, dva[dt]);
-                        dka[dt] = mma(trfrag<HD>(sQ, qb, st, dt, lane), db, dka[dt]);
-                    }
+                    for (int dt = 0; dt < G::DT; ++dt)
+                        acc[dt] = mma(trfrag<HD>(DO_DK ? sQ : sD, qb, st, dt, lane), fb, acc[dt]);
                 }
             }
         }
@@ -520,53 +567,59 @@ __global__ __launch_bounds__(kThreads) void fa2_dkv_k(float* dk, float* dv, cons
         }
         __syncthreads();
     }
-    float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 36;
-    store_T<HD>(dk + boff, nullptr, rs, kw, T, dka, scale, scratch, lane);
-    store_T<HD>(dv + boff, nullptr, rs, kw, T, dva, 1.0f, scratch, lane);
+    float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 68;
+    store_rows<HD>(at_head(out, b, h, T, HD), kw, T, acc, DO_DK ? scale : 1.0f, scratch, lane);
 }
 
 template <int HD>
 constexpr size_t fa2_lds(bool with_ld) {
     const size_t tiles = 4 * (size_t)Geo<HD>::TILE * sizeof(bf16) + (with_ld ? 4 * kTile * sizeof(float) : 0);
-    const size_t stage = 4 * 32 * 36 * sizeof(float);
+    const size_t stage = 4 * 32 * 68 * sizeof(float);
     return tiles > stage ? tiles : stage;
 }
 
 template <int HD>
-int32_t flash_hd(hipStream_t st, AttnOp op, float* o1, float* o2, bf16* ob, const bf16* q, const bf16* k,
+int32_t flash_hd(hipStream_t st, AttnOp op, float* o1, float* o2, const FlashOut& fo, const bf16* q, const bf16* k,
                  const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int B, int T, int H,
                  int window) {
     const float scale = 1.0f / sqrtf((float)HD);
     const float scale_log2 = scale * kLog2e;
     const unsigned grid = (unsigned)(((T + kOwn - 1) / kOwn) * B * H);
+    const int64_t rs = (int64_t)H * HD, brs = fo.brs > 0 ? fo.brs : rs;
     if (op == AttnOp::FWD) {
-        fa2_fwd_k<HD><<<grid, kThreads, fa2_lds<HD>(false), st>>>(o1, ob, o2, q, k, v, B, T, H, window,
-                                                                  scale_log2);
+        const RowOut out{o1, fo.b1, rs, brs, nullptr, nullptr, 0, 1};
+        fa2_fwd_k<HD><<<grid, kThreads, fa2_lds<HD>(false), st>>>(out, o2, q, k, v, B, T, H, window, scale_log2);
         return check_launch("flash_attn_fwd (bf16 operands)");
     }
+    const int64_t period = fo.period > 0 ? fo.period : (int64_t)B * T;
     if (op == AttnOp::DQ) {
-        fa2_dq_k<HD><<<grid, kThreads, fa2_lds<HD>(false), st>>>(o1, q, k, v, dout, lse, dbuf, B, T, H, window,
+        const RowOut out{o1, fo.b1, rs, brs, fo.cos_t, fo.sin_t, 0, period};
+        fa2_dq_k<HD><<<grid, kThreads, fa2_lds<HD>(false), st>>>(out, q, k, v, dout, lse, dbuf, B, T, H, window,
                                                                  scale_log2, scale);
         return check_launch("flash_attn_bwd_dq (bf16 operands)");
     }
-    fa2_dkv_k<HD><<<grid, kThreads, fa2_lds<HD>(true), st>>>(o1, o2, q, k, v, dout, lse, dbuf, B, T, H, window,
-                                                             scale_log2, scale);
+    const RowOut ov{o2, fo.b2, rs, brs, nullptr, nullptr, 0, 1};
+    const RowOut ok{o1, fo.b1, rs, brs, fo.cos_t, fo.sin_t, 0, period};
+    fa2_dkv_k<HD, kDV><<<grid, kThreads, fa2_lds<HD>(true), st>>>(ov, q, k, v, dout, lse, dbuf, B, T, H, window,
+                                                                  scale_log2, scale);
+    fa2_dkv_k<HD, kDK><<<grid, kThreads, fa2_lds<HD>(true), st>>>(ok, q, k, v, dout, lse, dbuf, B, T, H, window,
+                                                                  scale_log2, scale);
     return check_launch("flash_attn_bwd_dkv (bf16 operands)");
 }
 
 }  // namespace
 
-int32_t flash_attn_bf16(hipStream_t st, AttnOp op, float* o1, float* o2, bf16* ob, const bf16* q, const bf16* k,
-                        const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int64_t B, int64_t T,
-                        int64_t H, int64_t HD, int64_t window) {
+int32_t flash_attn_bf16(hipStream_t st, AttnOp op, float* o1, float* o2, const FlashOut& fo, const bf16* q,
+                        const bf16* k, const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int64_t B,
+                        int64_t T, int64_t H, int64_t HD, int64_t window) {
     if (B <= 0 || T <= 0 || H <= 0) return B == 0 || T == 0 ? AR_OK : set_error(AR_EINVAL, "flash attention: bad shape");
     if (((T + kOwn - 1) / kOwn) * B * H > 0x7fffffff || T > (1 << 30))
         return set_error(AR_EINVAL, "flash attention: shape too large");
     const int w = window > T ? (int)T : (int)window;  // a window >= T is full causal
     switch (HD) {
-        case 32: return flash_hd<32>(st, op, o1, o2, ob, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
-        case 64: return flash_hd<64>(st, op, o1, o2, ob, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
-        case 128: return flash_hd<128>(st, op, o1, o2, ob, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
+        case 32: return flash_hd<32>(st, op, o1, o2, fo, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
+        case 64: return flash_hd<64>(st, op, o1, o2, fo, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
+        case 128: return flash_hd<128>(st, op, o1, o2, fo, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
         default: return set_error(AR_EUNSUPPORTED, "flash attention: head_dim %lld not in {32, 64, 128}", (long long)HD);
     }
 }

@@ -14,9 +14,9 @@
 //                 (ops.mojo:543-564), written as bf16 attention operands
 //   ce_fused      cross_entropy_fwd + cross_entropy_softcap_bwd (ops.mojo:
 //                 713-864) from one read of the logits row
-//   qkv_bwd_post  rope_bwd of dq and dk (ops.mojo:1088-1123), ve_apply_bwd
-//                 (ops.mojo:1193-1237), packing [dq | dk | dv] as bf16 for
-//                 the fused QKV dX / dW GEMMs
+//   ve_bwd        ve_apply_bwd (ops.mojo:1193-1237) from the bf16 dV that the
+//                 attention backward writes into the packed [dq | dk | dv]
+//                 buffer (it also applies rope_bwd to dq / dk there)
 //   norm_bwd      rmsnorm_bwd (ops.mojo:1039-1085) + add_residual, and on the
 //                 attention norm the two learned-scalar gradient dots
 //                 (ops.mojo:1277-1308) and scaled_add_bwd (ops.mojo:1311-1336)
@@ -40,6 +40,10 @@ __device__ __forceinline__ void st_bf16x4(bf16* p, float4 v) {
     o[2] = (bf16)v.z;
     o[3] = (bf16)v.w;
     *reinterpret_cast<bf16x4*>(p) = o;
+}
+__device__ __forceinline__ float4 ld_bf16x4(const bf16* p) {
+    const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+    return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
 }
 __device__ __forceinline__ float dot4(float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; }
 __device__ __forceinline__ float4 axpby4(float sa, float4 a, float sb, float4 b) {
@@ -160,7 +164,7 @@ __global__ __launch_bounds__(kBlock) void resid_norm_k(NormArgs a) {
 // part 2 = v (+ gate * value embedding).  Writes bf16 [nt, C] each.
 struct QkvArgs {
     bf16 *q, *k, *v;
-    const float* qkv;  // [nt, 3C]
+    const bf16* qkv;  // [nt, 3C]
     const float *cos_t, *sin_t;
     const float* gate;     // [nt, H] (value-embedding layers)
     const float* table;    // value-embedding table [V, C] or null
@@ -179,7 +183,7 @@ __global__ __launch_bounds__(kBlock) void qkv_post_k(QkvArgs a) {
     for (int64_t w = wave_id(); w < a.nt * 3; w += wave_count()) {
         const int64_t t = w / 3;
         const int part = (int)(w % 3);
-        const float* src = a.qkv + t * 3 * C + part * C;
+        const bf16* src = a.qkv + t * 3 * C + part * C;
         if (part < 2) {
             bf16* dst = (part == 0 ? a.q : a.k) + t * C;
             const int64_t tok = t % a.period;
@@ -188,7 +192,7 @@ __global__ __launch_bounds__(kBlock) void qkv_post_k(QkvArgs a) {
                 const int h = h0 + sub;
                 float y1 = 0.f, y2 = 0.f;
                 if (h < a.H) {
-                    const float x1 = src[h * HD + d], x2 = src[h * HD + HALF + d];
+                    const float x1 = (float)src[h * HD + d], x2 = (float)src[h * HD + HALF + d];
                     y1 = x1 * c + x2 * s;
                     y2 = x1 * (-s) + x2 * c;
                 }
@@ -201,10 +205,9 @@ __global__ __launch_bounds__(kBlock) void qkv_post_k(QkvArgs a) {
             }
         } else {
             bf16* dst = a.v + t * C;
-            const float4* s4 = reinterpret_cast<const float4*>(src);
             const float4* ve = a.table ? reinterpret_cast<const float4*>(a.table + a.idx[t] * C) : nullptr;
             for (int64_t i = lane; i < C / 4; i += kWave) {
-                float4 x = s4[i];
+                float4 x = ld_bf16x4(src + 4 * i);
                 if (ve) {
                     const float g = a.gate[t * a.H + (4 * i) / HD];
                     const float4 e = ve[i];
@@ -287,66 +290,41 @@ __global__ __launch_bounds__(kBlock) void ce_fused_k(float* loss, bf16* grad, co
 }
 
 // ---------------------------------------------------------------------
-// qkv_bwd_post: wave per (token, part).  Parts 0 / 1: inverse rope of dq /
-// dk; part 2: dv, and on value-embedding layers gve = gate * dv and
-// ggate[h] = sum_d ve[d] dv[d] (groups of HD/4 lanes hold one head).
-struct QkvBwdArgs {
-    bf16* gqkv;  // [nt, 3C]
+// ve_bwd (ve_apply_bwd, ops.mojo:1193-1237) from a bf16 dV with row stride
+// ldv: wave per token; gve = gate * dv, ggate[h] = sum_d ve[d] dv[d]
+// (groups of HD/4 lanes hold one head).
+struct VeBwdArgs {
     float* gve;  // [nt, C]
     float* ggate;
-    const float *gq, *gk, *gv;
-    const float *cos_t, *sin_t;
+    const bf16* gv;
     const float* gate;
     const float* table;
     const int64_t* idx;
-    int64_t nt, C, period;
+    int64_t nt, C, ldv;
     int H;
 };
 
 template <int HD>
-__global__ __launch_bounds__(kBlock) void qkv_bwd_post_k(QkvBwdArgs a) {
-    constexpr int HALF = HD / 2;
-    constexpr int HPI = 64 / HALF;
+__global__ __launch_bounds__(kBlock) void ve_bwd_k(VeBwdArgs a) {
     constexpr int G = HD / 4;
     const int lane = threadIdx.x % kWave;
-    const int sub = lane / HALF, d = lane % HALF;
     const int64_t C = a.C;
-    for (int64_t w = wave_id(); w < a.nt * 3; w += wave_count()) {
-        const int64_t t = w / 3;
-        const int part = (int)(w % 3);
-        bf16* dst = a.gqkv + t * 3 * C + part * C;
-        if (part < 2) {
-            const float* src = (part == 0 ? a.gq : a.gk) + t * C;
-            const int64_t tok = t % a.period;
-            const float c = a.cos_t[tok * HALF + d], s = -a.sin_t[tok * HALF + d];
-            for (int h0 = 0; h0 < a.H; h0 += HPI) {
-                const int h = h0 + sub;
-                if (h < a.H) {
-                    const float x1 = src[h * HD + d], x2 = src[h * HD + HALF + d];
-                    dst[h * HD + d] = (bf16)(x1 * c + x2 * s);
-                    dst[h * HD + HALF + d] = (bf16)(x1 * (-s) + x2 * c);
-                }
+    for (int64_t t = wave_id(); t < a.nt; t += wave_count()) {
+        const bf16* src = a.gv + t * a.ldv;
+        const float4* ve = reinterpret_cast<const float4*>(a.table + a.idx[t] * C);
+        for (int64_t i0 = 0; i0 < C / 4; i0 += kWave) {
+            const int64_t i = i0 + lane;
+            const bool ok = i < C / 4;
+            const int h = (int)((4 * i) / HD);
+            float dg = 0.f;
+            if (ok) {
+                const float4 x = ld_bf16x4(src + 4 * i);
+                const float g = a.gate[t * a.H + h];
+                reinterpret_cast<float4*>(a.gve + t * C)[i] = mul4(x, g);
+                dg = dot4(ve[i], x);
             }
-        } else {
-            const float4* s4 = reinterpret_cast<const float4*>(a.gv + t * C);
-            const float4* ve = a.table ? reinterpret_cast<const float4*>(a.table + a.idx[t] * C) : nullptr;
-            for (int64_t i0 = 0; i0 < C / 4; i0 += kWave) {
-                const int64_t i = i0 + lane;
-                const bool ok = i < C / 4;
-                const float4 x = ok ? s4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-                if (ok) st_bf16x4(dst + 4 * i, x);
-                if (ve) {
-                    const int h = (int)((4 * i) / HD);
-                    float dg = 0.f;
-                    if (ok) {
-                        const float g = a.gate[t * a.H + h];
-                        reinterpret_cast<float4*>(a.gve + t * C)[i] = mul4(x, g);
-                        dg = dot4(ve[i], x);
-                    }
-                    dg = group_sum<G>(dg);
-                    if (ok && lane % G == 0) a.ggate[t * a.H + h] = dg;
-                }
-            }
+            dg = group_sum<G>(dg);
+            if (ok && lane % G == 0) a.ggate[t * a.H + h] = dg;
         }
     }
 }
@@ -490,7 +468,7 @@ int32_t resid_norm(hipStream_t st, int mode, float* x0_out, float* x_out, float*
     return check_launch("resid_norm");
 }
 
-int32_t qkv_post(hipStream_t st, bf16* q, bf16* k, bf16* v, const float* qkv, const float* cos_t, const float* sin_t,
+int32_t qkv_post(hipStream_t st, bf16* q, bf16* k, bf16* v, const bf16* qkv, const float* cos_t, const float* sin_t,
                  int64_t period, const float* gate, const float* table, const int64_t* idx, int64_t nt, int64_t C,
                  int64_t H, int64_t hd) {
     QkvArgs a{q, k, v, qkv, cos_t, sin_t, gate, table, idx, nt, C, period, (int)H};
@@ -519,18 +497,17 @@ int32_t ce_fused(hipStream_t st, float* loss, bf16* grad, const float* logits, c
     return check_launch("ce_fused");
 }
 
-int32_t qkv_bwd_post(hipStream_t st, bf16* gqkv, float* gve, float* ggate, const float* gq, const float* gk,
-                     const float* gv, const float* cos_t, const float* sin_t, int64_t period, const float* gate,
-                     const float* table, const int64_t* idx, int64_t nt, int64_t C, int64_t H, int64_t hd) {
-    QkvBwdArgs a{gqkv, gve, ggate, gq, gk, gv, cos_t, sin_t, gate, table, idx, nt, C, period, (int)H};
-    const unsigned grid = wave_blocks(nt * 3);
+int32_t ve_bwd(hipStream_t st, float* gve, float* ggate, const bf16* gv, int64_t ldv, const float* gate,
+               const float* table, const int64_t* idx, int64_t nt, int64_t C, int64_t H, int64_t hd) {
+    VeBwdArgs a{gve, ggate, gv, gate, table, idx, nt, C, ldv, (int)H};
+    const unsigned grid = wave_blocks(nt);
     switch (hd) {
-        case 32: qkv_bwd_post_k<32><<<grid, kBlock, 0, st>>>(a); break;
-        case 64: qkv_bwd_post_k<64><<<grid, kBlock, 0, st>>>(a); break;
-        case 128: qkv_bwd_post_k<128><<<grid, kBlock, 0, st>>>(a); break;
-        default: return set_error(AR_EUNSUPPORTED, "qkv_bwd_post: head_dim %lld", (long long)hd);
+        case 32: ve_bwd_k<32><<<grid, kBlock, 0, st>>>(a); break;
+        case 64: ve_bwd_k<64><<<grid, kBlock, 0, st>>>(a); break;
+        case 128: ve_bwd_k<128><<<grid, kBlock, 0, st>>>(a); break;
+        default: return set_error(AR_EUNSUPPORTED, "ve_bwd: head_dim %lld", (long long)hd);
     }
-    return check_launch("qkv_bwd_post");
+    return check_launch("ve_bwd");
 }
 
 int32_t norm_bwd(hipStream_t st, int mode, float* gx, bf16* gxb, const float* gn, const float* x, const float* rms,

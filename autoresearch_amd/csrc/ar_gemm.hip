@@ -356,18 +356,38 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
     // Epilogue through LDS: each wave stages a 32 x WN strip of its tile
     // (fp32, row stride SLD) and writes it back as row-contiguous 4-wide
     // vectors, so every global access (C, aux, partials) is coalesced.
-    constexpr int WN = TL::WN, SLD = WN + 8, VPR = WN / 4, RPI = kWave / VPR;
+    constexpr int WN = TL::WN, SLD = WN + 8, VPR = WN / 4, RPI = kWave / VPR, NR = 32 / RPI;
+    // Epilogues that read memory (C for ACCUM, aux for ADD / RELU2_BWD) load
+    // a strip's vectors before staging it, so the loads overlap each other
+    // and the LDS round trip instead of queueing behind the stores.
+    constexpr bool PRE = EPI == EPI_ACCUM || EPI == EPI_ADD || EPI == EPI_RELU2_BWD;
     float* const strip = reinterpret_cast<float*>(smem_raw) + wave * 32 * SLD;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
+        float4 pre[PRE ? NR : 1];
+        if constexpr (PRE) {
+#pragma unroll
+            for (int t = 0; t < NR; ++t) {
+                const int r = t * RPI + lane / VPR, c4 = (lane % VPR) * 4;
+                const int64_t row = m0 + wm * TL::WM + i * 32 + r, col = n0 + wn * WN + c4;
+                const int64_t o = row * ldc + col;
+                if (row < M && col < N) {
+                    if constexpr (EPI == EPI_ACCUM) pre[t] = ld4(C + o);
+                    else if constexpr (EPI == EPI_ADD) pre[t] = ld4(static_cast<const float*>(aux) + o);
+                    else pre[t] = ld4(static_cast<const TC*>(aux) + o);
+                } else {
+                    pre[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+            }
+        }
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) strip[acc_row(v, lane) * SLD + j * 32 + (lane & 31)] = acc[i][j][v];
         __syncthreads();
 #pragma unroll
-        for (int rr = 0; rr < 32; rr += RPI) {
-            const int r = rr + lane / VPR, c4 = (lane % VPR) * 4;
+        for (int t = 0; t < NR; ++t) {
+            const int r = t * RPI + lane / VPR, c4 = (lane % VPR) * 4;
             const int64_t row = m0 + wm * TL::WM + i * 32 + r, col = n0 + wn * WN + c4;
             if (row >= M || col >= N) continue;  // N % 4 == 0: col < N covers col + 3
             const float4 x = *reinterpret_cast<const float4*>(strip + r * SLD + c4);
@@ -376,10 +396,8 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
                 *reinterpret_cast<float4*>(partial + (z * M + row) * N + col) = x;
             } else if constexpr (EPI == EPI_STORE) {
                 st4(C + o, x);
-            } else if constexpr (EPI == EPI_ACCUM) {
-                st4(C + o, add4(ld4(C + o), x));
-            } else if constexpr (EPI == EPI_ADD) {
-                st4(C + o, add4(ld4(static_cast<const float*>(aux) + o), x));
+            } else if constexpr (EPI == EPI_ACCUM || EPI == EPI_ADD) {
+                st4(C + o, add4(pre[PRE ? t : 0], x));
             } else if constexpr (EPI == EPI_RELU2) {
                 const float4 r2 = make_float4(x.x > 0.f ? x.x * x.x : 0.f, x.y > 0.f ? x.y * x.y : 0.f,
                                               x.z > 0.f ? x.z * x.z : 0.f, x.w > 0.f ? x.w * x.w : 0.f);
@@ -389,7 +407,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
                 st4(C + o, make_float4(cap * tanhf(x.x / cap), cap * tanhf(x.y / cap), cap * tanhf(x.z / cap),
                                        cap * tanhf(x.w / cap)));
             } else if constexpr (EPI == EPI_RELU2_BWD) {
-                const float4 h = ld4(static_cast<const TC*>(aux) + o);
+                const float4 h = pre[PRE ? t : 0];
                 st4(C + o, make_float4(h.x > 0.f ? 2.f * h.x * x.x : 0.f, h.y > 0.f ? 2.f * h.y * x.y : 0.f,
                                        h.z > 0.f ? 2.f * h.z * x.z : 0.f, h.w > 0.f ? 2.f * h.w * x.w : 0.f));
             }

@@ -58,12 +58,22 @@ int32_t attn_dispatch(hipStream_t st, AttnOp op, float* o1, float* o2, const TIN
                       const TIN* dout, const float* lse, const float* dbuf, int64_t B, int64_t T, int64_t H,
                       int64_t HD, int64_t window);
 
-// bf16-stored operands (ar_flash.hip): q, k, v, dout bf16; FWD writes
-// o1 = O (fp32), o2 = LSE and, if ob is set, a bf16 copy of O; DQ writes
-// o1 = dQ; DKV writes o1 = dK, o2 = dV (fp32).
-int32_t flash_attn_bf16(hipStream_t st, AttnOp op, float* o1, float* o2, bf16* ob, const bf16* q, const bf16* k,
-                        const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int64_t B, int64_t T,
-                        int64_t H, int64_t HD, int64_t window);
+// bf16-stored operands (ar_flash.hip): q, k, v, dout bf16.  fp32 outputs
+// (may be null except LSE): FWD o1 = O, o2 = LSE; DQ o1 = dQ; DKV o1 = dK,
+// o2 = dV.  bf16 outputs per FlashOut: FWD b1 = O; DQ b1 = dQ; DKV b1 = dK,
+// b2 = dV (row stride brs, 0 = H*hd); with cos_t / sin_t the bf16 dQ / dK are
+// rotated back by the inverse rope (table row = flat token % period).
+struct FlashOut {
+    bf16* b1 = nullptr;
+    bf16* b2 = nullptr;
+    int64_t brs = 0;
+    const float* cos_t = nullptr;
+    const float* sin_t = nullptr;
+    int64_t period = 0;
+};
+int32_t flash_attn_bf16(hipStream_t st, AttnOp op, float* o1, float* o2, const FlashOut& fo, const bf16* q,
+                        const bf16* k, const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int64_t B,
+                        int64_t T, int64_t H, int64_t HD, int64_t window);
 
 // ---- element-wise (ar_elementwise.hip) ----
 int32_t rope(hipStream_t st, float* out, const float* in, const float* cos_t, const float* sin_t, int64_t nt,
@@ -77,18 +87,16 @@ int32_t resid_norm(hipStream_t st, int mode, float* x0_out, float* x_out, float*
                    float* xg_out, float* gate_out, const float* xin, const float* x0, const float* table,
                    const int64_t* idx, const float* sa, const float* sb, int64_t layer, const float* gate_w,
                    int64_t nkv, int64_t gc, int64_t rows, int64_t C);
-// qkv [nt, 3C] fp32 -> q, k (rope + per-head rmsnorm), v (+ gate * table[idx]), bf16.
-int32_t qkv_post(hipStream_t st, bf16* q, bf16* k, bf16* v, const float* qkv, const float* cos_t, const float* sin_t,
+// qkv [nt, 3C] bf16 -> q, k (rope + per-head rmsnorm), v (+ gate * table[idx]), bf16.
+int32_t qkv_post(hipStream_t st, bf16* q, bf16* k, bf16* v, const bf16* qkv, const float* cos_t, const float* sin_t,
                  int64_t period, const float* gate, const float* table, const int64_t* idx, int64_t nt, int64_t C,
                  int64_t H, int64_t hd);
 // loss (may be null) and bf16 grad = (softmax - onehot) * scale per row.
 int32_t ce_fused(hipStream_t st, float* loss, bf16* grad, const float* logits, const int64_t* targets, int64_t rows,
                  int64_t V, float scale);
-// [dq | dk | dv] bf16 [nt, 3C] with inverse rope on dq, dk; with a table
-// also gve = gate * dv and ggate = per-head sum of ve * dv.
-int32_t qkv_bwd_post(hipStream_t st, bf16* gqkv, float* gve, float* ggate, const float* gq, const float* gk,
-                     const float* gv, const float* cos_t, const float* sin_t, int64_t period, const float* gate,
-                     const float* table, const int64_t* idx, int64_t nt, int64_t C, int64_t H, int64_t hd);
+// gve = gate * dv, ggate = per-head sum of table[idx] * dv (dv bf16, row stride ldv).
+int32_t ve_bwd(hipStream_t st, float* gve, float* ggate, const bf16* gv, int64_t ldv, const float* gate,
+               const float* table, const int64_t* idx, int64_t nt, int64_t C, int64_t H, int64_t hd);
 // mode 0: gx = rmsnorm_bwd(gx); 1: gx += rmsnorm_bwd(gn); 2: g = gx +
 // rmsnorm_bwd(gn), g_res[l] += g.x, g_x0[l] += g.x0, gx = res[l] g.  gxb = bf16(gx).
 // partial: 2 * kNormBwdWaves floats (mode 2).

@@ -77,7 +77,7 @@ struct ar_gpt {
     // bf16 step
     ar::bf16* wb = nullptr;  // bf16 shadow of the parameter arena (same offsets)
     std::vector<LayerBufsB> LB;
-    float* qkv = nullptr;  // [BT, 3C] q | k | v GEMM output
+    ar::bf16* qkv = nullptr;  // [BT, 3C] q | k | v GEMM output
     ar::bf16 *x_final_b = nullptr, *grad_logits_b = nullptr, *grad_xb = nullptr, *grad_h = nullptr,
          *grad_attn_out_b = nullptr, *grad_qkv = nullptr;
     float grad_logits_scale = 0.f;  // loss_scale baked into grad_logits_b
@@ -200,10 +200,10 @@ int32_t attention(ar_gpt* m, AttnOp op, float* o1, float* o2, const float* q, co
     attn_prof_end(m, e, op, ws);
     return r;
 }
-int32_t attention_b(ar_gpt* m, AttnOp op, float* o1, float* o2, bf16* ob, const bf16* q, const bf16* k,
-                    const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int64_t ws) {
+int32_t attention_b(ar_gpt* m, AttnOp op, float* o1, float* o2, const FlashOut& fo, const bf16* q,
+                    const bf16* k, const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int64_t ws) {
     const int e = prof_begin(m);
-    const int32_t r = flash_attn_bf16(m->st, op, o1, o2, ob, q, k, v, dout, lse, dbuf, m->B, m->T, m->c.n_head,
+    const int32_t r = flash_attn_bf16(m->st, op, o1, o2, fo, q, k, v, dout, lse, dbuf, m->B, m->T, m->c.n_head,
                                       m->c.head_dim, ws);
     attn_prof_end(m, e, op, ws);
     return r;
@@ -285,9 +285,6 @@ static int32_t gpt_build(ar_gpt* m) {
     FALLOC(m->d_buf, BT * H);
     FALLOC(m->grad_x, BT * C);
     FALLOC(m->grad_x_norm, BT * C);
-    FALLOC(m->grad_q, BT * C);
-    FALLOC(m->grad_k, BT * kv);
-    FALLOC(m->grad_v, BT * kv);
     FALLOC(m->grad_ve, BT * kv);
     FALLOC(m->grad_gate, BT * H);
     auto balloc = [&](bf16** p, int64_t n) { return dalloc(m, (void**)p, (size_t)n * sizeof(bf16)); };
@@ -316,7 +313,7 @@ static int32_t gpt_build(ar_gpt* m) {
                 b.gate = b.xg = nullptr;
             }
         }
-        FALLOC(m->qkv, BT * 3 * C);
+        AR_TRY(balloc(&m->qkv, BT * 3 * C));
         AR_TRY(balloc(&m->x_final_b, BT * C));
         AR_TRY(balloc(&m->grad_logits_b, BT * V));
         AR_TRY(balloc(&m->grad_xb, BT * C));
@@ -350,6 +347,9 @@ static int32_t gpt_build(ar_gpt* m) {
                 b.ve = b.gate = nullptr;
             }
         }
+        FALLOC(m->grad_q, BT * C);
+        FALLOC(m->grad_k, BT * kv);
+        FALLOC(m->grad_v, BT * kv);
         FALLOC(m->grad_x0, BT * C);
         FALLOC(m->grad_logits, BT * V);
         FALLOC(m->grad_attn_out, BT * C);
@@ -486,10 +486,12 @@ static int32_t forward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* tar
                           ve ? b.gate : nullptr, m->x, m->x0, P(m, m->i_wte), inputs, P(m, m->i_res), P(m, m->i_x0),
                           i, ve ? P(m, m->i_gate[i]) : nullptr, H, kGateChannels, BT, C));
         // c_q | c_k | c_v: one [3C, C] weight
-        AR_TRY(gemm_b(m, 0, 0, m->qkv, false, b.xn, true, Wb(m, m->i_q[i]), true, BT, 3 * C, C, false));
+        AR_TRY(gemm_b(m, 0, 0, m->qkv, true, b.xn, true, Wb(m, m->i_q[i]), true, BT, 3 * C, C, false));
         AR_TRY(qkv_post(st, b.q, b.k, b.v, m->qkv, m->rope_cos, m->rope_sin, m->period, b.gate,
                         ve ? P(m, m->i_ve[i]) : nullptr, inputs, BT, C, H, hd));
-        AR_TRY(attention_b(m, AttnOp::FWD, b.attn_out, b.lse, b.attn_out_b, b.q, b.k, b.v, nullptr, nullptr, nullptr,
+        FlashOut fo;
+        fo.b1 = b.attn_out_b;
+        AR_TRY(attention_b(m, AttnOp::FWD, b.attn_out, b.lse, fo, b.q, b.k, b.v, nullptr, nullptr, nullptr,
                            window_size(c, i)));
         // x = x_layer + attn_out @ c_proj^T
         AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_ADD, m->x, false, b.attn_out_b, true, Wb(m, m->i_proj[i]), BT, C, C, b.x,
@@ -547,13 +549,24 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
         AR_TRY(gemm_b(m, 2, 2, G(m, m->i_proj[i]), false, m->grad_xb, true, b.attn_out_b, true, BT, C, C, true));
         const int64_t ws = window_size(c, i);
         AR_TRY(precompute_d_mixed(st, m->d_buf, b.attn_out, m->grad_attn_out_b, BT * H, hd));
-        AR_TRY(attention_b(m, AttnOp::DQ, m->grad_q, nullptr, nullptr, b.q, b.k, b.v, m->grad_attn_out_b, b.lse,
-                           m->d_buf, ws));
-        AR_TRY(attention_b(m, AttnOp::DKV, m->grad_k, m->grad_v, nullptr, b.q, b.k, b.v, m->grad_attn_out_b, b.lse,
-                           m->d_buf, ws));
-        // Q6: q/k per-head norm backward skipped; rope_bwd, ve_apply_bwd, pack [dq | dk | dv]
-        AR_TRY(qkv_bwd_post(st, m->grad_qkv, m->grad_ve, m->grad_gate, m->grad_q, m->grad_k, m->grad_v, m->rope_cos,
-                            m->rope_sin, m->period, b.gate, ve ? P(m, m->i_ve[i]) : nullptr, inputs, BT, C, H, hd));
+        // dQ | dK | dV straight into the packed bf16 [BT, 3C] buffer, dQ / dK
+        // rotated back by the inverse rope (rope_bwd; Q6: q/k norm backward skipped)
+        FlashOut fo;
+        fo.brs = 3 * C;
+        fo.cos_t = m->rope_cos;
+        fo.sin_t = m->rope_sin;
+        fo.period = m->period;
+        fo.b1 = m->grad_qkv;
+        AR_TRY(attention_b(m, AttnOp::DQ, nullptr, nullptr, fo, b.q, b.k, b.v, m->grad_attn_out_b, b.lse, m->d_buf,
+                           ws));
+        fo.b1 = m->grad_qkv + C;
+        fo.b2 = m->grad_qkv + 2 * C;
+        AR_TRY(attention_b(m, AttnOp::DKV, nullptr, nullptr, fo, b.q, b.k, b.v, m->grad_attn_out_b, b.lse, m->d_buf,
+                           ws));
+        // ve_apply_bwd from the bf16 dV
+        if (ve)
+            AR_TRY(ve_bwd(st, m->grad_ve, m->grad_gate, m->grad_qkv + 2 * C, 3 * C, b.gate, P(m, m->i_ve[i]), inputs,
+                          BT, C, H, hd));
         if (ve)
             AR_TRY(ar_embedding_bwd_sorted(AS(m), G(m, m->i_ve[i]), m->grad_ve, m->sorted_ids, m->sorted_tok, BT, kv,
                                            m->scratch));

@@ -309,10 +309,73 @@ __device__ __forceinline__ int64_t emb_upper(const uint32_t* k, int64_t lo, int6
     return lo;
 }
 
-// One wave per chunk start: partial[p] = rows of the chunk summed in token
-// order.  Lanes own float4 columns (dim % 4 == 0, 16-byte aligned rows) or
-// scalar columns otherwise; rows are read 4 at a time so their loads overlap.
-template <bool VEC>
+// Chunk sums, one workgroup per 64-position window of the sorted ids (every
+// chunk lies inside one window): the window's rows are walked in order, 8
+// rows' loads issued ahead, and each chunk's sum (started from its first row,
+// then += the next rows in token order) is written to partial[chunk start].
+// Threads own float2 columns t + 256 j (dim % 2 == 0).
+constexpr int kUnroll = 8;
+
+template <int NJ>
+__global__ __launch_bounds__(256) void emb_chunk_sum_win_k(float* partial, const uint32_t* keys, const int32_t* tok,
+                                                           const float* dy, int64_t n, int64_t dim) {
+    __shared__ uint32_t s_key[kEmbChunk];
+    __shared__ int32_t s_tok[kEmbChunk];
+    const int64_t w0 = (int64_t)blockIdx.x * kEmbChunk;
+    const int len = (int)(n - w0 < kEmbChunk ? n - w0 : kEmbChunk);
+    if (threadIdx.x < len) {
+        s_key[threadIdx.x] = keys[w0 + threadIdx.x];
+        s_tok[threadIdx.x] = tok[w0 + threadIdx.x];
+    }
+    __syncthreads();
+    const int64_t d2 = dim / 2;
+    float2 acc[NJ];
+    int start = 0;
+    for (int r0 = 0; r0 < len; r0 += kUnroll) {
+        float2 x[kUnroll][NJ];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int r = r0 + u < len ? r0 + u : 0;
+            const float2* row = reinterpret_cast<const float2*>(dy + (int64_t)s_tok[r] * dim);
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const int64_t c = threadIdx.x + 256 * j;
+                x[u][j] = (r0 + u < len && c < d2) ? row[c] : make_float2(0.f, 0.f);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int r = r0 + u;
+            if (r >= len) break;
+            if (r == 0 || s_key[r] != s_key[r - 1]) {
+                if (r > 0) {
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        const int64_t c = threadIdx.x + 256 * j;
+                        if (c < d2) reinterpret_cast<float2*>(partial + (w0 + start) * dim)[c] = acc[j];
+                    }
+                }
+                start = r;
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) acc[j] = x[u][j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    acc[j].x += x[u][j].x;
+                    acc[j].y += x[u][j].y;
+                }
+            }
+        }
+    }
+    if (len > 0) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int64_t c = threadIdx.x + 256 * j;
+            if (c < d2) reinterpret_cast<float2*>(partial + (w0 + start) * dim)[c] = acc[j];
+        }
+    }
+}
+
 __global__ void emb_chunk_sum_k(float* partial, const uint32_t* keys, const int32_t* tok, const float* dy, int64_t n,
                                 int64_t dim) {
     const int lane = threadIdx.x % kWave;
@@ -321,36 +384,58 @@ __global__ void emb_chunk_sum_k(float* partial, const uint32_t* keys, const int3
     int64_t q = (p / kEmbChunk + 1) * kEmbChunk;
     if (q > n) q = n;
     q = emb_upper(keys, p, q, keys[p]);
-    if (VEC) {
-        for (int64_t d = lane; d < dim / 4; d += kWave) {
-            float4 s = reinterpret_cast<const float4*>(dy + (int64_t)tok[p] * dim)[d];
-            int64_t r = p + 1;
-            for (; r + 4 <= q; r += 4) {
-                const float4 a = reinterpret_cast<const float4*>(dy + (int64_t)tok[r] * dim)[d];
-                const float4 b = reinterpret_cast<const float4*>(dy + (int64_t)tok[r + 1] * dim)[d];
-                const float4 c = reinterpret_cast<const float4*>(dy + (int64_t)tok[r + 2] * dim)[d];
-                const float4 e = reinterpret_cast<const float4*>(dy + (int64_t)tok[r + 3] * dim)[d];
-                s.x += a.x; s.y += a.y; s.z += a.z; s.w += a.w;
-                s.x += b.x; s.y += b.y; s.z += b.z; s.w += b.w;
-                s.x += c.x; s.y += c.y; s.z += c.z; s.w += c.w;
-                s.x += e.x; s.y += e.y; s.z += e.z; s.w += e.w;
-            }
-            for (; r < q; ++r) {
-                const float4 a = reinterpret_cast<const float4*>(dy + (int64_t)tok[r] * dim)[d];
-                s.x += a.x; s.y += a.y; s.z += a.z; s.w += a.w;
-            }
-            reinterpret_cast<float4*>(partial + p * dim)[d] = s;
-        }
-    } else {
-        for (int64_t d = lane; d < dim; d += kWave) {
-            float s = dy[(int64_t)tok[p] * dim + d];
-            for (int64_t r = p + 1; r < q; ++r) s += dy[(int64_t)tok[r] * dim + d];
-            partial[p * dim + d] = s;
-        }
+    for (int64_t d = lane; d < dim; d += kWave) {
+        float s = dy[(int64_t)tok[p] * dim + d];
+        for (int64_t r = p + 1; r < q; ++r) s += dy[(int64_t)tok[r] * dim + d];
+        partial[p * dim + d] = s;
     }
 }
 
-// One wave per id segment: G[v] = ((G[v] + chunk_0) + chunk_1) + ...
+// One wave per id segment: G[v] = ((G[v] + chunk_0) + chunk_1) + ..., where
+// chunk_0 starts at the segment start p and chunk_j (j >= 1) at the j-th
+// multiple of kEmbChunk after it.  Lane l owns the float4 columns l + 64 j
+// (j < NC); the chunk rows' loads are issued kUnroll at a time ahead of their
+// in-order adds.
+template <int NC>
+__global__ void emb_segment_apply_v_k(float* gw, const float* partial, const uint32_t* keys, int64_t n, int64_t dim) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t p = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+    if (p >= n || !(p == 0 || keys[p] != keys[p - 1])) return;
+    const uint32_t v = keys[p];
+    const int64_t end = emb_upper(keys, p + 1, n, v);
+    const int64_t d4 = dim / 4;
+    float4* row = reinterpret_cast<float4*>(gw + (int64_t)v * dim);
+    float4 acc[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) acc[j] = lane + 64 * j < d4 ? row[lane + 64 * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    // chunk starts: p, then (p / kEmbChunk + j) * kEmbChunk for j >= 1, below end
+    const int64_t nch = 1 + (end - 1) / kEmbChunk - p / kEmbChunk;
+    for (int64_t c0 = 0; c0 < nch; c0 += kUnroll) {
+        float4 x[kUnroll][NC];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t ci = c0 + u;
+            const bool ok = ci < nch;
+            const int64_t c = !ok ? p : (ci == 0 ? p : (p / kEmbChunk + ci) * kEmbChunk);
+            const float4* src = reinterpret_cast<const float4*>(partial + c * dim);
+#pragma unroll
+            for (int j = 0; j < NC; ++j)
+                x[u][j] = ok && lane + 64 * j < d4 ? src[lane + 64 * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            if (c0 + u >= nch) break;
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                acc[j].x += x[u][j].x; acc[j].y += x[u][j].y; acc[j].z += x[u][j].z; acc[j].w += x[u][j].w;
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NC; ++j)
+        if (lane + 64 * j < d4) row[lane + 64 * j] = acc[j];
+}
+
 __global__ void emb_segment_apply_k(float* gw, const float* partial, const uint32_t* keys, int64_t n, int64_t dim) {
     const int lane = threadIdx.x % kWave;
     const int64_t p = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
@@ -553,14 +638,20 @@ extern "C" int32_t ar_embedding_bwd_sorted(ar_stream_t stream, float* grad_weigh
                                            const uint32_t* sorted_ids, const int32_t* sorted_tokens,
                                            int64_t num_tokens, int64_t embd_dim, float* partial) {
     const int64_t n = num_tokens;
+    if (n <= 0 || embd_dim <= 0) return AR_OK;
     const unsigned grid = (unsigned)cdiv(n, kBlock / kWave);
-    if (embd_dim % 4 == 0 && al16(grad_output) && al16(partial))
-        emb_chunk_sum_k<true><<<grid, kBlock, 0, S(stream)>>>(partial, sorted_ids, sorted_tokens, grad_output, n,
-                                                              embd_dim);
-    else
-        emb_chunk_sum_k<false><<<grid, kBlock, 0, S(stream)>>>(partial, sorted_ids, sorted_tokens, grad_output, n,
-                                                               embd_dim);
-    emb_segment_apply_k<<<grid, kBlock, 0, S(stream)>>>(grad_weight, partial, sorted_ids, n, embd_dim);
+    const int64_t nc = cdiv(embd_dim, 256), nj = cdiv(embd_dim, 512);
+    if (embd_dim % 4 == 0 && al16(grad_output) && al16(partial) && al16(grad_weight) && nc <= 4) {
+        const unsigned wins = (unsigned)cdiv(n, kEmbChunk);
+        if (nj <= 1) emb_chunk_sum_win_k<1><<<wins, 256, 0, S(stream)>>>(partial, sorted_ids, sorted_tokens, grad_output, n, embd_dim);
+        else emb_chunk_sum_win_k<2><<<wins, 256, 0, S(stream)>>>(partial, sorted_ids, sorted_tokens, grad_output, n, embd_dim);
+        if (nc <= 1) emb_segment_apply_v_k<1><<<grid, kBlock, 0, S(stream)>>>(grad_weight, partial, sorted_ids, n, embd_dim);
+        else if (nc <= 2) emb_segment_apply_v_k<2><<<grid, kBlock, 0, S(stream)>>>(grad_weight, partial, sorted_ids, n, embd_dim);
+        else emb_segment_apply_v_k<4><<<grid, kBlock, 0, S(stream)>>>(grad_weight, partial, sorted_ids, n, embd_dim);
+    } else {
+        emb_chunk_sum_k<<<grid, kBlock, 0, S(stream)>>>(partial, sorted_ids, sorted_tokens, grad_output, n, embd_dim);
+        emb_segment_apply_k<<<grid, kBlock, 0, S(stream)>>>(grad_weight, partial, sorted_ids, n, embd_dim);
+    }
     return AR_LAUNCH_CHECK("embedding_bwd");
 }
 

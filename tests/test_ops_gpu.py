@@ -41,7 +41,8 @@ def test_embedding_kat(env):
     np.testing.assert_array_equal(gu.host(out), [[20, 21, 22, 23], [50, 51, 52, 53], [0, 1, 2, 3]])
 
 
-@pytest.mark.parametrize("n,dim,zipf", [(4096, 512, True), (333, 128, False), (64, 40, False)])
+@pytest.mark.parametrize("n,dim,zipf", [(4096, 512, True), (333, 128, False), (64, 40, False), (65536, 512, True),
+                                         (20000, 768, True), (3000, 1024, True), (500, 1000, False)])
 def test_embedding_bwd_bitexact(env, n, dim, zipf):
     ops, orc, gu = env
     r = gu.rng(2)
