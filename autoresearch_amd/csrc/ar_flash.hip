@@ -83,6 +83,21 @@ __device__ __forceinline__ bf16x8 trfrag(const bf16* tile, int rb, int s, int ct
     return __builtin_bit_cast(bf16x8, both);
 }
 
+// s_waitcnt vmcnt(0) (lgkmcnt / expcnt left open).  Issued once before a tile
+// loop: the loop body then starts with no vector-memory load outstanding on
+// any path, so the compiler does not make the first MFMAs of every tile wait
+// for the next tile's prefetch.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// The lane index, made opaque to the optimiser once per tile: the swizzled
+// LDS addresses derived from it are then recomputed inside the tile loop
+// (a few VALU ops) instead of being hoisted out of it, where dozens of them
+// would stay live for the whole loop and push the kernel into spills.
+__device__ __forceinline__ int opaque_lane(int lane) {
+    asm volatile("" : "+v"(lane));
+    return lane;
+}
+
 // B fragment (bf16x8) of the lane's own accumulator values, k-step s.
 __device__ __forceinline__ bf16x8 accfrag(const f32x16& a, int s) {
     bf16x8 f;
@@ -272,6 +287,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
         pk.store(lds);
         pv.store(lds + G::TILE);
     }
+    wait_vmem();
     __syncthreads();
     for (int it = 0; it < ntiles; ++it) {
         const int kv0 = kstart + it * kTile;
@@ -397,6 +413,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
         pk.store(lds);
         pv.store(lds + G::TILE);
     }
+    wait_vmem();
     __syncthreads();
     for (int it = 0; it < ntiles; ++it) {
         const int kv0 = kstart + it * kTile;
@@ -411,34 +428,31 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
         const bool skip = kv0 > qw + 31 || (window > 0 && kv0 + kTile - 1 < qw - window) || qw >= T;
         if (!skip) {
             const bool full = kv0 + kTile - 1 <= qw && qw + 31 < T && (window <= 0 || kv0 >= qw + 31 - window);
-            f32x16 s[2], dp[2];
+            // one 32-key half at a time keeps only one S / dP pair live
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
+                f32x16 s, dp;
 #pragma unroll
-                for (int e = 0; e < 16; ++e) s[kb][e] = dp[kb][e] = 0.f;
+                for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.f;
 #pragma unroll
                 for (int ks = 0; ks < G::KSTEPS; ++ks) {
-                    s[kb] = mma(rowfrag<HD>(sK, kb * 32 + (lane & 31), ks, lane), qf[ks], s[kb]);
-                    dp[kb] = mma(rowfrag<HD>(sV, kb * 32 + (lane & 31), ks, lane), df[ks], dp[kb]);
+                    s = mma(rowfrag<HD>(sK, kb * 32 + (lane & 31), ks, lane), qf[ks], s);
+                    dp = mma(rowfrag<HD>(sV, kb * 32 + (lane & 31), ks, lane), df[ks], dp);
                 }
-            }
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const bool ok = full || visible(kv0 + kb * 32 + acc_row(e, lane), my_q, T, window);
-                    const float p = ok ? exp2f(s[kb][e] * scale_log2 - my_lse2) : 0.f;
-                    s[kb][e] = p * (dp[kb][e] - my_D);
+                    const float p = ok ? exp2f(s[e] * scale_log2 - my_lse2) : 0.f;
+                    s[e] = p * (dp[e] - my_D);
                 }
-            // dQ^T += K^T dS^T
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+                // dQ^T += K^T dS^T
 #pragma unroll
                 for (int st = 0; st < 2; ++st) {
-                    const bf16x8 db = accfrag(s[kb], st);
+                    const bf16x8 db = accfrag(s, st);
 #pragma unroll
                     for (int dt = 0; dt < G::DT; ++dt) acc[dt] = mma(trfrag<HD>(sK, kb, st, dt, lane), db, acc[dt]);
                 }
+            }
         }
         if (more) {
             pk.store(lds + (2 * (cur ^ 1)) * G::TILE);
@@ -514,6 +528,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_k(RowOut out, const bf16*
         pd.store(lds + G::TILE);
         store_ld(0);
     }
+    wait_vmem();
     __syncthreads();
     for (int it = 0; it < ntiles; ++it) {
         const int qt0 = qstart + it * kTile;
@@ -530,6 +545,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_k(RowOut out, const bf16*
         const float* sDl = sL + kTile;
         const bool skip = qt0 + kTile - 1 < kw || (window > 0 && qt0 > kw + 31 + window) || kw >= T;
         if (!skip) {
+            const int lane = opaque_lane(threadIdx.x % kWave);
             // every (key, query) of the tile visible
             const bool full = qt0 >= kw + 31 && qt0 + kTile <= T && kw + 31 < T &&
                               (window <= 0 || kw >= qt0 + kTile - 1 - window);
@@ -543,13 +559,21 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_k(RowOut out, const bf16*
                     s = mma(rowfrag<HD>(sQ, qb * 32 + (lane & 31), ks, lane), kf[ks], s);
                     if constexpr (DO_DK) dp = mma(rowfrag<HD>(sD, qb * 32 + (lane & 31), ks, lane), vf[ks], dp);
                 }
-                // lane: key my_k; rows: queries qt0 + 32 qb + acc_row(e); s becomes P or dS
+                // lane: key my_k; rows: queries qt0 + 32 qb + acc_row(e); s becomes P or dS.
+                // acc_row(4a + j) = 8a + 4 (lane / 32) + j: four consecutive rows per float4.
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int qr = qb * 32 + acc_row(e, lane);
-                    const bool ok = full || (my_k < T && visible(my_k, qt0 + qr, T, window));
-                    const float pv = ok ? exp2f(s[e] * scale_log2 - sL[qr]) : 0.f;
-                    s[e] = DO_DK ? pv * (dp[e] - sDl[qr]) : pv;
+                for (int a = 0; a < 4; ++a) {
+                    const int q4 = qb * 32 + 8 * a + 4 * (lane >> 5);
+                    const float4 l4 = *reinterpret_cast<const float4*>(sL + q4);
+                    const float4 d4 = DO_DK ? *reinterpret_cast<const float4*>(sDl + q4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int e = 4 * a + j;
+                        const bool ok = full || (my_k < T && visible(my_k, qt0 + q4 + j, T, window));
+                        const float pv = ok ? exp2f(s[e] * scale_log2 - lv[j]) : 0.f;
+                        s[e] = DO_DK ? pv * (dp[e] - dv4[j]) : pv;
+                    }
                 }
 #pragma unroll
                 for (int st = 0; st < 2; ++st) {
