@@ -427,6 +427,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
         const bf16* sV = lds + (2 * cur + 1) * G::TILE;
         const bool skip = kv0 > qw + 31 || (window > 0 && kv0 + kTile - 1 < qw - window) || qw >= T;
         if (!skip) {
+            const int lane = opaque_lane(threadIdx.x % kWave);
             const bool full = kv0 + kTile - 1 <= qw && qw + 31 < T && (window <= 0 || kv0 >= qw + 31 - window);
             // one 32-key half at a time keeps only one S / dP pair live
 #pragma unroll
