@@ -1,7 +1,7 @@
 """Loader for libautoresearch_amd.so.
 
-The ctypes signatures are generated from include/ar_ops.h, so the Python view
-of the ABI cannot drift from the header.  Loading never falls back to anything:
+The ctypes signatures are generated from include/ar_ops.h and
+include/ar_data.h, so the Python view of the ABI cannot drift from the headers.  Loading never falls back to anything:
 a missing library raises.
 """
 from __future__ import annotations
@@ -14,6 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "libautoresearch_amd.so")
 HEADER = os.path.join(ROOT, "include", "ar_ops.h")
+HEADERS = [HEADER, os.path.join(ROOT, "include", "ar_data.h")]
 
 _TYPES = {
     "int32_t": ct.c_int32,
@@ -72,10 +73,11 @@ def load() -> ct.CDLL:
             f"{LIB_PATH} is missing: build it with `python -m autoresearch_amd.build` "
             "(there is no CPU fallback)")
     lib = ct.CDLL(LIB_PATH)
-    for name, (res, args) in parse_header().items():
-        fn = getattr(lib, name)
-        fn.restype = res
-        fn.argtypes = args
+    for h in HEADERS:
+        for name, (res, args) in parse_header(h).items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
     _lib = lib
     return lib
 

@@ -1,11 +1,12 @@
-"""Build libautoresearch_amd.so (gfx950) in-tree with hipcc.
+"""Build libautoresearch_amd.so (gfx950) and the ar_train driver in-tree.
 
-Usage: python -m autoresearch_amd.build [--jobs N]
+Usage: python -m autoresearch_amd.build [--jobs N] [--force]
 
-Each csrc/*.hip is compiled to an object under autoresearch_amd/_build/ and
-linked into autoresearch_amd/libautoresearch_amd.so.  Always compiles (the
-caller decides when to build); objects are rebuilt only when their source or
-a header is newer.
+Each csrc/*.hip is compiled with hipcc and each csrc/*.cpp (host-only code)
+with g++ to an object under autoresearch_amd/_build/; all are linked into
+autoresearch_amd/libautoresearch_amd.so.  host/ar_train.cpp is linked against
+it into autoresearch_amd/ar_train (rpath $ORIGIN).  Objects are rebuilt only
+when their source or a header is newer.
 """
 from __future__ import annotations
 
@@ -21,7 +22,10 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libautoresearch_amd.so")
+HOST = os.path.join(HERE, "host")
+TRAIN = os.path.join(HERE, "ar_train")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("CXX", "g++")
 ARCH = "gfx950"
 
 CFLAGS = [
@@ -50,8 +54,14 @@ def _needs(obj: str, src: str, deps) -> bool:
     return os.path.getmtime(src) > t or any(os.path.getmtime(h) > t for h in deps)
 
 
+HOST_CFLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", f"-I{os.path.join(ROOT, 'include')}"]
+
+
 def _compile(src: str, obj: str) -> str:
-    cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+    if src.endswith(".cpp"):
+        cmd = [CXX, *HOST_CFLAGS, "-c", src, "-o", obj]
+    else:
+        cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {os.path.basename(src)}\n{r.stderr[-6000:]}")
@@ -61,11 +71,15 @@ def _compile(src: str, obj: str) -> str:
 
 def build(jobs: int = 8, force: bool = False, verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
     deps = _headers()
     todo = []
+
+    def objname(src):
+        return os.path.join(BUILD, os.path.splitext(os.path.basename(src))[0] + ".o")
+
     for s in srcs:
-        obj = os.path.join(BUILD, os.path.basename(s)[:-4] + ".o")
+        obj = objname(s)
         if force or _needs(obj, s, deps):
             todo.append((s, obj))
     if todo:
@@ -75,7 +89,7 @@ def build(jobs: int = 8, force: bool = False, verbose: bool = True) -> str:
                 src = f.result()
                 if verbose:
                     print(f"[build] compiled {os.path.basename(src)}", flush=True)
-    objs = [os.path.join(BUILD, os.path.basename(s)[:-4] + ".o") for s in srcs]
+    objs = [objname(s) for s in srcs]
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -84,6 +98,17 @@ def build(jobs: int = 8, force: bool = False, verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"[build] linked {LIB}", flush=True)
+    # the training driver (host code over the C ABI)
+    drv = os.path.join(HOST, "ar_train.cpp")
+    tmp = TRAIN + ".tmp"
+    cmd = [HIPCC, "-O2", "-std=c++17", "-Wall", f"-I{os.path.join(ROOT, 'include')}", drv, "-o", tmp,
+           f"-L{HERE}", "-lautoresearch_amd", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"ar_train link failed\n{r.stderr[-4000:]}")
+    os.replace(tmp, TRAIN)
+    if verbose:
+        print(f"[build] linked {TRAIN}", flush=True)
     return LIB
 
 

@@ -447,13 +447,13 @@ constexpr size_t lds_bytes() {
 namespace ar {
 
 template <bool BF16>
-static int64_t choose_splits(int64_t tiles, int64_t K, int64_t splits_req, int64_t& kps) {
+static int64_t choose_splits(int64_t tiles, int64_t K, int64_t splits_req, int64_t& kps, int64_t target = 512) {
     constexpr int BKt = Mfma<BF16>::BK;
     int64_t splits = splits_req;
     if (splits < 1) {
-        // Aim for >= 512 workgroups (2 per CU) when the reduction is long.
+        // Aim for `target` workgroups when the reduction is long.
         splits = 1;
-        while (tiles * splits < 512 && K / (splits * 2) >= 4 * BKt) splits *= 2;
+        while (tiles * splits < target && K / (splits * 2) >= 4 * BKt) splits *= 2;
     }
     kps = ((K + splits - 1) / splits + BKt - 1) / BKt * BKt;
     if (kps < BKt) kps = BKt;
@@ -470,7 +470,9 @@ static int32_t gemm_launch_t(hipStream_t st, TC* C, const TA* A, const TB* B, in
                              int epi, const void* aux, void* aux_out, float cap) {
     const int64_t tiles = ((M + TL::BM - 1) / TL::BM) * ((N + TL::BN - 1) / TL::BN);
     int64_t kps = 0;
-    const int64_t splits = epi >= 0 ? 1 : choose_splits<BF16>(tiles * batch, K, splits_req, kps);
+    // one 256x256 workgroup per CU, two 128x128 ones
+    const int64_t target = TL::BM == 256 ? 256 : 512;
+    const int64_t splits = epi >= 0 ? 1 : choose_splits<BF16>(tiles * batch, K, splits_req, kps, target);
     if (epi >= 0) choose_splits<BF16>(tiles * batch, K, 1, kps);
     const size_t lds = lds_bytes<BF16, TL>();
     const unsigned grid = (unsigned)(tiles * splits * batch);
@@ -501,9 +503,11 @@ static int32_t gemm_launch_t(hipStream_t st, TC* C, const TA* A, const TB* B, in
     return check_launch(nm);
 }
 
-// Large tiles when the problem has enough of them to fill the chip.
-inline bool use_large(int64_t M, int64_t N, int64_t batch) {
-    return ((M + 255) / 256) * ((N + 255) / 256) * batch >= 256;
+// Large tiles when the problem has enough of them to fill the chip, or when
+// a long reduction (split over K) gives each of a few large tiles enough work.
+inline bool use_large(int64_t M, int64_t N, int64_t K, int64_t batch) {
+    const int64_t t = ((M + 255) / 256) * ((N + 255) / 256) * batch;
+    return t >= 256 || (K >= 16384 && t >= 4);
 }
 
 template <typename TA, typename TB, typename TC, bool AK, bool BKM, bool BF16>
@@ -512,7 +516,7 @@ static int32_t gemm_launch(hipStream_t st, TC* C, const TA* A, const TB* B, int6
                            float* partial, const char* nm, int64_t batch = 1, int64_t sA = 0, int64_t sB = 0,
                            int64_t sC = 0, int epi = -1, const void* aux = nullptr, void* aux_out = nullptr,
                            float cap = 0.f) {
-    if (use_large(M, N, batch))
+    if (use_large(M, N, K, batch))
         return gemm_launch_t<TA, TB, TC, AK, BKM, BF16, TileL>(st, C, A, B, M, N, K, lda, ldb, ldc, accumulate,
                                                                splits_req, partial, nm, batch, sA, sB, sC, epi, aux,
                                                                aux_out, cap);
@@ -532,9 +536,10 @@ int64_t gemm_auto_splits(int layout, bool bf16, int64_t M, int64_t N, int64_t K)
     if (layout != 2) return 1;
     int64_t gm, gn, gk, kps;
     gemm_space(layout, M, N, K, gm, gn, gk);
-    const int64_t tiles = use_large(gm, gn, 1) ? ((gm + 255) / 256) * ((gn + 255) / 256)
-                                               : ((gm + 127) / 128) * ((gn + 127) / 128);
-    return bf16 ? choose_splits<true>(tiles, gk, 0, kps) : choose_splits<false>(tiles, gk, 0, kps);
+    const bool large = use_large(gm, gn, gk, 1);
+    const int64_t tiles = large ? ((gm + 255) / 256) * ((gn + 255) / 256) : ((gm + 127) / 128) * ((gn + 127) / 128);
+    const int64_t target = large ? 256 : 512;
+    return bf16 ? choose_splits<true>(tiles, gk, 0, kps, target) : choose_splits<false>(tiles, gk, 0, kps, target);
 }
 
 int64_t gemm_partial_elems(int layout, int64_t M, int64_t N, int64_t K, int64_t splits) {

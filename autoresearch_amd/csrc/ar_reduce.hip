@@ -273,10 +273,19 @@ __global__ void ve_gate_bwd_partial_k(float* gx, float* partial, const float* gg
     }
 }
 
+// Partials summed in block order; 16 loads issued ahead of their adds.
 __global__ void ve_gate_bwd_finish_k(float* gw, const float* partial, int nblocks, int64_t n) {
     for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
         float s = 0.f;
-        for (int b = 0; b < nblocks; ++b) s += partial[(int64_t)b * n + i];
+        int b = 0;
+        for (; b + 16 <= nblocks; b += 16) {
+            float x[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) x[u] = partial[(int64_t)(b + u) * n + i];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) s += x[u];
+        }
+        for (; b < nblocks; ++b) s += partial[(int64_t)b * n + i];
         gw[i] += s;
     }
 }
