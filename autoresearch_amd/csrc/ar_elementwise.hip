@@ -190,6 +190,23 @@ __global__ void adamw_k(float* p, const float* g, float* m, float* v, float lr, 
     }
 }
 
+// adamw_k with the step-dependent scalars (lr, 1 - b1^t, 1 - b2^t) read from
+// device memory (sc[lr_i], sc[bc1_i], sc[bc2_i]) so a recorded HIP graph
+// picks up each step's values.
+__global__ void adamw_dev_k(float* p, const float* g, float* m, float* v, const float* sc, int lr_i, int bc1_i,
+                            int bc2_i, float b1, float b2, float eps, float wd, int64_t n) {
+    const float lr = sc[lr_i], bc1 = sc[bc1_i], bc2 = sc[bc2_i];
+    AR_GRID_LOOP(i, n) {
+        float pv = p[i], gv = g[i];
+        pv = pv * (1.0f - lr * wd);
+        float mm = b1 * m[i] + (1.0f - b1) * gv;
+        m[i] = mm;
+        float vv = b2 * v[i] + (1.0f - b2) * gv * gv;
+        v[i] = vv;
+        p[i] = pv - lr * (mm / bc1) / (sqrtf(vv / bc2) + eps);
+    }
+}
+
 // ---------------- K31 Nesterov (optimizer.mojo:132-146) ----------------
 __global__ void nesterov_k(float* out, const float* g, float* buf, float mu, int64_t n) {
     AR_GRID_LOOP(i, n) {
@@ -481,4 +498,11 @@ extern "C" int32_t ar_precompute_rope(ar_stream_t stream, float* cos_buf, float*
     if (e1 != hipSuccess || e2 != hipSuccess || e3 != hipSuccess)
         return set_error(AR_EHIP, "precompute_rope: copy failed");
     return AR_OK;
+}
+
+int32_t ar::adamw_dev(hipStream_t st, float* p, const float* g, float* m, float* v, int64_t n, const float* sc,
+                      int lr_i, int bc1_i, int bc2_i, float b1, float b2, float eps, float wd) {
+    if (n == 0) return AR_OK;
+    adamw_dev_k<<<flat_grid(n, kBlock * 4), kBlock, 0, st>>>(p, g, m, v, sc, lr_i, bc1_i, bc2_i, b1, b2, eps, wd, n);
+    return AR_LAUNCH_CHECK("adamw");
 }

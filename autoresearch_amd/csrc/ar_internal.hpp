@@ -78,6 +78,10 @@ int32_t flash_attn_bf16(hipStream_t st, AttnOp op, float* o1, float* o2, const F
 // ---- element-wise (ar_elementwise.hip) ----
 int32_t rope(hipStream_t st, float* out, const float* in, const float* cos_t, const float* sin_t, int64_t nt,
              int64_t nh, int64_t hd, int64_t period, bool inverse);
+// AdamW (optimizer.mojo:27-57) with lr = sc[lr_i], bias corrections
+// 1 - b1^t = sc[bc1_i], 1 - b2^t = sc[bc2_i] read from device memory.
+int32_t adamw_dev(hipStream_t st, float* p, const float* g, float* m, float* v, int64_t n, const float* sc,
+                  int lr_i, int bc1_i, int bc2_i, float b1, float b2, float eps, float wd);
 
 // ---- fused row kernels of the bf16 step (ar_fused.hip) ----
 // mode 0: x0 = rmsnorm(table[idx]), x = sa[l] x0 + sb[l] x0; 1: x = sa[l] xin +
@@ -110,12 +114,20 @@ int32_t precompute_d_mixed(hipStream_t st, float* d, const float* o, const bf16*
 
 // ---- Muon (ar_optim.hip) ----
 constexpr int kMuonMaxGroup = 48;
+// lr factor sqrt(max(1, rows / cols)) of a [rows, cols] matrix.
+double muon_lr_factor(int64_t rows, int64_t cols);
 // Scratch (floats) for a group of n same-shape [rows, cols] matrices.
 int64_t muon_scratch_elems(int64_t rows, int64_t cols, bool bf16, int64_t n);
-// MuonState.step for n same-shape matrices at once (batched GEMMs).
+// MuonState.step for n same-shape matrices at once (batched GEMMs).  With
+// dsc set, the step's lr, momentum and weight decay are read from device
+// memory (dsc[lr_i], dsc[mu_i], dsc[wd_i]) instead of the value arguments.
+struct MuonDev {
+    const float* dsc = nullptr;
+    int lr_i = 0, mu_i = 0, wd_i = 0;
+};
 int32_t muon_group_step(hipStream_t st, float* const* params, const float* const* grads, float* const* mbufs, int n,
                         int64_t rows, int64_t cols, double initial_lr, double lrm, double momentum, double wd,
-                        bool bf16, float* scratch);
+                        bool bf16, float* scratch, const MuonDev& dev = MuonDev());
 
 }  // namespace ar
 

@@ -82,6 +82,13 @@ struct ar_gpt {
          *grad_attn_out_b = nullptr, *grad_qkv = nullptr;
     float grad_logits_scale = 0.f;  // loss_scale baked into grad_logits_b
     bool grad_logits_valid = false;
+    // step-dependent optimizer scalars in device memory (StepScalars)
+    float* dsc = nullptr;
+    // graph replay of the step (ar_gpt_train_step_graph)
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    hipGraphNode_t graph_scalars = nullptr;
+    const int64_t *graph_in = nullptr, *graph_tg = nullptr;
     // scratch (sequential users on one stream)
     float* scratch = nullptr;
     int64_t scratch_elems = 0;
@@ -136,15 +143,17 @@ inline const bf16* Wb(ar_gpt* m, int64_t i) { return m->wb + m->t[i].offset; }
 inline ar_stream_t AS(ar_gpt* m) { return reinterpret_cast<ar_stream_t>(m->st); }
 
 // Profiling brackets (no-ops unless ar_gpt_profile enabled them).
+int32_t prof_reserve(ar_gpt* m, size_t n) {
+    while (m->ev.size() < n) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return set_error(AR_EHIP, "gpt_profile: event create failed");
+        m->ev.push_back(e);
+    }
+    return AR_OK;
+}
 int prof_begin(ar_gpt* m) {
     if (!m->prof) return -1;
-    if (m->ev_used + 2 > m->ev.size()) {
-        for (int i = 0; i < 1024; ++i) {
-            hipEvent_t e;
-            if (hipEventCreate(&e) != hipSuccess) return -1;
-            m->ev.push_back(e);
-        }
-    }
+    if (m->ev_used + 2 > m->ev.size() && prof_reserve(m, m->ev.size() + 1024) != AR_OK) return -1;
     const int e0 = (int)m->ev_used;
     m->ev_used += 2;
     hipEventRecord(m->ev[e0], m->st);
@@ -281,6 +290,7 @@ static int32_t gpt_build(ar_gpt* m) {
     FALLOC(m->logits, BT * V);
     FALLOC(m->loss, BT);
     FALLOC(m->mean_loss, 64);
+    FALLOC(m->dsc, 64);
     FALLOC(m->rms_final, BT);
     FALLOC(m->d_buf, BT * H);
     FALLOC(m->grad_x, BT * C);
@@ -419,6 +429,8 @@ extern "C" int32_t ar_gpt_create(ar_gpt** out, const ar_gpt_config* cfg, int64_t
 extern "C" int32_t ar_gpt_destroy(ar_gpt* m) {
     if (!m) return AR_OK;
     hipStreamSynchronize(m->st);
+    if (m->graph_exec) hipGraphExecDestroy(m->graph_exec);
+    if (m->graph) hipGraphDestroy(m->graph);
     for (hipEvent_t e : m->ev) hipEventDestroy(e);
     for (void* p : m->allocs) hipFree(p);
     delete m;
@@ -520,8 +532,6 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
     const int64_t C = c.n_embd, V = c.vocab_size, BT = m->BT, H = c.n_head, hd = c.head_dim, kv = c.kv_dim;
     const int64_t F = kMlpExpansion * C;
     hipStream_t st = m->st;
-    AR_TRY(ar_embedding_sort(AS(m), m->sorted_ids, m->sorted_tok, inputs, BT, m->sort_bits, m->sort_scratch,
-                             m->sort_bytes, nullptr));
     if (!m->grad_logits_valid || m->grad_logits_scale != loss_scale) {
         AR_TRY(ce_fused(st, nullptr, m->grad_logits_b, m->logits, targets, BT, V, loss_scale));
         m->grad_logits_scale = loss_scale;
@@ -584,18 +594,8 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
     return ar_embedding_bwd_sorted(AS(m), G(m, m->i_wte), m->grad_x, m->sorted_ids, m->sorted_tok, BT, C, m->scratch);
 }
 
-// model.mojo:576-772
-extern "C" int32_t ar_gpt_forward(ar_gpt* m, const int64_t* inputs, const int64_t* targets, float* loss_host) {
-    AR_CHECK_ARG(m && inputs && targets, "gpt_forward: null pointer");
-    if (m->bf16) {
-        AR_TRY(forward_bf16(m, inputs, targets));
-        if (loss_host) {
-            if (hipMemcpyAsync(loss_host, m->mean_loss, sizeof(float), hipMemcpyDeviceToHost, m->st) != hipSuccess ||
-                hipStreamSynchronize(m->st) != hipSuccess)
-                return set_error(AR_EHIP, "gpt_forward: loss copy failed");
-        }
-        return AR_OK;
-    }
+// model.mojo:576-772, fp32 step
+static int32_t forward_fp32(ar_gpt* m, const int64_t* inputs, const int64_t* targets) {
     const ar_gpt_config& c = m->c;
     const int64_t C = c.n_embd, V = c.vocab_size, BT = m->BT, H = c.n_head, hd = c.head_dim;
     const int64_t kv = c.kv_dim, F = kMlpExpansion * C;
@@ -634,7 +634,13 @@ extern "C" int32_t ar_gpt_forward(ar_gpt* m, const int64_t* inputs, const int64_
     AR_TRY(linear(m, m->logits, m->x_final, P(m, m->i_lm), BT, V, C));
     AR_TRY(ar_softcap_fwd(st, m->logits, m->logits, kSoftcap, BT * V));
     AR_TRY(ar_cross_entropy_fwd(st, m->loss, m->logits, targets, BT, V));
-    AR_TRY(fixed_sum(m->st, m->mean_loss, m->loss, nullptr, BT, 0, 0, 0, m->scratch));
+    return fixed_sum(m->st, m->mean_loss, m->loss, nullptr, BT, 0, 0, 0, m->scratch);
+}
+
+// model.mojo:576-772
+extern "C" int32_t ar_gpt_forward(ar_gpt* m, const int64_t* inputs, const int64_t* targets, float* loss_host) {
+    AR_CHECK_ARG(m && inputs && targets, "gpt_forward: null pointer");
+    AR_TRY(m->bf16 ? forward_bf16(m, inputs, targets) : forward_fp32(m, inputs, targets));
     if (loss_host) {
         if (hipMemcpyAsync(loss_host, m->mean_loss, sizeof(float), hipMemcpyDeviceToHost, m->st) != hipSuccess ||
             hipStreamSynchronize(m->st) != hipSuccess)
@@ -643,16 +649,18 @@ extern "C" int32_t ar_gpt_forward(ar_gpt* m, const int64_t* inputs, const int64_
     return AR_OK;
 }
 
-// model.mojo:819-1037 (quirks Q4-Q10 of the reference backward reproduced)
-extern "C" int32_t ar_gpt_backward(ar_gpt* m, const int64_t* inputs, const int64_t* targets, float loss_scale) {
-    AR_CHECK_ARG(m && inputs && targets, "gpt_backward: null pointer");
-    if (m->bf16) return backward_bf16(m, inputs, targets, loss_scale);
+// The stable token-id sort shared by the wte and value-embedding scatters
+// (depends on the inputs only; run before the rest of the backward).
+static int32_t sort_tokens(ar_gpt* m, const int64_t* inputs) {
+    return ar_embedding_sort(AS(m), m->sorted_ids, m->sorted_tok, inputs, m->BT, m->sort_bits, m->sort_scratch,
+                             m->sort_bytes, nullptr);
+}
+
+static int32_t backward_fp32(ar_gpt* m, const int64_t* inputs, const int64_t* targets, float loss_scale) {
     const ar_gpt_config& c = m->c;
     const int64_t C = c.n_embd, V = c.vocab_size, BT = m->BT, H = c.n_head, hd = c.head_dim;
     const int64_t kv = c.kv_dim, F = kMlpExpansion * C;
     ar_stream_t st = AS(m);
-    AR_TRY(ar_embedding_sort(st, m->sorted_ids, m->sorted_tok, inputs, BT, m->sort_bits, m->sort_scratch,
-                             m->sort_bytes, nullptr));
     AR_TRY(ar_cross_entropy_softcap_bwd(st, m->grad_logits, m->logits, targets, kSoftcap, BT, V, loss_scale));
     AR_TRY(linear_dx(m, m->grad_x, m->grad_logits, P(m, m->i_lm), BT, V, C));
     AR_TRY(linear_dw(m, G(m, m->i_lm), m->grad_logits, m->x_final, BT, V, C));
@@ -707,6 +715,13 @@ extern "C" int32_t ar_gpt_backward(ar_gpt* m, const int64_t* inputs, const int64
     return AR_OK;
 }
 
+// model.mojo:819-1037 (quirks Q4-Q10 of the reference backward reproduced)
+extern "C" int32_t ar_gpt_backward(ar_gpt* m, const int64_t* inputs, const int64_t* targets, float loss_scale) {
+    AR_CHECK_ARG(m && inputs && targets, "gpt_backward: null pointer");
+    AR_TRY(sort_tokens(m, inputs));
+    return m->bf16 ? backward_bf16(m, inputs, targets, loss_scale) : backward_fp32(m, inputs, targets, loss_scale);
+}
+
 // train.mojo:25-33
 static double lr_multiplier(double progress) {
     const double kWarmup = 0.0, kWarmdown = 0.5, kFinal = 0.0;  // config.mojo:81-83
@@ -716,35 +731,86 @@ static double lr_multiplier(double progress) {
     return cd + (1.0 - cd) * kFinal;
 }
 
-// train.mojo:246-281
-extern "C" int32_t ar_gpt_optimizer_step(ar_gpt* m, double progress) {
-    AR_CHECK_ARG(m != nullptr, "gpt_optimizer_step: null model");
+// Step-dependent optimizer scalars (train.mojo:246-281), computed on the
+// host as the reference does and handed to the kernels through device memory
+// (m->dsc) so a recorded graph replays with each step's values.
+enum {
+    kScLrLm = 0, kScLrWte, kScLrRes, kScLrX0, kScLrVe, kScLrGate,  // AdamW group lr (f32(lr_g * lrm))
+    kScBc1Default, kScBc1X0, kScBc2,                             // 1 - beta^step
+    kScMuonLr0,                                                  // + shape class 0 / 1 / 2
+    kScMu = kScMuonLr0 + 3, kScWd, kScCount
+};
+struct StepScalars {
+    float v[16];
+};
+static_assert(kScCount <= 16, "step scalars");
+
+__global__ void set_scalars_k(float* dst, StepScalars s) {
+    if (threadIdx.x < kScCount) dst[threadIdx.x] = s.v[threadIdx.x];
+}
+
+// Muon shape classes: c_q / c_k / c_v / c_proj [C, C], c_fc [4C, C], mlp_proj [C, 4C].
+static int muon_class(const ar_gpt* m, int64_t ti) {
+    const Tensor& t = m->t[ti];
+    return t.rows == t.cols ? 0 : (t.rows > t.cols ? 1 : 2);
+}
+
+// Advances the AdamW step counter (train.mojo:253) and returns the scalars.
+static StepScalars step_scalars(ar_gpt* m, double progress) {
     const ar_gpt_config& c = m->c;
     if (progress > 1.0) progress = 1.0;
     const double lrm = lr_multiplier(progress);
     const double lr_scale = pow((double)c.n_embd / 768.0, -0.5);  // train.mojo:167
     m->adam_step += 1;
-    ar_stream_t st = AS(m);
-    auto adam = [&](int64_t ti, double lr, double b1) -> int32_t {
-        const Tensor& t = m->t[ti];
-        return ar_adamw_step_group(st, m->params + t.offset, m->grads + t.offset, m->adam_m + t.offset,
-                                   m->adam_v + t.offset, t.size, lr, b1, 0.95, 1e-10, 0.0, lrm, m->adam_step);
-    };
-    AR_TRY(adam(m->i_lm, 0.004 * lr_scale, 0.8));   // UNEMBEDDING_LR
-    AR_TRY(adam(m->i_wte, 0.6 * lr_scale, 0.8));    // EMBEDDING_LR
-    AR_TRY(adam(m->i_res, 0.5 * 0.01, 0.8));        // SCALAR_LR * 0.01
-    AR_TRY(adam(m->i_x0, 0.5, 0.96));               // SCALAR_LR, beta1 0.96
-    for (int64_t i = 0; i < c.n_layer; ++i)
-        if (has_ve(c, i)) {
-            AR_TRY(adam(m->i_ve[i], 0.6 * lr_scale, 0.8));
-            AR_TRY(adam(m->i_gate[i], 0.04, 0.8));  // MATRIX_LR
-        }
+    StepScalars s{};
+    s.v[kScLrLm] = (float)(0.004 * lr_scale * lrm);    // UNEMBEDDING_LR
+    s.v[kScLrWte] = (float)(0.6 * lr_scale * lrm);     // EMBEDDING_LR
+    s.v[kScLrRes] = (float)(0.5 * 0.01 * lrm);         // SCALAR_LR * 0.01
+    s.v[kScLrX0] = (float)(0.5 * lrm);                 // SCALAR_LR (beta1 0.96)
+    s.v[kScLrVe] = (float)(0.6 * lr_scale * lrm);      // EMBEDDING_LR
+    s.v[kScLrGate] = (float)(0.04 * lrm);              // MATRIX_LR
+    // optimizer.mojo:114-118: bias corrections by repeated f32 multiplication
+    float p08 = 1.f, p096 = 1.f, p095 = 1.f;
+    for (int64_t k = 0; k < m->adam_step; ++k) {
+        p08 *= 0.8f;
+        p096 *= 0.96f;
+        p095 *= 0.95f;
+    }
+    s.v[kScBc1Default] = 1.f - p08;
+    s.v[kScBc1X0] = 1.f - p096;
+    s.v[kScBc2] = 1.f - p095;
+    // Muon: lr = f32(0.04 lrm sqrt(max(1, rows/cols))); momentum 0.85 -> 0.95
+    // over 300 steps (train.mojo:268-271); wd = 0.2 (1 - progress) (train.mojo:272)
+    const double shapes[3][2] = {{(double)c.n_embd, (double)c.n_embd},
+                                 {(double)kMlpExpansion * c.n_embd, (double)c.n_embd},
+                                 {(double)c.n_embd, (double)kMlpExpansion * c.n_embd}};
+    for (int k = 0; k < 3; ++k)
+        s.v[kScMuonLr0 + k] = (float)(0.04 * lrm * muon_lr_factor((int64_t)shapes[k][0], (int64_t)shapes[k][1]));
     double frac = (double)m->adam_step / 300.0;
     if (frac > 1.0) frac = 1.0;
-    const double mu = (1.0 - frac) * 0.85 + frac * 0.95;
-    const double wd = 0.2 * (1.0 - progress);
-    // Muon on every 2-D matrix, grouped by shape (c_q/c_k/c_v/c_proj are
-    // [C, C]; c_fc [4C, C]; mlp_proj [C, 4C]) and run as batched GEMMs.
+    s.v[kScMu] = (float)((1.0 - frac) * 0.85 + frac * 0.95);
+    s.v[kScWd] = (float)(0.2 * (1.0 - progress));
+    return s;
+}
+
+// The optimizer's kernels, all scalars read from m->dsc.
+static int32_t optimizer_kernels(ar_gpt* m) {
+    const ar_gpt_config& c = m->c;
+    auto adam = [&](int64_t ti, int lr_i, int bc1_i, float b1) -> int32_t {
+        const Tensor& t = m->t[ti];
+        return adamw_dev(m->st, m->params + t.offset, m->grads + t.offset, m->adam_m + t.offset,
+                         m->adam_v + t.offset, t.size, m->dsc, lr_i, bc1_i, kScBc2, b1, 0.95f, 1e-10f, 0.0f);
+    };
+    AR_TRY(adam(m->i_lm, kScLrLm, kScBc1Default, 0.8f));
+    AR_TRY(adam(m->i_wte, kScLrWte, kScBc1Default, 0.8f));
+    AR_TRY(adam(m->i_res, kScLrRes, kScBc1Default, 0.8f));
+    AR_TRY(adam(m->i_x0, kScLrX0, kScBc1X0, 0.96f));
+    for (int64_t i = 0; i < c.n_layer; ++i)
+        if (has_ve(c, i)) {
+            AR_TRY(adam(m->i_ve[i], kScLrVe, kScBc1Default, 0.8f));
+            AR_TRY(adam(m->i_gate[i], kScLrGate, kScBc1Default, 0.8f));
+        }
+    // Muon on every 2-D matrix, grouped by shape and run as batched GEMMs.
     std::vector<int64_t> sq, fc, mp;
     for (int64_t i = 0; i < c.n_layer; ++i) {
         sq.push_back(m->i_q[i]);
@@ -770,14 +836,29 @@ extern "C" int32_t ar_gpt_optimizer_step(ar_gpt* m, double progress) {
                 gs[j] = m->grads + t.offset;
                 ms[j] = m->muon_buf + t.offset;
             }
+            MuonDev dev;
+            dev.dsc = m->dsc;
+            dev.lr_i = kScMuonLr0 + muon_class(m, (*grp)[g0]);
+            dev.mu_i = kScMu;
+            dev.wd_i = kScWd;
             const int e = prof_begin(m);
-            AR_TRY(muon_group_step(m->st, ps, gs, ms, n, t0.rows, t0.cols, 0.04, lrm, mu, wd, m->bf16, m->scratch));
+            AR_TRY(muon_group_step(m->st, ps, gs, ms, n, t0.rows, t0.cols, 0.04, 1.0, 0.0, 0.0, m->bf16, m->scratch,
+                                   dev));
             const double smd = (double)(t0.rows < t0.cols ? t0.rows : t0.cols);
             const double lgd = (double)(t0.rows < t0.cols ? t0.cols : t0.rows);
             prof_end(m, e, 6, n * 5.0 * (4.0 * lgd * smd * smd + 2.0 * smd * smd * smd));
         }
     }
     return AR_OK;
+}
+
+// train.mojo:246-281
+extern "C" int32_t ar_gpt_optimizer_step(ar_gpt* m, double progress) {
+    AR_CHECK_ARG(m != nullptr, "gpt_optimizer_step: null model");
+    const StepScalars s = step_scalars(m, progress);
+    set_scalars_k<<<1, 64, 0, m->st>>>(m->dsc, s);
+    AR_TRY(check_launch("gpt_optimizer_step: scalars"));
+    return optimizer_kernels(m);
 }
 
 // train.mojo:231-282
@@ -791,6 +872,73 @@ extern "C" int32_t ar_gpt_train_step(ar_gpt* m, const int64_t* inputs, const int
         if (hipMemcpyAsync(loss_host, m->mean_loss, sizeof(float), hipMemcpyDeviceToHost, m->st) != hipSuccess ||
             hipStreamSynchronize(m->st) != hipSuccess)
             return set_error(AR_EHIP, "gpt_train_step: loss copy failed");
+    }
+    return AR_OK;
+}
+
+// ar_gpt_train_step from a HIP graph: [set scalars] -> [zero_grads, forward,
+// backward without the sort, optimizer kernels].  The scalar node's kernel
+// arguments are replaced before each launch (hipGraphExecKernelNodeSetParams
+// copies them), so the host never races a pending replay.
+extern "C" int32_t ar_gpt_train_step_graph(ar_gpt* m, const int64_t* inputs, const int64_t* targets,
+                                           double progress, float* loss_host) {
+    AR_CHECK_ARG(m && inputs && targets, "gpt_train_step_graph: null pointer");
+    AR_CHECK_ARG(m->st != nullptr, "gpt_train_step_graph: the model's stream must not be the null stream");
+    // events recorded by graph nodes give no usable elapsed times on this runtime
+    AR_CHECK_ARG(!m->prof, "gpt_train_step_graph: disable profiling (ar_gpt_profile) first");
+    StepScalars s = step_scalars(m, progress);
+    void* sargs[] = {&m->dsc, &s};
+    hipKernelNodeParams kp{};
+    kp.func = reinterpret_cast<void*>(set_scalars_k);
+    kp.gridDim = dim3(1);
+    kp.blockDim = dim3(64);
+    kp.sharedMemBytes = 0;
+    kp.kernelParams = sargs;
+    kp.extra = nullptr;
+    if (!m->graph_exec || m->graph_in != inputs || m->graph_tg != targets) {
+        if (m->graph_exec) hipGraphExecDestroy(m->graph_exec);
+        if (m->graph) hipGraphDestroy(m->graph);
+        m->graph_exec = nullptr;
+        m->graph = nullptr;
+        if (hipStreamSynchronize(m->st) != hipSuccess) return set_error(AR_EHIP, "gpt_train_step_graph: sync failed");
+        hipGraph_t body = nullptr;
+        if (hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal) != hipSuccess)
+            return set_error(AR_EHIP, "gpt_train_step_graph: begin capture failed");
+        int32_t r = ar_zero_buffer(AS(m), m->grads, m->nparams);
+        if (!r) r = m->bf16 ? forward_bf16(m, inputs, targets) : forward_fp32(m, inputs, targets);
+        if (!r) r = m->bf16 ? backward_bf16(m, inputs, targets, 1.0f) : backward_fp32(m, inputs, targets, 1.0f);
+        if (!r) r = optimizer_kernels(m);
+        const hipError_t ec = hipStreamEndCapture(m->st, &body);
+        if (r) {
+            if (body) hipGraphDestroy(body);
+            return r;
+        }
+        if (ec != hipSuccess || !body) return set_error(AR_EHIP, "gpt_train_step_graph: capture failed");
+        hipGraph_t g = nullptr;
+        hipGraphNode_t sn = nullptr, cn = nullptr;
+        bool ok = hipGraphCreate(&g, 0) == hipSuccess && hipGraphAddKernelNode(&sn, g, nullptr, 0, &kp) == hipSuccess &&
+                  hipGraphAddChildGraphNode(&cn, g, &sn, 1, body) == hipSuccess;
+        hipGraphDestroy(body);  // the child node holds its own copy
+        hipGraphExec_t ex = nullptr;
+        ok = ok && hipGraphInstantiate(&ex, g, nullptr, nullptr, 0) == hipSuccess;
+        if (!ok) {
+            if (g) hipGraphDestroy(g);
+            return set_error(AR_EHIP, "gpt_train_step_graph: graph build failed");
+        }
+        m->graph = g;
+        m->graph_exec = ex;
+        m->graph_scalars = sn;
+        m->graph_in = inputs;
+        m->graph_tg = targets;
+    } else if (hipGraphExecKernelNodeSetParams(m->graph_exec, m->graph_scalars, &kp) != hipSuccess) {
+        return set_error(AR_EHIP, "gpt_train_step_graph: scalar update failed");
+    }
+    AR_TRY(sort_tokens(m, inputs));
+    if (hipGraphLaunch(m->graph_exec, m->st) != hipSuccess) return set_error(AR_EHIP, "gpt_train_step_graph: launch failed");
+    if (loss_host) {
+        if (hipMemcpyAsync(loss_host, m->mean_loss, sizeof(float), hipMemcpyDeviceToHost, m->st) != hipSuccess ||
+            hipStreamSynchronize(m->st) != hipSuccess)
+            return set_error(AR_EHIP, "gpt_train_step_graph: loss copy failed");
     }
     return AR_OK;
 }

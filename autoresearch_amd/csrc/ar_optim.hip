@@ -38,8 +38,9 @@ inline int64_t align64(int64_t n) { return (n + 63) & ~int64_t(63); }
 
 // X_j = (1-mu) g + mu * (mu buf + (1-mu) g); buf updated (optimizer.mojo:132-146);
 // partial[j][b] = this block's sum of X^2.
-__global__ void nesterov_multi_k(GroupTable t, float* X, int64_t size, float mu, float* partial) {
+__global__ void nesterov_multi_k(GroupTable t, float* X, int64_t size, float mu, const float* dmu, float* partial) {
     __shared__ float red[4];
+    if (dmu) mu = *dmu;
     const int j = blockIdx.y;
     const float* g = t.g[j];
     float* buf = t.m[j];
@@ -74,7 +75,12 @@ __global__ void scale_multi_k(float* X, int64_t size, const float* scale) {
 }
 
 // p -= lr (X + wd p [X p >= 0])  (optimizer.mojo:197-210)
-__global__ void update_multi_k(GroupTable t, const float* X, int64_t size, float lr, float wd) {
+__global__ void update_multi_k(GroupTable t, const float* X, int64_t size, float lr, float wd, const float* dlr,
+                               const float* dwd) {
+    if (dlr) {
+        lr = *dlr;
+        wd = *dwd;
+    }
     const int j = blockIdx.y;
     float* p = t.p[j];
     const float* x = X + (int64_t)j * size;
@@ -87,6 +93,12 @@ __global__ void update_multi_k(GroupTable t, const float* X, int64_t size, float
 
 }  // namespace
 
+// optimizer.mojo:266-268: lr * sqrt(max(1, rows / cols))
+double muon_lr_factor(int64_t rows, int64_t cols) {
+    const double aspect = (double)rows / (double)cols;
+    return aspect > 1.0 ? sqrt(aspect) : 1.0;
+}
+
 int64_t muon_scratch_elems(int64_t rows, int64_t cols, bool bf16, int64_t n) {
     (void)bf16;
     const int64_t size = rows * cols;
@@ -96,7 +108,7 @@ int64_t muon_scratch_elems(int64_t rows, int64_t cols, bool bf16, int64_t n) {
 
 int32_t muon_group_step(hipStream_t st, float* const* params, const float* const* grads, float* const* mbufs, int n,
                         int64_t rows, int64_t cols, double initial_lr, double lrm, double momentum, double wd,
-                        bool bf16, float* scratch) {
+                        bool bf16, float* scratch, const MuonDev& dev) {
     if (n <= 0) return AR_OK;
     if (n > kMuonMaxGroup) return set_error(AR_EINVAL, "muon: group of %d > %d matrices", n, kMuonMaxGroup);
     const int64_t size = rows * cols;
@@ -117,10 +129,10 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
         t.g[j] = grads[j];
         t.m[j] = mbufs[j];
     }
-    const double aspect = (double)rows / (double)cols;
-    const float lr = (float)(initial_lr * lrm * (aspect > 1.0 ? sqrt(aspect) : 1.0));
+    const float lr = (float)(initial_lr * lrm * muon_lr_factor(rows, cols));
     const dim3 eg(kNormBlocks, n);
-    nesterov_multi_k<<<eg, 256, 0, st>>>(t, X, size, (float)momentum, partial);
+    nesterov_multi_k<<<eg, 256, 0, st>>>(t, X, size, (float)momentum, dev.dsc ? dev.dsc + dev.mu_i : nullptr,
+                                         partial);
     norm_finish_k<<<1, n, 0, st>>>(scale, partial);
     scale_multi_k<<<eg, 256, 0, st>>>(X, size, scale);
     int32_t r = check_launch("muon: normalise");
@@ -146,7 +158,8 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
         if (r) return r;
         if ((r = ar_scale_add(s, X, X, Y, ca, 1.0f, n * size))) return r;
     }
-    update_multi_k<<<eg, 256, 0, st>>>(t, X, size, lr, (float)wd);
+    update_multi_k<<<eg, 256, 0, st>>>(t, X, size, lr, (float)wd, dev.dsc ? dev.dsc + dev.lr_i : nullptr,
+                                       dev.dsc ? dev.dsc + dev.wd_i : nullptr);
     return check_launch("muon: update");
 }
 

@@ -12,11 +12,12 @@
 //     the BPE tokenizer, which are not part of this build;
 //   * the next batch is packed on the host while the GPU runs forward and
 //     backward, into the other of two device token buffers;
-//   * --graph replays the whole step from a HIP graph (ar_gpt_graph_step).
+//   * --graph replays the whole step from a HIP graph (ar_gpt_train_step_graph,
+//     bit-identical to the eager step).
 //
 // Usage: ar_train [--data DIR] [--tokenizer DIR] [--vocab V] [--depth D]
 //                 [--batch B] [--seq T] [--fp32] [--graph] [--fake-dt SEC]
-//   TRAIN_TIME_BUDGET=<seconds> overrides the 300 s budget (train.mojo:213-221).
+//   TRAIN_TIME_BUDGET=<seconds> overrides the 300 s budget (train.mojo:211-221).
 //   --fake-dt replaces each step's measured time in the schedule (tests).
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -37,7 +38,7 @@ constexpr int kTimeBudget = 300;     // config.mojo:61
 constexpr int kDepth = 8;            // config.mojo:62
 constexpr int kMaxSeqLen = 2048;     // config.mojo:60
 constexpr int kVocab = 8192;         // prepare.py:45
-constexpr int kWarmupSteps = 10;     // train.mojo:293-295: steps 0..10 untimed
+constexpr int kWarmupSteps = 10;     // train.mojo:291-293: steps 0..10 untimed
 
 double now_s() {
     return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
@@ -188,27 +189,38 @@ int main(int argc, char** argv) {
     int64_t step = 0;
     for (;;) {
         const double t0 = now_s();
-        CHECK(ar_gpt_zero_grads(m), "zero_grads");
-        CHECK(ar_gpt_forward(m, d_tok[cur][0], d_tok[cur][1], nullptr), "forward");
-        CHECK(ar_gpt_backward(m, d_tok[cur][0], d_tok[cur][1], 1.0f), "backward");
-        // the next batch is packed while the GPU works
-        int64_t next_epoch = epoch;
-        CHECK(ar_loader_next(train, h_in, h_tg, &next_epoch), "load batch");
-        float loss32 = 0.f;
-        HIPCHECK(hipMemcpyAsync(&loss32, ar_gpt_mean_loss(m), sizeof(float), hipMemcpyDeviceToHost, st), "loss");
-        HIPCHECK(hipStreamSynchronize(st), "step");
-        const double loss = loss32;
-        upload(cur ^ 1);
-        epoch = next_epoch;
-
+        // progress depends on the time of the finished steps only, so it is
+        // known before this step's forward (train.mojo:247-250)
         double progress = training_time / (double)time_budget;
         if (progress > 1.0) progress = 1.0;
         const double lrm = lr_multiplier(progress);
-        CHECK(ar_gpt_optimizer_step(m, progress), "optimizer");
-        HIPCHECK(hipStreamSynchronize(st), "optimizer");
-        cur ^= 1;
+        int64_t next_epoch = epoch;
+        float loss32 = 0.f;
+        if (a.graph) {
+            // one graph replay (zero_grads -> forward -> backward -> AdamW + Muon)
+            // on the fixed token buffers; the next batch is packed meanwhile
+            CHECK(ar_gpt_train_step_graph(m, d_tok[0][0], d_tok[0][1], progress, nullptr), "graph step");
+            CHECK(ar_loader_next(train, h_in, h_tg, &next_epoch), "load batch");
+            HIPCHECK(hipMemcpyAsync(&loss32, ar_gpt_mean_loss(m), sizeof(float), hipMemcpyDeviceToHost, st), "loss");
+            HIPCHECK(hipStreamSynchronize(st), "step");
+            upload(0);
+        } else {
+            CHECK(ar_gpt_zero_grads(m), "zero_grads");
+            CHECK(ar_gpt_forward(m, d_tok[cur][0], d_tok[cur][1], nullptr), "forward");
+            CHECK(ar_gpt_backward(m, d_tok[cur][0], d_tok[cur][1], 1.0f), "backward");
+            // the next batch is packed while the GPU works
+            CHECK(ar_loader_next(train, h_in, h_tg, &next_epoch), "load batch");
+            HIPCHECK(hipMemcpyAsync(&loss32, ar_gpt_mean_loss(m), sizeof(float), hipMemcpyDeviceToHost, st), "loss");
+            HIPCHECK(hipStreamSynchronize(st), "step");
+            upload(cur ^ 1);
+            CHECK(ar_gpt_optimizer_step(m, progress), "optimizer");
+            HIPCHECK(hipStreamSynchronize(st), "optimizer");
+            cur ^= 1;
+        }
+        const double loss = loss32;
+        epoch = next_epoch;
 
-        if (isnan(loss) || loss > 100.0) {  // train.mojo:283-286
+        if (isnan(loss) || loss > 100.0) {  // train.mojo:285-287
             printf("FAIL: loss = %s\n", f64(loss).c_str());
             return 0;
         }

@@ -135,6 +135,14 @@ class GPT:
         check(self.lib.ar_gpt_train_step(self.h, _ptr(inputs), _ptr(targets), progress, None), "gpt_train_step")
         return None
 
+    def train_step_graph(self, inputs, targets, progress: float = 0.0, sync_loss: bool = True):
+        """train_step replayed from a HIP graph (same buffers every call; the
+        model must have been created on a non-default stream)."""
+        loss = ct.c_float()
+        check(self.lib.ar_gpt_train_step_graph(self.h, _ptr(inputs), _ptr(targets), progress,
+                                               ct.byref(loss) if sync_loss else None), "gpt_train_step_graph")
+        return loss.value if sync_loss else None
+
 
 def _ptr(t: torch.Tensor) -> int:
     if not (t.is_cuda and t.dtype == torch.int64 and t.is_contiguous()):

@@ -9,13 +9,17 @@ fp32 master weights.  Token ids are Zipf(1.1) over the vocabulary from seed 0
 (synthetic; no dataset).  Weights follow the reference init (seed 42).
 
 A "step" = zero_grads -> forward -> backward -> AdamW + Muon update
-(train.mojo:231-282), all on the GPU through the C ABI.  W untimed warm-up
+(train.mojo:231-282), all on the GPU through the C ABI (--graph: replayed
+from a HIP graph, ar_gpt_train_step_graph, bit-identical).  W untimed warm-up
 steps, then exactly K steps between two device synchronisations.
 
 Prints ONE JSON line.  `roofline` describes the dominant kernel class
-(largest share of step time), measured with HIP events bracketing each of its
-launches on the model's stream during the timed steps; `cpu_baseline` times
-the fp32 CPU oracle on this host on a bounded sample of the same workload.
+(largest share of step time): HIP events bracket each GEMM / attention / Muon
+launch on the model's stream during P further profiled steps, which run the
+same kernels on the same stream right after the timed ones (events are kept
+out of the timed steps, where they would add ~2 % of launch overhead);
+`cpu_baseline` times the fp32 CPU oracle on this host on a bounded sample of
+the same workload.
 """
 from __future__ import annotations
 
@@ -93,6 +97,8 @@ def main(argv=None) -> int:
     ap.add_argument("--vocab", type=int, default=8192)
     ap.add_argument("--precision", choices=["bf16", "fp32"], default="bf16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", action="store_true", help="replay the step from a HIP graph")
+    ap.add_argument("--prof-steps", type=int, default=5, help="profiled steps after the timed ones")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the training step is single-GPU in the reference; "
@@ -106,6 +112,8 @@ def main(argv=None) -> int:
     B, T, V = a.batch, a.seq, a.vocab
     prec = BF16 if a.precision == "bf16" else FP32
     torch.cuda.set_device(0)
+    stream = torch.cuda.Stream()  # a stream of its own (graph capture cannot use the null stream)
+    torch.cuda.set_stream(stream)
     toks = zipf_tokens(B * (T + 1), V, 1.1, 0).reshape(B, T + 1)
     x = torch.from_numpy(np.ascontiguousarray(toks[:, :-1]).ravel()).cuda()
     y = torch.from_numpy(np.ascontiguousarray(toks[:, 1:]).ravel()).cuda()
@@ -113,31 +121,36 @@ def main(argv=None) -> int:
     m.init_weights(42)
     torch.cuda.synchronize()
     print(f"[bench] model ready: L={cfg.n_layer} C={cfg.n_embd} H={cfg.n_head} V={V} B={B} T={T} "
-          f"{a.precision}", file=sys.stderr, flush=True)
+          f"{a.precision} {'graph' if a.graph else 'eager'}", file=sys.stderr, flush=True)
+    step = m.train_step_graph if a.graph else m.train_step
+    from autoresearch_amd._lib import check
 
     for i in range(a.warmup):
-        m.train_step(x, y, 0.0, sync_loss=False)
+        step(x, y, 0.0, sync_loss=False)
     torch.cuda.synchronize()
     print(f"[bench] warmup done ({a.warmup} steps)", file=sys.stderr, flush=True)
 
-    # Timed region (profiling events on the dominant kernel classes).
-    m.lib.ar_gpt_profile(m.h, 1)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(a.steps):
-        m.train_step(x, y, 0.0, sync_loss=False)
+        step(x, y, 0.0, sync_loss=False)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms = (t1 - t0) * 1e3 / a.steps
-    loss = float(torch.tensor(0.0))
+
+    # Per-class timing: HIP events around every GEMM / attention / Muon launch
+    # of P eager steps on the same stream.
     import ctypes as ct
+    check(m.lib.ar_gpt_profile(m.h, 1), "gpt_profile")
+    for i in range(a.prof_steps):
+        m.train_step(x, y, 0.0, sync_loss=False)
     cls_stats = []
+    per = max(a.prof_steps, 1)
     for c in range(len(CLASS_NAMES)):
         t, n, f = ct.c_double(), ct.c_int64(), ct.c_double()
-        m.lib.ar_gpt_profile_read(m.h, c, ct.byref(t), ct.byref(n), ct.byref(f))
-        cls_stats.append((CLASS_NAMES[c], t.value, n.value, f.value))
-    m.lib.ar_gpt_profile(m.h, 0)
-    lbuf = ct.c_float()
+        check(m.lib.ar_gpt_profile_read(m.h, c, ct.byref(t), ct.byref(n), ct.byref(f)), "gpt_profile_read")
+        cls_stats.append((CLASS_NAMES[c], t.value / per, n.value // per, f.value / per))
+    check(m.lib.ar_gpt_profile(m.h, 0), "gpt_profile")
     torch.cuda.synchronize()
     loss = m.forward(x, y)
     print(f"[bench] timed {a.steps} steps: {ms:.2f} ms/step, loss after = {loss:.4f}", file=sys.stderr, flush=True)
@@ -153,14 +166,15 @@ def main(argv=None) -> int:
     peak = PEAK_BF16_TFLOPS if prec == BF16 else PEAK_FP32_TFLOPS
     mfma_util = flops / (ms / 1e3) / (peak * 1e12)
 
+    # per-step figures: (name, ms, launches, flops)
     dom = max(cls_stats, key=lambda s: s[1])
     name, t_ms, n, f = dom
     achieved = (f / (t_ms / 1e3)) / 1e12 if t_ms > 0 else 0.0
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                 "frac": round(achieved / peak, 4), "traffic": None, "kernel": name,
-                "launches_per_step": n // a.steps, "avg_launch_ms": round(t_ms / max(n, 1), 4),
-                "share_of_step": round(t_ms / a.steps / ms, 4)}
-    breakdown = {s[0]: {"ms_per_step": round(s[1] / a.steps, 3),
+                "launches_per_step": n, "avg_launch_ms": round(t_ms / max(n, 1), 4),
+                "share_of_step": round(t_ms / ms, 4)}
+    breakdown = {s[0]: {"ms_per_step": round(s[1], 3),
                         "tflops": round((s[3] / (s[1] / 1e3)) / 1e12, 1) if s[1] > 0 else 0.0}
                  for s in cls_stats}
 
@@ -173,6 +187,7 @@ def main(argv=None) -> int:
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": a.precision, "data": "synthetic Zipf(1.1) token ids, seed 0",
+        "step_mode": "hip_graph" if a.graph else "eager",
         "config": {"workload": f"config 4: full training step depth{cfg.n_layer} d{cfg.n_embd} "
                                f"H{cfg.n_head}x{cfg.head_dim} V{V} T{T} B{B} SSSL, AdamW+Muon",
                    "global_batch": B, "seq_len": T, "parallelism": "single GPU"},

@@ -265,6 +265,16 @@ int32_t ar_gpt_optimizer_step(ar_gpt* model, double progress);
 /* train.mojo:231-282: zero_grads -> forward -> backward(1.0) -> optimizer */
 int32_t ar_gpt_train_step(ar_gpt* model, const int64_t* inputs, const int64_t* targets, double progress,
                           float* loss_host);
+/* ar_gpt_train_step replayed from a HIP graph (the "HIP-graph capture of the
+ * whole step" of the training driver; no counterpart in the reference, whose
+ * step is ~1,700 separate launches).  Same results as ar_gpt_train_step,
+ * bit for bit.  The graph records inputs / targets: pass the same device
+ * buffers every call (new pointers re-record it).  The token-id sort of the
+ * embedding backward runs eagerly before each replay.  The model's stream
+ * must not be the null stream, and profiling (ar_gpt_profile) must be off.
+ * loss_host as in ar_gpt_train_step. */
+int32_t ar_gpt_train_step_graph(ar_gpt* model, const int64_t* inputs, const int64_t* targets, double progress,
+                                float* loss_host);
 
 /* Per-kernel-class timing of the step (no counterpart in the reference: the
  * measurement hook behind bench.py's roofline figure).  When enabled, every

@@ -19,6 +19,7 @@ DRIVER = os.path.join(ROOT, "autoresearch_amd", "ar_train")
 STEP_RE = re.compile(r"^step (\d+)  \| (\d+) % \|  loss: (\S+)  \| lrm: (\S+)  \| dt: (\d+) ms  \| "
                      r"epoch: (\d+)  \| rem: (\d+) s$")
 V, DEPTH, B, T, DT, BUDGET = 512, 2, 2, 64, 0.05, 1
+_LOSSES = {}  # mode -> logged losses (graph replay must match the eager step exactly)
 
 
 def _make_data(d):
@@ -39,13 +40,14 @@ def _make_data(d):
     data.write_token_bytes(os.path.join(d, "token_bytes.bin"), tb)
 
 
-def test_driver_schedule_log_and_summary(tmp_path):
+@pytest.mark.parametrize("graph", [False, True])
+def test_driver_schedule_log_and_summary(tmp_path, graph):
     assert os.path.exists(DRIVER), "build the driver first (python -m autoresearch_amd.build)"
     d = str(tmp_path)
     _make_data(d)
     env = dict(os.environ, TRAIN_TIME_BUDGET=str(BUDGET))
     cmd = [DRIVER, "--data", d, "--tokenizer", d, "--vocab", str(V), "--depth", str(DEPTH), "--batch", str(B),
-           "--seq", str(T), "--fake-dt", str(DT)]
+           "--seq", str(T), "--fake-dt", str(DT)] + (["--graph"] if graph else [])
     print("running", " ".join(cmd), flush=True)
     r = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=180)
     print(r.stdout[-3000:], r.stderr[-2000:], flush=True)
@@ -81,6 +83,9 @@ def test_driver_schedule_log_and_summary(tmp_path):
         losses.append(float(loss))
     assert all(math.isfinite(x) for x in losses)
     assert losses[-1] < losses[0]  # the debiased smoothed loss falls
+    _LOSSES[graph] = losses
+    if len(_LOSSES) == 2:
+        assert _LOSSES[True] == _LOSSES[False]
     # summary block (train.mojo:331-339)
     summ = dict(l.split(":", 1) for l in lines[lines.index("---") + 1:])
     assert [k for k in summ] == ["val_bpb", "training_seconds", "total_seconds", "startup_seconds",
