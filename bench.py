@@ -63,6 +63,17 @@ def step_flops(L, C, V, B, T, H, hd, windows, mats) -> float:
     return gemm + attn + muon
 
 
+def measured_traffic(cls: str, a, bf16: bool):
+    """HBM bytes per launch of kernel class `cls` from the committed counter
+    passes (rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled by a 1 GiB copy; see
+    profiles/counters_config4_bf16.md), for the workload those passes ran."""
+    path = os.path.join(ROOT, "profiles", "traffic_config4_bf16.json")
+    if not (bf16 and (a.depth, a.batch, a.seq, a.vocab) == (8, 32, 2048, 8192) and os.path.exists(path)):
+        return None
+    with open(path) as f:
+        return json.load(f)["classes"].get(cls)
+
+
 def cpu_baseline(cfg, T, V, steps_tokens_B: int) -> dict:
     """fp32 CPU oracle on this host: one forward+backward at B=1 (2048 tokens)
     and one optimizer step, extrapolated to the B=32 step."""
@@ -99,6 +110,8 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph", action="store_true", help="replay the step from a HIP graph")
     ap.add_argument("--prof-steps", type=int, default=5, help="profiled steps after the timed ones")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run one device copy of MIB MiB (calibrates rocprofv3 byte counters) and exit")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the training step is single-GPU in the reference; "
@@ -107,6 +120,16 @@ def main(argv=None) -> int:
 
     import torch
     from autoresearch_amd.model import BF16, FP32, GPT, GPTConfig
+
+    if a.copy_probe:
+        n = a.copy_probe * (1 << 20) // 4
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty(n, device="cuda")
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_read": 4 * n, "copy_probe_bytes_written": 4 * n}), flush=True)
+        return 0
 
     cfg = GPTConfig.default(a.vocab, a.depth)
     B, T, V = a.batch, a.seq, a.vocab
@@ -171,7 +194,7 @@ def main(argv=None) -> int:
     name, t_ms, n, f = dom
     achieved = (f / (t_ms / 1e3)) / 1e12 if t_ms > 0 else 0.0
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(achieved / peak, 4), "traffic": None, "kernel": name,
+                "frac": round(achieved / peak, 4), "traffic": measured_traffic(name, a, prec == BF16), "kernel": name,
                 "launches_per_step": n, "avg_launch_ms": round(t_ms / max(n, 1), 4),
                 "share_of_step": round(t_ms / ms, 4)}
     breakdown = {s[0]: {"ms_per_step": round(s[1], 3),
