@@ -35,6 +35,8 @@
 //     (deterministic; the reference's single-block loop over M is serial).
 #include "ar_internal.hpp"
 
+#include <type_traits>
+
 using namespace ar;
 
 namespace {
@@ -433,6 +435,248 @@ __global__ void splitk_reduce_k(TC* C, const float* partial, int64_t M, int64_t 
     }
 }
 
+// ---------------------------------------------------------------------
+// Persistent GEMM for bf16 operands in memory (the bf16 training step).
+//
+// One 512-thread workgroup per CU walks a strided list of 256x256 output
+// tiles (x reduction splits).  Every k-tile (BK = 64) of A and B goes from
+// global memory straight into LDS with 16-byte global_load_lds (no VGPR
+// staging, no ds_write), two stages deep; the stream of k-tiles runs on
+// across tile boundaries, so the next tile's first loads are in flight while
+// the current tile's epilogue drains.  8 waves of 128 x 64 as in gemm_k.
+//   K-major operand tile: 256 rows x 8 16-byte units, unit c of row r at
+//     slot r*8 + (c ^ ((r >> 1) & 7)): each 16-lane phase of a fragment read
+//     (rows r0..r0+15, one unit) covers all 64 banks once.
+//   MN-major operand tile: 64 k-rows x 32 units, unit c of k-row k at slot
+//     k*32 + (c ^ tr_swz(k)), read with tr_frag as in gemm_k.
+// A lane's DMA slot is fixed (wave-instruction j of wave w fills slots
+// (8j + w)*64 + lane), so the swizzle is applied to the global address the
+// lane fetches.  The epilogue stages 16-row half strips (fp32) in a separate
+// 32 KB region.  Shapes: M, N % 256, K (per split) % 64, lda/ldb % 8.
+constexpr int kPkThreads = 512, kPkBK = 64, kPkStage = 2 * 256 * kPkBK * 2;  // bytes per stage (A + B)
+constexpr int kPkLds = 2 * kPkStage + 8 * 16 * 64 * 4;                      // 160 KB
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 16, "vmcnt");
+    __builtin_amdgcn_s_waitcnt(N | 0x0F70);  // vmcnt(N), expcnt / lgkmcnt not waited
+}
+
+// Issues the DMA of one operand tile (4 wave-instructions per thread).
+template <bool KMAJ>
+__device__ __forceinline__ void pk_dma(unsigned char* dst, const bf16* g, int64_t ld, int64_t row0, int64_t k0,
+                                       int wave, int lane) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int slot = (j * 8 + wave) * 64 + lane;
+        const bf16* src;
+        if constexpr (KMAJ) {
+            const int r = slot >> 3, c = (slot & 7) ^ ((r >> 1) & 7);
+            src = g + (row0 + r) * ld + k0 + c * 8;
+        } else {
+            const int k = slot >> 5, c = (slot & 31) ^ tr_swz(k);
+            src = g + (k0 + k) * ld + row0 + c * 8;
+        }
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(dst + (j * 8 + wave) * 1024),
+                                         16, 0, 0);
+    }
+}
+
+// Work item -> (split z, tile_m, tile_n); each XCD (workgroups are dispatched
+// round-robin over 8) owns a contiguous run of items.
+__device__ __forceinline__ void pk_item(int64_t lin, int64_t items, int64_t tiles_n, int64_t tiles_mn, int64_t& z,
+                                        int64_t& tm, int64_t& tn) {
+    int64_t id = lin;
+    if (items % 8 == 0 && gridDim.x % 8 == 0) id = (lin % 8) * (items / 8) + lin / 8;
+    z = id / tiles_mn;
+    const int64_t r = id % tiles_mn;
+    tm = r / tiles_n;
+    tn = r % tiles_n;
+}
+
+template <bool AK, bool BKM, typename TC, int EPI>
+__global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, const bf16* B, int64_t M, int64_t N,
+                                                     int64_t lda, int64_t ldb, int64_t ldc, int64_t kps,
+                                                     int64_t splits, float* partial, const void* aux, void* aux_out,
+                                                     float cap) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    constexpr int OPB = kPkStage / 2;
+    const int lane = threadIdx.x % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int wm = wave >> 2, wn = wave & 3;
+    const int64_t tiles_n = N / 256, tiles_mn = (M / 256) * tiles_n, items = tiles_mn * splits;
+    const int64_t grid = gridDim.x, b = blockIdx.x;
+    const int nk = (int)(kps / kPkBK);
+    const int nmine = (int)((items - b + grid - 1) / grid);
+    const int G = nmine * nk;  // k-tiles this workgroup streams
+
+    auto issue = [&](int g) {
+        const int i = g / nk, kt = g - i * nk;
+        int64_t z, tm, tn;
+        pk_item(i * grid + b, items, tiles_n, tiles_mn, z, tm, tn);
+        unsigned char* st = smem_raw + (g & 1) * kPkStage;
+        const int64_t k0 = z * kps + (int64_t)kt * kPkBK;
+        pk_dma<AK>(st, A, lda, tm * 256, k0, wave, lane);
+        pk_dma<BKM>(st + OPB, B, ldb, tn * 256, k0, wave, lane);
+    };
+
+    // K-major fragment byte offsets per k-step (row swizzle depends on the lane only)
+    const int r32 = lane & 31, hi = lane >> 5;
+    int aoff[4], boff[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const int ra = wm * 128 + r32, rb = wn * 64 + r32;
+        aoff[ks] = (ra * 8 + ((2 * ks + hi) ^ ((ra >> 1) & 7))) * 16;
+        boff[ks] = (rb * 8 + ((2 * ks + hi) ^ ((rb >> 1) & 7))) * 16;
+    }
+
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+    if (G > 0) issue(0);
+    float* const strip = reinterpret_cast<float*>(smem_raw + 2 * kPkStage) + wave * 16 * 64;
+
+    for (int g = 0; g < G; ++g) {
+        // vmcnt(0): this wave's DMA of k-tile g (and anything older) has
+        // landed; the barrier then publishes every wave's part and retires
+        // all reads of the stage that the next DMA overwrites.
+        vm_wait<0>();
+        __builtin_amdgcn_s_barrier();
+        if (g + 1 < G) issue(g + 1);
+        const unsigned char* sa = smem_raw + (g & 1) * kPkStage;
+        const unsigned char* sb = sa + OPB;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            bf16x8 fa[4], fb[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (AK) fa[i] = *reinterpret_cast<const bf16x8*>(sa + aoff[ks] + i * 4096);
+                else fa[i] = tr_frag<256>(reinterpret_cast<const bf16*>(sa), wm * 128 + i * 32, ks, lane);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if constexpr (BKM) fb[j] = *reinterpret_cast<const bf16x8*>(sb + boff[ks] + j * 4096);
+                else fb[j] = tr_frag<256>(reinterpret_cast<const bf16*>(sb), wn * 64 + j * 32, ks, lane);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        }
+        const int it = g / nk;
+        if (g - it * nk != nk - 1) continue;
+
+        // Epilogue of item `it`: per 32-row MFMA block i, two 16-row half
+        // strips; lane (t, lane/16, lane%16) owns 4 consecutive columns.
+        int64_t z, tm, tn;
+        pk_item(it * grid + b, items, tiles_n, tiles_mn, z, tm, tn);
+        const int64_t row0 = tm * 256 + wm * 128, col0 = tn * 256 + wn * 64;
+        constexpr bool PRE = EPI == EPI_ACCUM || EPI == EPI_ADD || EPI == EPI_RELU2_BWD;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                float4 pre[PRE ? 4 : 1];
+                if constexpr (PRE) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const int64_t o = (row0 + i * 32 + h * 16 + t * 4 + (lane >> 4)) * ldc + col0 + (lane & 15) * 4;
+                        if constexpr (EPI == EPI_ACCUM) pre[t] = ld4(C + o);
+                        else if constexpr (EPI == EPI_ADD) pre[t] = ld4(static_cast<const float*>(aux) + o);
+                        else pre[t] = ld4(static_cast<const TC*>(aux) + o);
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int vv = 0; vv < 8; ++vv) {
+                        const int v = h * 8 + vv;
+                        const int r = acc_row(v, lane) - 16 * h;
+                        strip[r * 64 + ((j * 32 + r32) ^ (((r >> 2) & 1) << 5))] = acc[i][j][v];
+                    }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int r = t * 4 + (lane >> 4), c4 = (lane & 15) * 4;
+                    const float4 x = *reinterpret_cast<const float4*>(strip + r * 64 + (c4 ^ (((r >> 2) & 1) << 5)));
+                    const int64_t row = row0 + i * 32 + h * 16 + r, col = col0 + c4;
+                    const int64_t o = row * ldc + col;
+                    if constexpr (EPI == EPI_PARTIAL) {
+                        *reinterpret_cast<float4*>(partial + (z * M + row) * N + col) = x;
+                    } else if constexpr (EPI == EPI_STORE) {
+                        st4(C + o, x);
+                    } else if constexpr (EPI == EPI_ACCUM || EPI == EPI_ADD) {
+                        st4(C + o, add4(pre[PRE ? t : 0], x));
+                    } else if constexpr (EPI == EPI_RELU2) {
+                        const float4 r2 = make_float4(x.x > 0.f ? x.x * x.x : 0.f, x.y > 0.f ? x.y * x.y : 0.f,
+                                                      x.z > 0.f ? x.z * x.z : 0.f, x.w > 0.f ? x.w * x.w : 0.f);
+                        st4(C + o, x);
+                        st4(static_cast<TC*>(aux_out) + o, r2);
+                    } else if constexpr (EPI == EPI_SOFTCAP) {
+                        st4(C + o, make_float4(cap * tanhf(x.x / cap), cap * tanhf(x.y / cap),
+                                               cap * tanhf(x.z / cap), cap * tanhf(x.w / cap)));
+                    } else if constexpr (EPI == EPI_RELU2_BWD) {
+                        const float4 hv = pre[PRE ? t : 0];
+                        st4(C + o, make_float4(hv.x > 0.f ? 2.f * hv.x * x.x : 0.f, hv.y > 0.f ? 2.f * hv.y * x.y : 0.f,
+                                               hv.z > 0.f ? 2.f * hv.z * x.z : 0.f, hv.w > 0.f ? 2.f * hv.w * x.w : 0.f));
+                    }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+        }
+    }
+}
+
+// Vector form of splitk_reduce_k (N % 4 == 0, ldc % 4 == 0, 16-byte aligned
+// partial / C): four columns per thread, the split partials' loads issued
+// eight at a time ahead of their in-order adds (same order as the scalar form).
+template <typename TC>
+__global__ __launch_bounds__(256) void splitk_reduce4_k(TC* C, const float* partial, int64_t M, int64_t N,
+                                                        int64_t ldc, int64_t splits, int accumulate) {
+    const int64_t mn = M * N, n4 = mn / 4;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n4; j += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t i = j * 4, r = i / N, c = i % N;
+        float4 s = accumulate ? ld4(C + r * ldc + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        int64_t z = 0;
+        for (; z + 8 <= splits; z += 8) {
+            float4 p[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) p[u] = *reinterpret_cast<const float4*>(partial + (z + u) * mn + i);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s = add4(s, p[u]);
+        }
+        for (; z < splits; ++z) s = add4(s, *reinterpret_cast<const float4*>(partial + z * mn + i));
+        st4(C + r * ldc + c, s);
+    }
+}
+
+template <typename TC>
+static void splitk_reduce(hipStream_t st, TC* C, const float* partial, int64_t M, int64_t N, int64_t ldc,
+                          int64_t splits, bool accumulate, int64_t batch, int64_t sC) {
+    const bool vec = batch == 1 && N % 4 == 0 && ldc % 4 == 0 &&
+                     ((reinterpret_cast<uintptr_t>(C) | reinterpret_cast<uintptr_t>(partial)) & 15) == 0;
+    if (vec)
+        splitk_reduce4_k<TC><<<flat_grid(M * N / 4, 256), 256, 0, st>>>(C, partial, M, N, ldc, splits,
+                                                                        accumulate ? 1 : 0);
+    else
+        splitk_reduce_k<TC><<<flat_grid(M * N * batch, 256 * 4), 256, 0, st>>>(C, partial, M, N, ldc, splits,
+                                                                               accumulate ? 1 : 0, batch, sC);
+}
+
 template <bool BF16, typename TL>
 constexpr size_t lds_bytes() {
     using MM = Mfma<BF16>;
@@ -498,8 +742,77 @@ static int32_t gemm_launch_t(hipStream_t st, TC* C, const TA* A, const TB* B, in
     if (!partial) return set_error(AR_EINVAL, "%s: split-K scratch missing", nm);
     AR_GK(EPI_PARTIAL);
 #undef AR_GK
-    splitk_reduce_k<TC><<<flat_grid(M * N * batch, 256 * 4), 256, 0, st>>>(C, partial, M, N, ldc, splits,
-                                                                           accumulate ? 1 : 0, batch, sC);
+    splitk_reduce<TC>(st, C, partial, M, N, ldc, splits, accumulate, batch, sC);
+    return check_launch(nm);
+}
+
+// ---- persistent bf16-operand GEMM (gemm_pk) ----
+// GEMM-space shapes it takes: whole 256 x 256 tiles, 64-deep k-tiles, 16-byte
+// aligned operands whose rows start on 16-byte boundaries.
+static bool pk_shape(int64_t gm, int64_t gn, int64_t gk) {
+    return gm > 0 && gn > 0 && gk > 0 && gm % 256 == 0 && gn % 256 == 0 && gk % kPkBK == 0;
+}
+static bool pk_ok(int64_t gm, int64_t gn, int64_t gk, int64_t lda, int64_t ldb, int64_t ldc, const void* A,
+                  const void* B, const void* C) {
+    return pk_shape(gm, gn, gk) && lda % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 &&
+           ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C)) & 15) == 0;
+}
+// Reduction splits: powers of two (each split a whole number of k-tiles and
+// at least 4 of them) until there are >= 256 work items.
+static int64_t pk_splits(int64_t tiles, int64_t gk) {
+    int64_t s = 1;
+    while (tiles * s < 256 && gk % (2 * s * kPkBK) == 0 && gk / (2 * s) >= 4 * kPkBK) s *= 2;
+    return s;
+}
+static int pk_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// C (+)= A . B^T in GEMM space with gemm_pk (operands checked by pk_ok).
+// epi < 0: STORE / ACCUM by `accumulate`, split over the reduction when
+// splits > 1 (fp32 partials in `partial`, then an in-order reduce).
+template <bool AK, bool BKM, typename TC>
+static int32_t pk_launch(hipStream_t st, TC* C, const bf16* A, const bf16* B, int64_t gm, int64_t gn, int64_t gk,
+                         int64_t lda, int64_t ldb, int64_t ldc, bool accumulate, int64_t splits, float* partial,
+                         int epi, const void* aux, void* aux_out, float cap, const char* nm) {
+    if (splits < 1) splits = 1;
+    if (gk % (splits * kPkBK) != 0) return set_error(AR_EINVAL, "%s: split %lld does not divide K", nm, (long long)splits);
+    const int64_t kps = gk / splits, items = (gm / 256) * (gn / 256) * splits;
+    const int cus = pk_cus();
+    const unsigned grid = (unsigned)(items < cus ? items : cus);
+#define AR_PK(E)                                                                                                      do {                                                                                                                  static bool attr_set = false;                                                                                     if (!attr_set) {                                                                                                      if (hipFuncSetAttribute((const void*)gemm_pk<AK, BKM, TC, E>,                                                                              hipFuncAttributeMaxDynamicSharedMemorySize, kPkLds) != hipSuccess)                            return set_error(AR_EHIP, "%s: cannot set the LDS size", nm);                                                 attr_set = true;                                                                                              }                                                                                                                 gemm_pk<AK, BKM, TC, E><<<grid, kPkThreads, kPkLds, st>>>(C, A, B, gm, gn, lda, ldb, ldc, kps, splits,                                                                       partial, aux, aux_out, cap);                         } while (0)
+    if (epi >= 0) {
+        if (splits != 1) return set_error(AR_EINVAL, "%s: fused epilogues take no reduction split", nm);
+        if constexpr (AK) {  // fused epilogues exist for the NT and NN layouts only
+            switch (epi) {
+                case EPI_ADD: AR_PK(EPI_ADD); break;
+                case EPI_RELU2: AR_PK(EPI_RELU2); break;
+                case EPI_SOFTCAP: AR_PK(EPI_SOFTCAP); break;
+                case EPI_RELU2_BWD: AR_PK(EPI_RELU2_BWD); break;
+                default: return set_error(AR_EINVAL, "%s: bad epilogue %d", nm, epi);
+            }
+            return check_launch(nm);
+        } else {
+            return set_error(AR_EINVAL, "%s: no fused epilogue for this layout", nm);
+        }
+    }
+    if (splits == 1) {
+        if (accumulate) AR_PK(EPI_ACCUM);
+        else AR_PK(EPI_STORE);
+        return check_launch(nm);
+    }
+    if (!partial) return set_error(AR_EINVAL, "%s: split-K scratch missing", nm);
+    AR_PK(EPI_PARTIAL);
+#undef AR_PK
+    splitk_reduce<TC>(st, C, partial, gm, gn, ldc, splits, accumulate, 1, 0);
     return check_launch(nm);
 }
 
@@ -532,14 +845,27 @@ static void gemm_space(int layout, int64_t M, int64_t N, int64_t K, int64_t& gm,
     else { gm = N; gn = K; gk = M; }
 }
 
-int64_t gemm_auto_splits(int layout, bool bf16, int64_t M, int64_t N, int64_t K) {
-    if (layout != 2) return 1;
-    int64_t gm, gn, gk, kps;
-    gemm_space(layout, M, N, K, gm, gn, gk);
+// Split count of gemm_k's automatic choice for a TN call.
+static int64_t gemm_k_splits(bool bf16, int64_t gm, int64_t gn, int64_t gk) {
+    int64_t kps;
     const bool large = use_large(gm, gn, gk, 1);
     const int64_t tiles = large ? ((gm + 255) / 256) * ((gn + 255) / 256) : ((gm + 127) / 128) * ((gn + 127) / 128);
     const int64_t target = large ? 256 : 512;
     return bf16 ? choose_splits<true>(tiles, gk, 0, kps, target) : choose_splits<false>(tiles, gk, 0, kps, target);
+}
+
+// The larger of the two kernels' split counts, so that scratch sized with it
+// serves whichever kernel a TN call of this shape runs on.
+int64_t gemm_auto_splits(int layout, bool bf16, int64_t M, int64_t N, int64_t K) {
+    if (layout != 2) return 1;
+    int64_t gm, gn, gk;
+    gemm_space(layout, M, N, K, gm, gn, gk);
+    int64_t s = gemm_k_splits(bf16, gm, gn, gk);
+    if (bf16 && pk_shape(gm, gn, gk)) {
+        const int64_t p = pk_splits((gm / 256) * (gn / 256), gk);
+        if (p > s) s = p;
+    }
+    return s;
 }
 
 int64_t gemm_partial_elems(int layout, int64_t M, int64_t N, int64_t K, int64_t splits) {
@@ -570,6 +896,21 @@ int32_t gemm_batched_f32(hipStream_t st, bool bf, bool ak, bool bk, float* C, co
 template <typename TX, typename TW, typename TC>
 static int32_t gemm_typed(hipStream_t st, int layout, TC* C, const TX* X, const TW* W, int64_t M, int64_t N,
                           int64_t K, bool accumulate, int64_t splits, float* partial) {
+    if constexpr (std::is_same<TX, bf16>::value && std::is_same<TW, bf16>::value) {
+        // bf16 operands in memory: the persistent direct-to-LDS kernel when the shape allows
+        if (layout == 0 && pk_ok(M, N, K, K, K, N, X, W, C))
+            return pk_launch<true, true, TC>(st, C, X, W, M, N, K, K, K, N, accumulate, 1, nullptr, -1, nullptr,
+                                             nullptr, 0.f, "linear_fwd");
+        if (layout == 1 && pk_ok(M, K, N, N, K, K, X, W, C))
+            return pk_launch<true, false, TC>(st, C, X, W, M, K, N, N, K, K, accumulate, 1, nullptr, -1, nullptr,
+                                              nullptr, 0.f, "linear_bwd_dx");
+        if (layout == 2 && pk_ok(N, K, M, N, K, K, X, W, C)) {
+            const int64_t s = splits >= 1 ? splits : pk_splits((N / 256) * (K / 256), M);
+            if (M % (s * kPkBK) == 0)
+                return pk_launch<false, false, TC>(st, C, X, W, N, K, M, N, K, K, accumulate, s, partial, -1, nullptr,
+                                                   nullptr, 0.f, "linear_bwd_dw");
+        }
+    }
     if (layout == 0)
         return gemm_launch<TX, TW, TC, true, true, true>(st, C, X, W, M, N, K, K, K, N, accumulate, 1, nullptr,
                                                          "linear_fwd");
@@ -601,6 +942,20 @@ int32_t gemm_bf16io(hipStream_t st, int layout, void* C, int c_bf16, const void*
 int32_t gemm_epilogue(hipStream_t st, int layout, int epi, void* C, int c_bf16, const void* X, int x_bf16,
                       const void* W, int w_bf16, int64_t M, int64_t N, int64_t K, const void* aux, void* aux_out,
                       float cap) {
+    if (x_bf16 && w_bf16) {
+        // bf16 operands in memory: the persistent direct-to-LDS kernel when the shape allows
+        const bf16 *Xb = (const bf16*)X, *Wb = (const bf16*)W;
+        if (layout == 0 && pk_ok(M, N, K, K, K, N, X, W, C))
+            return c_bf16 ? pk_launch<true, true, bf16>(st, (bf16*)C, Xb, Wb, M, N, K, K, K, N, false, 1, nullptr, epi,
+                                                        aux, aux_out, cap, "gemm_epilogue")
+                          : pk_launch<true, true, float>(st, (float*)C, Xb, Wb, M, N, K, K, K, N, false, 1, nullptr,
+                                                         epi, aux, aux_out, cap, "gemm_epilogue");
+        if (layout == 1 && pk_ok(M, K, N, N, K, K, X, W, C))
+            return c_bf16 ? pk_launch<true, false, bf16>(st, (bf16*)C, Xb, Wb, M, K, N, N, K, K, false, 1, nullptr, epi,
+                                                         aux, aux_out, cap, "gemm_epilogue")
+                          : pk_launch<true, false, float>(st, (float*)C, Xb, Wb, M, K, N, N, K, K, false, 1, nullptr,
+                                                          epi, aux, aux_out, cap, "gemm_epilogue");
+    }
 #define AR_GE(TX, TW, TC)                                                                                          \
     (layout == 0 ? gemm_launch<TX, TW, TC, true, true, true>(st, (TC*)C, (const TX*)X, (const TW*)W, M, N, K, K, K, N, \
                                                              false, 1, nullptr, "gemm_epilogue", 1, 0, 0, 0, epi, aux, \

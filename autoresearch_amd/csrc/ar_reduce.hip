@@ -404,9 +404,10 @@ __global__ void emb_chunk_sum_k(float* partial, const uint32_t* keys, const int3
 // chunk_0 starts at the segment start p and chunk_j (j >= 1) at the j-th
 // multiple of kEmbChunk after it.  Lane l owns the float4 columns l + 64 j
 // (j < NC); the chunk rows' loads are issued kUnroll at a time ahead of their
-// in-order adds.
+// in-order adds (8 x NC float4 registers: the 256-thread bound keeps NC = 4
+// out of scratch).
 template <int NC>
-__global__ void emb_segment_apply_v_k(float* gw, const float* partial, const uint32_t* keys, int64_t n, int64_t dim) {
+__global__ __launch_bounds__(256) void emb_segment_apply_v_k(float* gw, const float* partial, const uint32_t* keys, int64_t n, int64_t dim) {
     const int lane = threadIdx.x % kWave;
     const int64_t p = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
     if (p >= n || !(p == 0 || keys[p] != keys[p - 1])) return;

@@ -7,6 +7,8 @@ value embeddings, softcap 15, Muon (5 Polar Express iterations) on every 2-D
 matrix and AdamW on embeddings and scalars; bf16 matrix-core compute with
 fp32 master weights.  Token ids are Zipf(1.1) over the vocabulary from seed 0
 (synthetic; no dataset).  Weights follow the reference init (seed 42).
+`--config 5` runs BASELINE config 5 instead (depth 12, d_model 768, 6 heads,
+B = 64, same architecture), reported with the same fields.
 
 A "step" = zero_grads -> forward -> backward -> AdamW + Muon update
 (train.mojo:231-282), all on the GPU through the C ABI (--graph: replayed
@@ -102,8 +104,10 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=11)
-    ap.add_argument("--depth", type=int, default=8)
-    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--config", type=int, choices=[4, 5], default=4,
+                    help="BASELINE workload: 4 = depth 8 d512 B32 (the metric), 5 = depth 12 d768 B64")
+    ap.add_argument("--depth", type=int, default=None)
+    ap.add_argument("--batch", type=int, default=None)
     ap.add_argument("--seq", type=int, default=2048)
     ap.add_argument("--vocab", type=int, default=8192)
     ap.add_argument("--precision", choices=["bf16", "fp32"], default="bf16")
@@ -113,6 +117,10 @@ def main(argv=None) -> int:
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run one device copy of MIB MiB (calibrates rocprofv3 byte counters) and exit")
     a = ap.parse_args(argv)
+    if a.depth is None:
+        a.depth = 8 if a.config == 4 else 12
+    if a.batch is None:
+        a.batch = 32 if a.config == 4 else 64
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the training step is single-GPU in the reference; "
               "multi-GPU data parallelism is a design note, not built). Run with --gpus 1.", file=sys.stderr)
@@ -211,7 +219,7 @@ def main(argv=None) -> int:
         "warmup": a.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": a.precision, "data": "synthetic Zipf(1.1) token ids, seed 0",
         "step_mode": "hip_graph" if a.graph else "eager",
-        "config": {"workload": f"config 4: full training step depth{cfg.n_layer} d{cfg.n_embd} "
+        "config": {"workload": f"config {a.config}: full training step depth{cfg.n_layer} d{cfg.n_embd} "
                                f"H{cfg.n_head}x{cfg.head_dim} V{V} T{T} B{B} SSSL, AdamW+Muon",
                    "global_batch": B, "seq_len": T, "parallelism": "single GPU"},
         "mfma_util": round(mfma_util, 4), "step_tflop": round(flops / 1e12, 3),

@@ -90,6 +90,53 @@ def test_gemm_config3_shapes(env, K, N):
     assert rel_err(gu.host(out), gu.host(ref)) <= TOL_FP32
 
 
+@pytest.mark.parametrize("layout", [0, 1, 2])
+@pytest.mark.parametrize("M,N,K", [(2048, 768, 512), (1024, 256, 2048), (65536, 512, 512)])
+def test_gemm_bf16_storage_persistent(env, layout, M, N, K):
+    """bf16 operands in memory at whole-256-tile shapes run the persistent
+    direct-to-LDS kernel (the bf16 training step's GEMMs).  Reference: torch
+    fp64 matmul of the same bf16 values.  bf16 products are exact in fp32, so
+    the fp32-output bound is the accumulation order's (1e-5); bf16 outputs add
+    one rounding (2^-9 relative per element, 4e-3 in norm).  Covers NT, NN,
+    TN with its reduction split + in-order reduce, and accumulate."""
+    ops, orc, gu = env
+    import torch
+    from autoresearch_amd._lib import check, load
+    L = load()
+    g = torch.Generator(device="cuda").manual_seed(M + N + K + layout)
+    s0 = torch.cuda.current_stream().cuda_stream
+    X = (torch.randn(M, N if layout else K, device="cuda", generator=g)).bfloat16()  # X, or dY for NN / TN
+    if layout == 2:
+        W = torch.randn(M, K, device="cuda", generator=g).bfloat16()                 # the layer input
+        ref = X.double().T @ W.double()
+        shape = (N, K)
+    elif layout == 1:
+        W = (torch.randn(N, K, device="cuda", generator=g) * 0.05).bfloat16()
+        ref = X.double() @ W.double()
+        shape = (M, K)
+    else:
+        W = (torch.randn(N, K, device="cuda", generator=g) * 0.05).bfloat16()
+        ref = X.double() @ W.double().T
+        shape = (M, N)
+    for c_bf16 in (0, 1):
+        C = torch.empty(*shape, device="cuda", dtype=torch.bfloat16 if c_bf16 else torch.float32)
+        check(L.ar_gemm_mixed(s0, layout, C.data_ptr(), c_bf16, X.data_ptr(), 1, W.data_ptr(), 1, M, N, K, 0))
+        torch.cuda.synchronize()
+        tol = 4e-3 if c_bf16 else 1e-5
+        assert rel_err(gu.host(C.float()), gu.host(ref.float())) <= tol, (layout, c_bf16)
+    # accumulate into an fp32 C that already holds values
+    C0 = torch.randn(*shape, device="cuda", generator=g)
+    C = C0.clone()
+    check(L.ar_gemm_mixed(s0, layout, C.data_ptr(), 0, X.data_ptr(), 1, W.data_ptr(), 1, M, N, K, 1))
+    torch.cuda.synchronize()
+    assert rel_err(gu.host(C), gu.host((C0.double() + ref).float())) <= 1e-5
+    # bit-reproducible: a second call gives the same bits
+    C2 = C0.clone()
+    check(L.ar_gemm_mixed(s0, layout, C2.data_ptr(), 0, X.data_ptr(), 1, W.data_ptr(), 1, M, N, K, 1))
+    torch.cuda.synchronize()
+    assert torch.equal(C, C2)
+
+
 def _attn_inputs(gu, r, B, T, H, hd):
     q = gu.randn(r, B, T, H, hd)
     k = gu.randn(r, B, T, H, hd)
