@@ -59,11 +59,13 @@ using TileL = Tile<256, 256, 2, 4>;
 
 // Epilogues.  STORE: C = acc.  ACCUM: C += acc.  PARTIAL: split-K partial.
 // ADD: C = R + acc (R = aux, fp32, row stride ldc; may alias C).
-// RELU2: C = acc (the pre-activation) and aux_out = relu(acc)^2, both TC
-//   (c_fc + relu_squared_fwd, ops.mojo:486-497, fused).
+// RELU2: C = relu(acc)^2, the activation only (c_fc + relu_squared_fwd,
+//   ops.mojo:486-497, fused; the pre-activation is not kept).
 // SOFTCAP: C = cap * tanh(acc / cap) (lm_head + softcap_fwd, ops.mojo:500-510).
-// RELU2_BWD: C = h > 0 ? 2 h acc : 0 with h = aux (TC, row stride ldc)
-//   (mlp_proj dX + relu_squared_bwd, ops.mojo:1126-1140).
+// RELU2_BWD: C = a > 0 ? 2 sqrt(a) acc : 0 with a = aux the stored activation
+//   (TC, row stride ldc): relu(h)^2 = a gives h = sqrt(a) where h > 0, so
+//   relu_squared_bwd's 2 h (ops.mojo:1126-1140) comes from the activation,
+//   whose bf16 rounding perturbs sqrt(a) by at most 2^-10 relative.
 enum Epi { EPI_STORE = 0, EPI_ACCUM = 1, EPI_PARTIAL = 2, EPI_ADD = 3, EPI_RELU2 = 4, EPI_SOFTCAP = 5,
            EPI_RELU2_BWD = 6 };
 
@@ -113,6 +115,8 @@ __device__ __forceinline__ void st4(bf16* p, float4 x) {
 __device__ __forceinline__ float4 add4(float4 a, float4 b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
+// d/dh relu(h)^2 times g, from the activation a = relu(h)^2: 2 sqrt(a) g (0 where a == 0).
+__device__ __forceinline__ float relu2_grad(float a, float g) { return a > 0.f ? 2.f * sqrtf(a) * g : 0.f; }
 
 template <typename T, int N>
 __device__ __forceinline__ void vload(T (&dst)[N], const T* src) {
@@ -401,17 +405,15 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
             } else if constexpr (EPI == EPI_ACCUM || EPI == EPI_ADD) {
                 st4(C + o, add4(pre[PRE ? t : 0], x));
             } else if constexpr (EPI == EPI_RELU2) {
-                const float4 r2 = make_float4(x.x > 0.f ? x.x * x.x : 0.f, x.y > 0.f ? x.y * x.y : 0.f,
-                                              x.z > 0.f ? x.z * x.z : 0.f, x.w > 0.f ? x.w * x.w : 0.f);
-                st4(C + o, x);
-                st4(static_cast<TC*>(aux_out) + o, r2);
+                st4(C + o, make_float4(x.x > 0.f ? x.x * x.x : 0.f, x.y > 0.f ? x.y * x.y : 0.f,
+                                       x.z > 0.f ? x.z * x.z : 0.f, x.w > 0.f ? x.w * x.w : 0.f));
             } else if constexpr (EPI == EPI_SOFTCAP) {
                 st4(C + o, make_float4(cap * tanhf(x.x / cap), cap * tanhf(x.y / cap), cap * tanhf(x.z / cap),
                                        cap * tanhf(x.w / cap)));
             } else if constexpr (EPI == EPI_RELU2_BWD) {
-                const float4 h = pre[PRE ? t : 0];
-                st4(C + o, make_float4(h.x > 0.f ? 2.f * h.x * x.x : 0.f, h.y > 0.f ? 2.f * h.y * x.y : 0.f,
-                                       h.z > 0.f ? 2.f * h.z * x.z : 0.f, h.w > 0.f ? 2.f * h.w * x.w : 0.f));
+                const float4 a = pre[PRE ? t : 0];
+                st4(C + o, make_float4(relu2_grad(a.x, x.x), relu2_grad(a.y, x.y), relu2_grad(a.z, x.z),
+                                       relu2_grad(a.w, x.w)));
             }
         }
         __syncthreads();
@@ -616,17 +618,15 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
                     } else if constexpr (EPI == EPI_ACCUM || EPI == EPI_ADD) {
                         st4(C + o, add4(pre[PRE ? t : 0], x));
                     } else if constexpr (EPI == EPI_RELU2) {
-                        const float4 r2 = make_float4(x.x > 0.f ? x.x * x.x : 0.f, x.y > 0.f ? x.y * x.y : 0.f,
-                                                      x.z > 0.f ? x.z * x.z : 0.f, x.w > 0.f ? x.w * x.w : 0.f);
-                        st4(C + o, x);
-                        st4(static_cast<TC*>(aux_out) + o, r2);
+                        st4(C + o, make_float4(x.x > 0.f ? x.x * x.x : 0.f, x.y > 0.f ? x.y * x.y : 0.f,
+                                               x.z > 0.f ? x.z * x.z : 0.f, x.w > 0.f ? x.w * x.w : 0.f));
                     } else if constexpr (EPI == EPI_SOFTCAP) {
                         st4(C + o, make_float4(cap * tanhf(x.x / cap), cap * tanhf(x.y / cap),
                                                cap * tanhf(x.z / cap), cap * tanhf(x.w / cap)));
                     } else if constexpr (EPI == EPI_RELU2_BWD) {
-                        const float4 hv = pre[PRE ? t : 0];
-                        st4(C + o, make_float4(hv.x > 0.f ? 2.f * hv.x * x.x : 0.f, hv.y > 0.f ? 2.f * hv.y * x.y : 0.f,
-                                               hv.z > 0.f ? 2.f * hv.z * x.z : 0.f, hv.w > 0.f ? 2.f * hv.w * x.w : 0.f));
+                        const float4 a = pre[PRE ? t : 0];
+                        st4(C + o, make_float4(relu2_grad(a.x, x.x), relu2_grad(a.y, x.y), relu2_grad(a.z, x.z),
+                                               relu2_grad(a.w, x.w)));
                     }
                 }
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -24,8 +24,9 @@ int32_t gemm_f32(hipStream_t st, int layout, bool bf16, float* C, const float* X
 int32_t gemm_bf16io(hipStream_t st, int layout, void* C, int c_bf16, const void* X, int x_bf16, const void* W,
                     int w_bf16, int64_t M, int64_t N, int64_t K, bool accumulate, int64_t splits, float* partial);
 // NT (layout 0) / NN (layout 1) GEMM with a fused epilogue, bf16 compute:
-// epi 3 ADD (C = aux + acc, aux fp32), 4 RELU2 (C = acc, aux_out = relu(acc)^2),
-// 5 SOFTCAP (C = cap tanh(acc/cap)), 6 RELU2_BWD (C = aux > 0 ? 2 aux acc : 0).
+// epi 3 ADD (C = aux + acc, aux fp32), 4 RELU2 (C = relu(acc)^2),
+// 5 SOFTCAP (C = cap tanh(acc/cap)), 6 RELU2_BWD (C = aux > 0 ? 2 sqrt(aux) acc : 0,
+// aux = the activation relu(h)^2).
 enum { GEMM_EPI_ADD = 3, GEMM_EPI_RELU2 = 4, GEMM_EPI_SOFTCAP = 5, GEMM_EPI_RELU2_BWD = 6 };
 int32_t gemm_epilogue(hipStream_t st, int layout, int epi, void* C, int c_bf16, const void* X, int x_bf16,
                       const void* W, int w_bf16, int64_t M, int64_t N, int64_t K, const void* aux, void* aux_out,

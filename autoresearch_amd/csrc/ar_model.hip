@@ -51,7 +51,7 @@ struct LayerBufs {
 // Saved activations of one layer in the bf16 step.
 struct LayerBufsB {
     float *x, *lse, *attn_out, *rms_attn, *rms_mlp, *gate, *xg;
-    ar::bf16 *xn, *q, *k, *v, *attn_out_b, *xn_mlp, *h, *act;
+    ar::bf16 *xn, *q, *k, *v, *attn_out_b, *xn_mlp, *act;
 };
 
 }  // namespace
@@ -314,7 +314,6 @@ static int32_t gpt_build(ar_gpt* m) {
             AR_TRY(balloc(&b.v, BT * kv));
             AR_TRY(balloc(&b.attn_out_b, BT * C));
             AR_TRY(balloc(&b.xn_mlp, BT * C));
-            AR_TRY(balloc(&b.h, BT * F));
             AR_TRY(balloc(&b.act, BT * F));
             if (has_ve(c, i)) {
                 FALLOC(b.gate, BT * H);
@@ -510,9 +509,9 @@ static int32_t forward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* tar
                       nullptr, 0.f));
         AR_TRY(resid_norm(st, 2, nullptr, nullptr, b.rms_mlp, b.xn_mlp, nullptr, nullptr, m->x, nullptr, nullptr,
                           nullptr, nullptr, nullptr, 0, nullptr, 0, 0, BT, C));
-        // h = xn @ c_fc^T, act = relu(h)^2; x += act @ mlp_proj^T
-        AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_RELU2, b.h, true, b.xn_mlp, true, Wb(m, m->i_fc[i]), BT, F, C, nullptr,
-                      b.act, 0.f));
+        // act = relu(xn @ c_fc^T)^2 (the pre-activation is not kept); x += act @ mlp_proj^T
+        AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_RELU2, b.act, true, b.xn_mlp, true, Wb(m, m->i_fc[i]), BT, F, C, nullptr,
+                      nullptr, 0.f));
         AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_ADD, m->x, false, b.act, true, Wb(m, m->i_mlpp[i]), BT, C, F, m->x,
                       nullptr, 0.f));
     }
@@ -545,9 +544,9 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
         const int64_t i = c.n_layer - 1 - r;
         LayerBufsB& b = m->LB[i];
         const bool ve = has_ve(c, i);
-        // MLP: dh = relu2_bwd(grad_x @ mlp_proj, h)
+        // MLP: dh = relu2_bwd(grad_x @ mlp_proj), 2 h taken as 2 sqrt(act)
         AR_TRY(gemm_e(m, 1, 1, GEMM_EPI_RELU2_BWD, m->grad_h, true, m->grad_xb, true, Wb(m, m->i_mlpp[i]), BT, C, F,
-                      b.h, nullptr, 0.f));
+                      b.act, nullptr, 0.f));
         AR_TRY(gemm_b(m, 2, 2, G(m, m->i_mlpp[i]), false, m->grad_xb, true, b.act, true, BT, C, F, true));
         AR_TRY(gemm_b(m, 1, 1, m->grad_x_norm, false, m->grad_h, true, Wb(m, m->i_fc[i]), true, BT, F, C, false));
         AR_TRY(gemm_b(m, 2, 2, G(m, m->i_fc[i]), false, m->grad_h, true, b.xn_mlp, true, BT, F, C, true));

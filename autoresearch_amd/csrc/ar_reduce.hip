@@ -237,37 +237,63 @@ __global__ void ve_apply_bwd_k(float* gve, float* ggate, const float* gv, const 
 }
 
 // ---------------- K27 ve_gate_bwd (ops.mojo:1240-1274), deterministic ----------------
-// Block b owns a fixed token range.  Thread (c = tid % 64, j = tid / 64):
-// gx[t,c] += sum_h dz[t,h] W[h,c] for its tokens (no conflicts), and a
-// per-block partial of gW[h,c] = sum_t dz[t,h] x[t,c] reduced over j in LDS.
-__global__ void ve_gate_bwd_partial_k(float* gx, float* partial, const float* ggate, const float* gate,
-                                      const float* xn, const float* w, int64_t nt, int64_t nkv, int64_t gc,
-                                      int64_t C, int64_t ldx) {
-    __shared__ float acc_s[4][kGateMaxH][64];
-    const int c = threadIdx.x % 64, j = threadIdx.x / 64;
+// Block b owns a fixed token range.  Thread (c = tid % CW, j = tid / CW),
+// CW = 32 or 64 channel lanes (gc <= CW), walks tokens t0 + j + NJ i with
+// four tokens' loads issued together: gx[t,c] += sum_h dz[t,h] W[h,c] for
+// its tokens (no conflicts), and a per-block partial of
+// gW[h,c] = sum_t dz[t,h] x[t,c], reduced over j in LDS in j order.
+template <int CW>
+__global__ __launch_bounds__(256) void ve_gate_bwd_partial_k(float* gx, float* partial, const float* ggate,
+                                                             const float* gate, const float* xn, const float* w,
+                                                             int64_t nt, int64_t nkv, int64_t gc, int64_t C,
+                                                             int64_t ldx) {
+    constexpr int NJ = 256 / CW, U = 4;
+    __shared__ float acc_s[NJ][kGateMaxH][CW];
+    const int c = threadIdx.x % CW, j = threadIdx.x / CW;
     const int64_t per = (nt + gridDim.x - 1) / gridDim.x;
     const int64_t t0 = (int64_t)blockIdx.x * per;
     const int64_t t1 = t0 + per < nt ? t0 + per : nt;
     float accw[kGateMaxH];
+#pragma unroll
     for (int h = 0; h < kGateMaxH; ++h) accw[h] = 0.f;
     if (c < gc) {
-        for (int64_t t = t0 + j; t < t1; t += 4) {
-            const float x = xn[t * ldx + c];
-            float ax = 0.f;
-            for (int64_t h = 0; h < nkv; ++h) {
-                const float g = gate[t * nkv + h];
-                const float dz = ggate[t * nkv + h] * g * (1.0f - g / 2.0f);
-                ax += dz * w[h * gc + c];
-                accw[h] += dz * x;
+        for (int64_t t = t0 + j; t < t1; t += U * NJ) {
+            float x[U], ax[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t tt = t + u * NJ;
+                x[u] = tt < t1 ? xn[tt * ldx + c] : 0.f;
+                ax[u] = 0.f;
             }
-            gx[t * C + c] += ax;
+#pragma unroll
+            for (int h = 0; h < kGateMaxH; ++h) {
+                if (h >= nkv) break;
+                const float wv = w[h * gc + c];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int64_t tt = t + u * NJ;
+                    if (tt >= t1) break;
+                    const float g = gate[tt * nkv + h];
+                    const float dz = ggate[tt * nkv + h] * g * (1.0f - g / 2.0f);
+                    ax[u] += dz * wv;
+                    accw[h] += dz * x[u];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t tt = t + u * NJ;
+                if (tt < t1) gx[tt * C + c] += ax[u];
+            }
         }
     }
+#pragma unroll
     for (int h = 0; h < kGateMaxH; ++h) acc_s[j][h][c] = accw[h];
     __syncthreads();
     if (j == 0 && c < gc) {
         for (int64_t h = 0; h < nkv; ++h) {
-            const float s = ((acc_s[0][h][c] + acc_s[1][h][c]) + acc_s[2][h][c]) + acc_s[3][h][c];
+            float s = acc_s[0][h][c];
+#pragma unroll
+            for (int jj = 1; jj < NJ; ++jj) s += acc_s[jj][h][c];
             partial[(int64_t)blockIdx.x * nkv * gc + h * gc + c] = s;
         }
     }
@@ -543,7 +569,10 @@ int32_t frob_normalize(hipStream_t st, float* data, int64_t n, float* scratch) {
 int32_t ve_gate_bwd(hipStream_t st, float* gx, float* gw, const float* ggate, const float* gate, const float* xn,
                     const float* w, int64_t nt, int64_t nkv, int64_t gc, int64_t C, int64_t ldx, float* partial) {
     if (nt == 0) return AR_OK;
-    ve_gate_bwd_partial_k<<<kGateBlocks, 256, 0, st>>>(gx, partial, ggate, gate, xn, w, nt, nkv, gc, C, ldx);
+    if (gc <= 32)
+        ve_gate_bwd_partial_k<32><<<kGateBlocks, 256, 0, st>>>(gx, partial, ggate, gate, xn, w, nt, nkv, gc, C, ldx);
+    else
+        ve_gate_bwd_partial_k<64><<<kGateBlocks, 256, 0, st>>>(gx, partial, ggate, gate, xn, w, nt, nkv, gc, C, ldx);
     ve_gate_bwd_finish_k<<<1, 256, 0, st>>>(gw, partial, kGateBlocks, nkv * gc);
     return check_launch("ve_gate_bwd");
 }

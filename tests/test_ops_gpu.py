@@ -244,10 +244,11 @@ def test_softmax(env):
     assert rel_err(gu.host(out), ex / ex.sum(1, keepdims=True)) <= TOL_FP32
 
 
-def test_ve_kernels(env):
+@pytest.mark.parametrize("nt,gc", [(512, 32), (3001, 48), (70000, 32)])
+def test_ve_kernels(env, nt, gc):
     ops, orc, gu = env
     r = gu.rng(8)
-    nt, H, hd, gc = 512, 4, 128, 32
+    H, hd = 4, 128
     C = H * hd
     xn = gu.randn(r, nt, C)
     w = gu.randn(r, H, gc, scale=0.2)
