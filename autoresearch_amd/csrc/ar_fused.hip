@@ -416,6 +416,34 @@ __global__ void to_bf16_k(bf16* out, const float* in, int64_t n4) {
         st_bf16x4(out + 4 * i, reinterpret_cast<const float4*>(in)[i]);
 }
 
+// Batched fp32 -> bf16 transpose: entry e maps the [rows, cols] fp32 matrix
+// at in + src to the [cols, rows] bf16 matrix at out + dst.  One 64 x 64
+// tile per workgroup (tiles numbered per entry from tab[e].tile0), staged
+// through LDS so both the read (rows of the source) and the write (rows of
+// the transpose) are coalesced.
+__global__ __launch_bounds__(256) void transpose_bf16_k(bf16* out, const float* in, const TransposeEntry* tab,
+                                                         int n) {
+    __shared__ float t[64][65];
+    int e = 0;
+    while (e + 1 < n && (int64_t)blockIdx.x >= tab[e + 1].tile0) ++e;
+    const TransposeEntry te = tab[e];
+    const int64_t local = (int64_t)blockIdx.x - te.tile0;
+    const int64_t tcols = (te.cols + 63) / 64;
+    const int64_t r0 = (local / tcols) * 64, c0 = (local % tcols) * 64;
+    const float* src = in + te.src;
+    bf16* dst = out + te.dst;
+    const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
+    for (int r = ty; r < 64; r += 4) {
+        const int64_t gr = r0 + r, gc = c0 + tx;
+        t[r][tx] = gr < te.rows && gc < te.cols ? src[gr * te.cols + gc] : 0.f;
+    }
+    __syncthreads();
+    for (int c = ty; c < 64; c += 4) {
+        const int64_t gc = c0 + c, gr = r0 + tx;
+        if (gc < te.cols && gr < te.rows) dst[gc * te.rows + gr] = (bf16)t[tx][c];
+    }
+}
+
 // D[r] = sum_d O[r, d] * dO[r, d] with dO stored as bf16; groups of HD/4
 // lanes hold one row.
 template <int G>
@@ -538,6 +566,13 @@ int32_t to_bf16(hipStream_t st, bf16* out, const float* in, int64_t n) {
     if (n == 0) return AR_OK;
     to_bf16_k<<<flat_grid(n / 4, kBlock * 4), kBlock, 0, st>>>(out, in, n / 4);
     return check_launch("to_bf16");
+}
+
+int32_t transpose_bf16(hipStream_t st, bf16* out, const float* in, const TransposeEntry* tab, int n,
+                       int64_t tiles) {
+    if (n <= 0 || tiles <= 0) return AR_OK;
+    transpose_bf16_k<<<(unsigned)tiles, 256, 0, st>>>(out, in, tab, n);
+    return check_launch("transpose_bf16");
 }
 
 int32_t precompute_d_mixed(hipStream_t st, float* d, const float* o, const bf16* g, int64_t rows, int64_t hd) {

@@ -110,6 +110,14 @@ int32_t norm_bwd(hipStream_t st, int mode, float* gx, bf16* gxb, const float* gn
                  const float* x0, const float* res, int64_t layer, float* g_res, float* g_x0, float* partial,
                  int64_t rows, int64_t C);
 int32_t to_bf16(hipStream_t st, bf16* out, const float* in, int64_t n);
+// One matrix of a batched transpose: fp32 [rows, cols] at in + src becomes
+// bf16 [cols, rows] at out + dst; tile0 = 64 x 64 tiles of the entries before.
+struct TransposeEntry {
+    int64_t src, dst, rows, cols, tile0;
+};
+// tab: n entries in device memory; tiles: total 64 x 64 tiles.
+int32_t transpose_bf16(hipStream_t st, bf16* out, const float* in, const TransposeEntry* tab, int n,
+                       int64_t tiles);
 // D = rowsum(O * dO), dO stored as bf16.
 int32_t precompute_d_mixed(hipStream_t st, float* d, const float* o, const bf16* g, int64_t rows, int64_t hd);
 

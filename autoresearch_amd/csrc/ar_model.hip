@@ -76,6 +76,12 @@ struct ar_gpt {
         *grad_mlp, *grad_ve, *grad_gate;
     // bf16 step
     ar::bf16* wb = nullptr;  // bf16 shadow of the parameter arena (same offsets)
+    // bf16 transposes of the matrices the backward multiplies by (W^T at W's
+    // offset): dX = dY . W runs as an NT product with both operands K-major.
+    ar::bf16* wbt = nullptr;
+    ar::TransposeEntry* wbt_tab = nullptr;
+    int wbt_n = 0;
+    int64_t wbt_tiles = 0;
     std::vector<LayerBufsB> LB;
     ar::bf16* qkv = nullptr;  // [BT, 3C] q | k | v GEMM output
     ar::bf16 *x_final_b = nullptr, *grad_logits_b = nullptr, *grad_xb = nullptr, *grad_h = nullptr,
@@ -139,6 +145,7 @@ int64_t add_tensor(ar_gpt* m, int64_t rows, int64_t cols, const std::string& nm)
 inline float* P(ar_gpt* m, int64_t i) { return m->params + m->t[i].offset; }
 inline float* G(ar_gpt* m, int64_t i) { return m->grads + m->t[i].offset; }
 inline const bf16* Wb(ar_gpt* m, int64_t i) { return m->wb + m->t[i].offset; }
+inline const bf16* WbT(ar_gpt* m, int64_t i) { return m->wbt + m->t[i].offset; }
 
 inline ar_stream_t AS(ar_gpt* m) { return reinterpret_cast<ar_stream_t>(m->st); }
 
@@ -322,6 +329,27 @@ static int32_t gpt_build(ar_gpt* m) {
                 b.gate = b.xg = nullptr;
             }
         }
+        // transposed shadows: fused [3C, C] c_q|c_k|c_v, c_proj, c_fc, mlp_proj, lm_head
+        AR_TRY(balloc(&m->wbt, m->nparams));
+        std::vector<TransposeEntry> tab;
+        auto add_t = [&](int64_t idx, int64_t rows, int64_t cols) {
+            const int64_t off = m->t[idx].offset;
+            const int64_t t0 = tab.empty() ? 0 : tab.back().tile0 + cdiv(tab.back().rows, 64) * cdiv(tab.back().cols, 64);
+            tab.push_back(TransposeEntry{off, off, rows, cols, t0});
+        };
+        for (int64_t i = 0; i < Lr; ++i) {
+            add_t(m->i_q[i], 3 * C, C);
+            add_t(m->i_proj[i], C, C);
+            add_t(m->i_fc[i], F, C);
+            add_t(m->i_mlpp[i], C, F);
+        }
+        add_t(m->i_lm, V, C);
+        m->wbt_n = (int)tab.size();
+        m->wbt_tiles = tab.back().tile0 + cdiv(tab.back().rows, 64) * cdiv(tab.back().cols, 64);
+        AR_TRY(dalloc(m, (void**)&m->wbt_tab, tab.size() * sizeof(TransposeEntry)));
+        if (hipMemcpy(m->wbt_tab, tab.data(), tab.size() * sizeof(TransposeEntry), hipMemcpyHostToDevice) !=
+            hipSuccess)
+            return set_error(AR_EHIP, "gpt: transpose table upload failed");
         AR_TRY(balloc(&m->qkv, BT * 3 * C));
         AR_TRY(balloc(&m->x_final_b, BT * C));
         AR_TRY(balloc(&m->grad_logits_b, BT * V));
@@ -489,6 +517,7 @@ static int32_t forward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* tar
     const int64_t F = kMlpExpansion * C;
     hipStream_t st = m->st;
     AR_TRY(to_bf16(st, m->wb, m->params, m->nparams));
+    AR_TRY(transpose_bf16(st, m->wbt, m->params, m->wbt_tab, m->wbt_n, m->wbt_tiles));
     for (int64_t i = 0; i < c.n_layer; ++i) {
         LayerBufsB& b = m->LB[i];
         const bool ve = has_ve(c, i);
@@ -536,7 +565,8 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
         m->grad_logits_scale = loss_scale;
         m->grad_logits_valid = true;
     }
-    AR_TRY(gemm_b(m, 1, 1, m->grad_x, false, m->grad_logits_b, true, Wb(m, m->i_lm), true, BT, V, C, false));
+    // dX = dY . W as dY . (W^T)^T: NT with both operands K-major
+    AR_TRY(gemm_b(m, 1, 0, m->grad_x, false, m->grad_logits_b, true, WbT(m, m->i_lm), true, BT, C, V, false));
     AR_TRY(gemm_b(m, 2, 2, G(m, m->i_lm), false, m->grad_logits_b, true, m->x_final_b, true, BT, V, C, true));
     AR_TRY(norm_bwd(st, 0, m->grad_x, m->grad_xb, nullptr, m->x, m->rms_final, nullptr, nullptr, 0, nullptr, nullptr,
                     nullptr, BT, C));
@@ -545,15 +575,15 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
         LayerBufsB& b = m->LB[i];
         const bool ve = has_ve(c, i);
         // MLP: dh = relu2_bwd(grad_x @ mlp_proj), 2 h taken as 2 sqrt(act)
-        AR_TRY(gemm_e(m, 1, 1, GEMM_EPI_RELU2_BWD, m->grad_h, true, m->grad_xb, true, Wb(m, m->i_mlpp[i]), BT, C, F,
+        AR_TRY(gemm_e(m, 1, 0, GEMM_EPI_RELU2_BWD, m->grad_h, true, m->grad_xb, true, WbT(m, m->i_mlpp[i]), BT, F, C,
                       b.act, nullptr, 0.f));
         AR_TRY(gemm_b(m, 2, 2, G(m, m->i_mlpp[i]), false, m->grad_xb, true, b.act, true, BT, C, F, true));
-        AR_TRY(gemm_b(m, 1, 1, m->grad_x_norm, false, m->grad_h, true, Wb(m, m->i_fc[i]), true, BT, F, C, false));
+        AR_TRY(gemm_b(m, 1, 0, m->grad_x_norm, false, m->grad_h, true, WbT(m, m->i_fc[i]), true, BT, C, F, false));
         AR_TRY(gemm_b(m, 2, 2, G(m, m->i_fc[i]), false, m->grad_h, true, b.xn_mlp, true, BT, F, C, true));
         AR_TRY(norm_bwd(st, 1, m->grad_x, m->grad_xb, m->grad_x_norm, b.x, b.rms_mlp, nullptr, nullptr, 0, nullptr,
                         nullptr, nullptr, BT, C));  // Q7: saved x of the layer
         // attention output projection
-        AR_TRY(gemm_b(m, 1, 1, m->grad_attn_out_b, true, m->grad_xb, true, Wb(m, m->i_proj[i]), true, BT, C, C,
+        AR_TRY(gemm_b(m, 1, 0, m->grad_attn_out_b, true, m->grad_xb, true, WbT(m, m->i_proj[i]), true, BT, C, C,
                       false));
         AR_TRY(gemm_b(m, 2, 2, G(m, m->i_proj[i]), false, m->grad_xb, true, b.attn_out_b, true, BT, C, C, true));
         const int64_t ws = window_size(c, i);
@@ -579,7 +609,7 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
         if (ve)
             AR_TRY(ar_embedding_bwd_sorted(AS(m), G(m, m->i_ve[i]), m->grad_ve, m->sorted_ids, m->sorted_tok, BT, kv,
                                            m->scratch));
-        AR_TRY(gemm_b(m, 1, 1, m->grad_x_norm, false, m->grad_qkv, true, Wb(m, m->i_q[i]), true, BT, 3 * C, C,
+        AR_TRY(gemm_b(m, 1, 0, m->grad_x_norm, false, m->grad_qkv, true, WbT(m, m->i_q[i]), true, BT, C, 3 * C,
                       false));
         AR_TRY(gemm_b(m, 2, 2, G(m, m->i_q[i]), false, m->grad_qkv, true, b.xn, true, BT, 3 * C, C, true));
         if (ve)
