@@ -105,16 +105,6 @@ __device__ __forceinline__ bf16x8 accfrag(const f32x16& a, int s) {
     for (int e = 0; e < 8; ++e) f[e] = (bf16)a[8 * s + e];
     return f;
 }
-// Rounding residual of accfrag (accfrag + accfrag_lo ~ 16 significant bits).
-__device__ __forceinline__ bf16x8 accfrag_lo(const f32x16& a, int s) {
-    bf16x8 f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const float x = a[8 * s + e];
-        f[e] = (bf16)(x - (float)(bf16)x);
-    }
-    return f;
-}
 
 // Global -> register prefetch of one 64-row tile (rows >= T read as zero).
 template <int HD>
@@ -342,20 +332,15 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
             for (int dt = 0; dt < G::DT; ++dt)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
-            // O^T += V^T P^T with P as a two-term bf16 split (hi + lo): the
-            // backward's D = rowsum(dO * O) must equal sum_j P_j dP_j.
+            // O^T += V^T P^T, P rounded to bf16 once (the normaliser l keeps
+            // the fp32 row sums).
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int st = 0; st < 2; ++st) {
                     const bf16x8 ph = accfrag(s[kb], st);
-                    const bf16x8 pl = accfrag_lo(s[kb], st);
 #pragma unroll
-                    for (int dt = 0; dt < G::DT; ++dt) {
-                        const bf16x8 va = trfrag<HD>(sV, kb, st, dt, lane);
-                        o[dt] = mma(va, ph, o[dt]);
-                        o[dt] = mma(va, pl, o[dt]);
-                    }
+                    for (int dt = 0; dt < G::DT; ++dt) o[dt] = mma(trfrag<HD>(sV, kb, st, dt, lane), ph, o[dt]);
                 }
         }
         if (more) {
