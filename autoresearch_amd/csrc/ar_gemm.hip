@@ -62,12 +62,15 @@ using TileL = Tile<256, 256, 2, 4>;
 // RELU2: C = relu(acc)^2, the activation only (c_fc + relu_squared_fwd,
 //   ops.mojo:486-497, fused; the pre-activation is not kept).
 // SOFTCAP: C = cap * tanh(acc / cap) (lm_head + softcap_fwd, ops.mojo:500-510).
+// AXPBY: C = cap acc + beta aux (aux fp32, same batch stride / row stride as
+//   C): the Polar Express combinations B = b A + c A^2 and X' = a X + B X
+//   (optimizer.mojo:310-330) folded into the product that precedes them.
 // RELU2_BWD: C = a > 0 ? 2 sqrt(a) acc : 0 with a = aux the stored activation
 //   (TC, row stride ldc): relu(h)^2 = a gives h = sqrt(a) where h > 0, so
 //   relu_squared_bwd's 2 h (ops.mojo:1126-1140) comes from the activation,
 //   whose bf16 rounding perturbs sqrt(a) by at most 2^-10 relative.
 enum Epi { EPI_STORE = 0, EPI_ACCUM = 1, EPI_PARTIAL = 2, EPI_ADD = 3, EPI_RELU2 = 4, EPI_SOFTCAP = 5,
-           EPI_RELU2_BWD = 6 };
+           EPI_RELU2_BWD = 6, EPI_AXPBY = 7 };
 
 template <bool BF16> struct Mfma;
 
@@ -274,7 +277,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
                                                       int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
                                                       int64_t k_per_split, float* partial, int64_t batch,
                                                       int64_t sA, int64_t sB, int64_t sC, const void* aux,
-                                                      void* aux_out, float cap) {
+                                                      void* aux_out, float cap, float beta) {
     using MM = Mfma<BF16>;
     using LT = typename MM::LT;
     constexpr int BM = TL::BM, BN = TL::BN, TM = TL::TM, TN = TL::TN;
@@ -366,7 +369,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
     // Epilogues that read memory (C for ACCUM, aux for ADD / RELU2_BWD) load
     // a strip's vectors before staging it, so the loads overlap each other
     // and the LDS round trip instead of queueing behind the stores.
-    constexpr bool PRE = EPI == EPI_ACCUM || EPI == EPI_ADD || EPI == EPI_RELU2_BWD;
+    constexpr bool PRE = EPI == EPI_ACCUM || EPI == EPI_ADD || EPI == EPI_RELU2_BWD || EPI == EPI_AXPBY;
     float* const strip = reinterpret_cast<float*>(smem_raw) + wave * 32 * SLD;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -380,6 +383,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
                 if (row < M && col < N) {
                     if constexpr (EPI == EPI_ACCUM) pre[t] = ld4(C + o);
                     else if constexpr (EPI == EPI_ADD) pre[t] = ld4(static_cast<const float*>(aux) + o);
+                    else if constexpr (EPI == EPI_AXPBY) pre[t] = ld4(static_cast<const float*>(aux) + bt * sC + o);
                     else pre[t] = ld4(static_cast<const TC*>(aux) + o);
                 } else {
                     pre[t] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -414,6 +418,10 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
                 const float4 a = pre[PRE ? t : 0];
                 st4(C + o, make_float4(relu2_grad(a.x, x.x), relu2_grad(a.y, x.y), relu2_grad(a.z, x.z),
                                        relu2_grad(a.w, x.w)));
+            } else if constexpr (EPI == EPI_AXPBY) {
+                const float4 y = pre[PRE ? t : 0];
+                st4(C + o, make_float4(cap * x.x + beta * y.x, cap * x.y + beta * y.y, cap * x.z + beta * y.z,
+                                       cap * x.w + beta * y.w));
             }
         }
         __syncthreads();
@@ -711,7 +719,7 @@ template <typename TA, typename TB, typename TC, bool AK, bool BKM, bool BF16, t
 static int32_t gemm_launch_t(hipStream_t st, TC* C, const TA* A, const TB* B, int64_t M, int64_t N, int64_t K,
                              int64_t lda, int64_t ldb, int64_t ldc, bool accumulate, int64_t splits_req,
                              float* partial, const char* nm, int64_t batch, int64_t sA, int64_t sB, int64_t sC,
-                             int epi, const void* aux, void* aux_out, float cap) {
+                             int epi, const void* aux, void* aux_out, float cap, float beta) {
     const int64_t tiles = ((M + TL::BM - 1) / TL::BM) * ((N + TL::BN - 1) / TL::BN);
     int64_t kps = 0;
     // one 256x256 workgroup per CU, two 128x128 ones
@@ -723,13 +731,14 @@ static int32_t gemm_launch_t(hipStream_t st, TC* C, const TA* A, const TB* B, in
 #define AR_GK(E)                                                                                              \
     gemm_k<TA, TB, TC, AK, BKM, BF16, E, TL><<<grid, TL::THREADS, lds, st>>>(C, A, B, M, N, K, lda, ldb, ldc, kps, \
                                                                             partial, batch, sA, sB, sC, aux,    \
-                                                                            aux_out, cap)
+                                                                            aux_out, cap, beta)
     if (epi >= 0) {
         switch (epi) {
             case EPI_ADD: AR_GK(EPI_ADD); break;
             case EPI_RELU2: AR_GK(EPI_RELU2); break;
             case EPI_SOFTCAP: AR_GK(EPI_SOFTCAP); break;
             case EPI_RELU2_BWD: AR_GK(EPI_RELU2_BWD); break;
+            case EPI_AXPBY: AR_GK(EPI_AXPBY); break;
             default: return set_error(AR_EINVAL, "%s: bad epilogue %d", nm, epi);
         }
         return check_launch(nm);
@@ -828,14 +837,14 @@ static int32_t gemm_launch(hipStream_t st, TC* C, const TA* A, const TB* B, int6
                            int64_t lda, int64_t ldb, int64_t ldc, bool accumulate, int64_t splits_req,
                            float* partial, const char* nm, int64_t batch = 1, int64_t sA = 0, int64_t sB = 0,
                            int64_t sC = 0, int epi = -1, const void* aux = nullptr, void* aux_out = nullptr,
-                           float cap = 0.f) {
+                           float cap = 0.f, float beta = 0.f) {
     if (use_large(M, N, K, batch))
         return gemm_launch_t<TA, TB, TC, AK, BKM, BF16, TileL>(st, C, A, B, M, N, K, lda, ldb, ldc, accumulate,
                                                                splits_req, partial, nm, batch, sA, sB, sC, epi, aux,
-                                                               aux_out, cap);
+                                                               aux_out, cap, beta);
     return gemm_launch_t<TA, TB, TC, AK, BKM, BF16, TileS>(st, C, A, B, M, N, K, lda, ldb, ldc, accumulate,
                                                            splits_req, partial, nm, batch, sA, sB, sC, epi, aux,
-                                                           aux_out, cap);
+                                                           aux_out, cap, beta);
 }
 
 // GEMM-space sizes of a reference-layout call.
@@ -879,12 +888,15 @@ int64_t gemm_partial_elems(int layout, int64_t M, int64_t N, int64_t K, int64_t 
 // reduction split: the batch supplies the parallelism.
 int32_t gemm_batched_f32(hipStream_t st, bool bf, bool ak, bool bk, float* C, const float* A, const float* B,
                          int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch,
-                         int64_t sA, int64_t sB, int64_t sC) {
+                         int64_t sA, int64_t sB, int64_t sC, const float* aux, float alpha, float beta) {
+    const int epi = aux ? EPI_AXPBY : -1;
 #define AR_GB(AKv, BKv)                                                                                        \
     (bf ? gemm_launch<float, float, float, AKv, BKv, true>(st, C, A, B, M, N, K, lda, ldb, ldc, false, 1, nullptr, \
-                                                           "gemm_batched", batch, sA, sB, sC)                  \
+                                                           "gemm_batched", batch, sA, sB, sC, epi, aux, nullptr, \
+                                                           alpha, beta)                                       \
         : gemm_launch<float, float, float, AKv, BKv, false>(st, C, A, B, M, N, K, lda, ldb, ldc, false, 1, nullptr, \
-                                                            "gemm_batched", batch, sA, sB, sC))
+                                                            "gemm_batched", batch, sA, sB, sC, epi, aux, nullptr, \
+                                                            alpha, beta))
     if (ak && bk) return AR_GB(true, true);
     if (ak && !bk) return AR_GB(true, false);
     if (!ak && !bk) return AR_GB(false, false);

@@ -33,9 +33,11 @@ int32_t gemm_epilogue(hipStream_t st, int layout, int epi, void* C, int c_bf16, 
                       float cap);
 // Batched GEMM-space form: C_b[mo,no] = sum_r A_b(mo,r) B_b(no,r); ak / bk
 // select K-major (r contiguous, row stride lda/ldb) vs MN-major storage.
+// With aux: C_b = alpha * (A_b B_b^T) + beta * aux_b (aux laid out as C).
 int32_t gemm_batched_f32(hipStream_t st, bool bf16, bool ak, bool bk, float* C, const float* A, const float* B,
                          int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch,
-                         int64_t sA, int64_t sB, int64_t sC);
+                         int64_t sA, int64_t sB, int64_t sC, const float* aux = nullptr, float alpha = 1.f,
+                         float beta = 0.f);
 
 // ---- reductions (ar_reduce.hip) ----
 constexpr int kSumBlocks = 512;

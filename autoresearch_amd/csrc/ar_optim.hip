@@ -103,7 +103,7 @@ int64_t muon_scratch_elems(int64_t rows, int64_t cols, bool bf16, int64_t n) {
     (void)bf16;
     const int64_t size = rows * cols;
     const int64_t small = rows >= cols ? cols : rows;
-    return align64(n * kNormBlocks) + align64(n) + 2 * align64(n * size) + 3 * align64(n * small * small);
+    return align64(n * kNormBlocks) + align64(n) + 2 * align64(n * size) + 2 * align64(n * small * small);
 }
 
 int32_t muon_group_step(hipStream_t st, float* const* params, const float* const* grads, float* const* mbufs, int n,
@@ -120,8 +120,7 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
     float* X = scale + align64(n);
     float* Y = X + align64(n * size);
     float* A = Y + align64(n * size);
-    float* AA = A + align64(n * ss);
-    float* Bm = AA + align64(n * ss);
+    float* Bm = A + align64(n * ss);
 
     GroupTable t{};
     for (int j = 0; j < n; ++j) {
@@ -138,27 +137,35 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
     int32_t r = check_launch("muon: normalise");
     if (r) return r;
     ar_stream_t s = reinterpret_cast<ar_stream_t>(st);
+    // Each iteration's combinations ride on the product before them:
+    // Bm = cb A + cc (A A) in the A.A epilogue, and X' = ca X + (B X or X B)
+    // in the last product's epilogue, written to the other of X / Y.
+    float* Xc = X;
+    float* Yc = Y;
     for (int it = 0; it < 5; ++it) {
         const float ca = (float)kPolarA[it], cb = (float)kPolarB[it], cc = (float)kPolarC[it];
         if (tall)  // A = X^T X : mo = c1, no = c2, r = row (both operands MN-major)
-            r = gemm_batched_f32(st, bf16, false, false, A, X, X, cols, cols, rows, cols, cols, cols, n, size, size,
+            r = gemm_batched_f32(st, bf16, false, false, A, Xc, Xc, cols, cols, rows, cols, cols, cols, n, size, size,
                                  ss);
         else  // A = X X^T : mo = r1, no = r2, r = col (both K-major)
-            r = gemm_batched_f32(st, bf16, true, true, A, X, X, rows, rows, cols, cols, cols, rows, n, size, size, ss);
+            r = gemm_batched_f32(st, bf16, true, true, A, Xc, Xc, rows, rows, cols, cols, cols, rows, n, size, size,
+                                 ss);
         if (r) return r;
-        // AA = A @ A
-        if ((r = gemm_batched_f32(st, bf16, true, false, AA, A, A, sm, sm, sm, sm, sm, sm, n, ss, ss, ss))) return r;
-        if ((r = ar_scale_add(s, Bm, A, AA, cb, cc, n * ss))) return r;
-        if (tall)  // Y = X @ B
-            r = gemm_batched_f32(st, bf16, true, false, Y, X, Bm, rows, cols, cols, cols, cols, cols, n, size, ss,
-                                 size);
-        else  // Y = B @ X
-            r = gemm_batched_f32(st, bf16, true, false, Y, Bm, X, rows, cols, rows, rows, cols, cols, n, ss, size,
-                                 size);
+        // Bm = cb A + cc (A @ A)
+        if ((r = gemm_batched_f32(st, bf16, true, false, Bm, A, A, sm, sm, sm, sm, sm, sm, n, ss, ss, ss, A, cc, cb)))
+            return r;
+        if (tall)  // X' = ca X + X @ B
+            r = gemm_batched_f32(st, bf16, true, false, Yc, Xc, Bm, rows, cols, cols, cols, cols, cols, n, size, ss,
+                                 size, Xc, 1.0f, ca);
+        else  // X' = ca X + B @ X
+            r = gemm_batched_f32(st, bf16, true, false, Yc, Bm, Xc, rows, cols, rows, rows, cols, cols, n, ss, size,
+                                 size, Xc, 1.0f, ca);
         if (r) return r;
-        if ((r = ar_scale_add(s, X, X, Y, ca, 1.0f, n * size))) return r;
+        float* tmp = Xc;
+        Xc = Yc;
+        Yc = tmp;
     }
-    update_multi_k<<<eg, 256, 0, st>>>(t, X, size, lr, (float)wd, dev.dsc ? dev.dsc + dev.lr_i : nullptr,
+    update_multi_k<<<eg, 256, 0, st>>>(t, Xc, size, lr, (float)wd, dev.dsc ? dev.dsc + dev.lr_i : nullptr,
                                        dev.dsc ? dev.dsc + dev.wd_i : nullptr);
     return check_launch("muon: update");
 }
