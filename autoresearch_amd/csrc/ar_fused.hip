@@ -160,8 +160,10 @@ __global__ __launch_bounds__(kBlock) void resid_norm_k(NormArgs a) {
 
 // ---------------------------------------------------------------------
 // qkv_post: wave per (token, part); part 0 / 1 = q / k: rope then per-head
-// rmsnorm (lane d of head group `sub` holds the pair (d, d + HD/2));
-// part 2 = v (+ gate * value embedding).  Writes bf16 [nt, C] each.
+// rmsnorm, lane (sub, j) of a head group holding the four pairs
+// (d, d + HD/2), d = 4 j .. 4 j + 3, of head h0 + sub (8-byte bf16 loads and
+// stores, 16-byte cos / sin loads); part 2 = v (+ gate * value embedding).
+// Writes bf16 [nt, C] each.
 struct QkvArgs {
     bf16 *q, *k, *v;
     const bf16* qkv;  // [nt, 3C]
@@ -176,9 +178,10 @@ struct QkvArgs {
 template <int HD>
 __global__ __launch_bounds__(kBlock) void qkv_post_k(QkvArgs a) {
     constexpr int HALF = HD / 2;
-    constexpr int HPI = 64 / HALF;  // heads per wave iteration
+    constexpr int LPH = HALF / 4;   // lanes per head
+    constexpr int HPI = 64 / LPH;   // heads per wave iteration
     const int lane = threadIdx.x % kWave;
-    const int sub = lane / HALF, d = lane % HALF;
+    const int sub = lane / LPH, d0 = (lane % LPH) * 4;
     const int64_t C = a.C;
     for (int64_t w = wave_id(); w < a.nt * 3; w += wave_count()) {
         const int64_t t = w / 3;
@@ -187,20 +190,24 @@ __global__ __launch_bounds__(kBlock) void qkv_post_k(QkvArgs a) {
         if (part < 2) {
             bf16* dst = (part == 0 ? a.q : a.k) + t * C;
             const int64_t tok = t % a.period;
-            const float c = a.cos_t[tok * HALF + d], s = a.sin_t[tok * HALF + d];
+            const float4 c = *reinterpret_cast<const float4*>(a.cos_t + tok * HALF + d0);
+            const float4 s = *reinterpret_cast<const float4*>(a.sin_t + tok * HALF + d0);
             for (int h0 = 0; h0 < a.H; h0 += HPI) {
                 const int h = h0 + sub;
-                float y1 = 0.f, y2 = 0.f;
+                float4 y1 = make_float4(0.f, 0.f, 0.f, 0.f), y2 = y1;
                 if (h < a.H) {
-                    const float x1 = (float)src[h * HD + d], x2 = (float)src[h * HD + HALF + d];
-                    y1 = x1 * c + x2 * s;
-                    y2 = x1 * (-s) + x2 * c;
+                    const float4 x1 = ld_bf16x4(src + h * HD + d0), x2 = ld_bf16x4(src + h * HD + HALF + d0);
+                    y1 = make_float4(x1.x * c.x + x2.x * s.x, x1.y * c.y + x2.y * s.y, x1.z * c.z + x2.z * s.z,
+                                     x1.w * c.w + x2.w * s.w);
+                    y2 = make_float4(x1.x * (-s.x) + x2.x * c.x, x1.y * (-s.y) + x2.y * c.y,
+                                     x1.z * (-s.z) + x2.z * c.z, x1.w * (-s.w) + x2.w * c.w);
                 }
-                const float ss = group_sum<HALF>(y1 * y1 + y2 * y2);
-                const float rms = sqrtf(ss / (float)HD + kNormEps);
+                const float ss = group_sum<LPH>(y1.x * y1.x + y2.x * y2.x + y1.y * y1.y + y2.y * y2.y +
+                                                y1.z * y1.z + y2.z * y2.z + y1.w * y1.w + y2.w * y2.w);
+                const float inv = 1.0f / sqrtf(ss / (float)HD + kNormEps);
                 if (h < a.H) {
-                    dst[h * HD + d] = (bf16)(y1 / rms);
-                    dst[h * HD + HALF + d] = (bf16)(y2 / rms);
+                    st_bf16x4(dst + h * HD + d0, make_float4(y1.x * inv, y1.y * inv, y1.z * inv, y1.w * inv));
+                    st_bf16x4(dst + h * HD + HALF + d0, make_float4(y2.x * inv, y2.y * inv, y2.z * inv, y2.w * inv));
                 }
             }
         } else {
