@@ -83,6 +83,10 @@ __device__ __forceinline__ bf16x8 trfrag(const bf16* tile, int rb, int s, int ct
     return __builtin_bit_cast(bf16x8, both);
 }
 
+// 2^x with the hardware's v_exp_f32: results below 2^-126 (probabilities
+// that change no fp32 sum they enter) flush to zero, and 2^-inf = 0.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // s_waitcnt vmcnt(0) (lgkmcnt / expcnt left open).  Issued once before a tile
 // loop: the loop body then starts with no vector-memory load outstanding on
 // any path, so the compiler does not make the first MFMAs of every tile wait
@@ -315,23 +319,27 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
             mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
             const float m_new = fmaxf(m, mt);
             const float m_use = m_new == -INFINITY ? 0.f : m_new;
-            const float alpha = exp2f(m - m_use);
+            const float alpha = exp2_fast(m - m_use);
             float rsum = 0.f;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const float p = exp2f(s[kb][e] - m_use);
+                    const float p = exp2_fast(s[kb][e] - m_use);
                     s[kb][e] = p;
                     rsum += p;
                 }
             rsum += __shfl_xor(rsum, 32, kWave);
             l = l * alpha + rsum;
             m = m_new;
+            // the running max moves on a few tiles only: skip the rescale
+            // (a multiply by 1) when it moved for no row of the wave
+            if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-            for (int dt = 0; dt < G::DT; ++dt)
+                for (int dt = 0; dt < G::DT; ++dt)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+                    for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+            }
             // O^T += V^T P^T, P rounded to bf16 once (the normaliser l keeps
             // the fp32 row sums).
 #pragma unroll
@@ -428,7 +436,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const bool ok = full || visible(kv0 + kb * 32 + acc_row(e, lane), my_q, T, window);
-                    const float p = ok ? exp2f(s[e] * scale_log2 - my_lse2) : 0.f;
+                    const float p = ok ? exp2_fast(s[e] * scale_log2 - my_lse2) : 0.f;
                     s[e] = p * (dp[e] - my_D);
                 }
                 // dQ^T += K^T dS^T
@@ -557,7 +565,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_k(RowOut out, const bf16*
                     for (int j = 0; j < 4; ++j) {
                         const int e = 4 * a + j;
                         const bool ok = full || (my_k < T && visible(my_k, qt0 + q4 + j, T, window));
-                        const float pv = ok ? exp2f(s[e] * scale_log2 - lv[j]) : 0.f;
+                        const float pv = ok ? exp2_fast(s[e] * scale_log2 - lv[j]) : 0.f;
                         s[e] = DO_DK ? pv * (dp[e] - dv4[j]) : pv;
                     }
                 }
