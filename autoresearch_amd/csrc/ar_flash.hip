@@ -306,17 +306,17 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
                 for (int ks = 0; ks < G::KSTEPS; ++ks)
                     s[kb] = mma(rowfrag<HD>(sK, kb * 32 + (lane & 31), ks, lane), qf[ks], s[kb]);
             }
+            // running max in log2 units: max of the raw scores, scaled once
+            // (the scale is positive), and p = 2^(s scale - m) as one fma
             float mt = -INFINITY;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    float x = s[kb][e] * scale_log2;
-                    if (!full && !visible(kv0 + kb * 32 + acc_row(e, lane), my_q, T, window)) x = -INFINITY;
-                    s[kb][e] = x;
-                    mt = fmaxf(mt, x);
+                    if (!full && !visible(kv0 + kb * 32 + acc_row(e, lane), my_q, T, window)) s[kb][e] = -INFINITY;
+                    mt = fmaxf(mt, s[kb][e]);
                 }
-            mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+            mt = fmaxf(mt, __shfl_xor(mt, 32, kWave)) * scale_log2;
             const float m_new = fmaxf(m, mt);
             const float m_use = m_new == -INFINITY ? 0.f : m_new;
             const float alpha = exp2_fast(m - m_use);
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const float p = exp2_fast(s[kb][e] - m_use);
+                    const float p = exp2_fast(fmaf(s[kb][e], scale_log2, -m_use));
                     s[kb][e] = p;
                     rsum += p;
                 }

@@ -118,6 +118,18 @@ __device__ __forceinline__ void st4(bf16* p, float4 x) {
 __device__ __forceinline__ float4 add4(float4 a, float4 b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
+// cap * tanh(x / cap) from the hardware exp2 and reciprocal:
+// tanh(y) = sign(y) (1 - 2 / (2^(2 |y| log2 e) + 1)), absolute error ~1e-7
+// (times cap); |y| large gives 2^inf = inf and exactly +-1.
+__device__ __forceinline__ float softcap(float x, float cap) {
+    const float y = fabsf(x) / cap;
+    const float e = __builtin_amdgcn_exp2f(2.8853900817779268f * y);  // 2 log2(e) y
+    const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+    return copysignf(cap * t, x);
+}
+__device__ __forceinline__ float4 softcap4(float4 x, float cap) {
+    return make_float4(softcap(x.x, cap), softcap(x.y, cap), softcap(x.z, cap), softcap(x.w, cap));
+}
 // d/dh relu(h)^2 times g, from the activation a = relu(h)^2: 2 sqrt(a) g (0 where a == 0).
 __device__ __forceinline__ float relu2_grad(float a, float g) { return a > 0.f ? 2.f * sqrtf(a) * g : 0.f; }
 
@@ -412,8 +424,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
                 st4(C + o, make_float4(x.x > 0.f ? x.x * x.x : 0.f, x.y > 0.f ? x.y * x.y : 0.f,
                                        x.z > 0.f ? x.z * x.z : 0.f, x.w > 0.f ? x.w * x.w : 0.f));
             } else if constexpr (EPI == EPI_SOFTCAP) {
-                st4(C + o, make_float4(cap * tanhf(x.x / cap), cap * tanhf(x.y / cap), cap * tanhf(x.z / cap),
-                                       cap * tanhf(x.w / cap)));
+                st4(C + o, softcap4(x, cap));
             } else if constexpr (EPI == EPI_RELU2_BWD) {
                 const float4 a = pre[PRE ? t : 0];
                 st4(C + o, make_float4(relu2_grad(a.x, x.x), relu2_grad(a.y, x.y), relu2_grad(a.z, x.z),
@@ -629,8 +640,7 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
                         st4(C + o, make_float4(x.x > 0.f ? x.x * x.x : 0.f, x.y > 0.f ? x.y * x.y : 0.f,
                                                x.z > 0.f ? x.z * x.z : 0.f, x.w > 0.f ? x.w * x.w : 0.f));
                     } else if constexpr (EPI == EPI_SOFTCAP) {
-                        st4(C + o, make_float4(cap * tanhf(x.x / cap), cap * tanhf(x.y / cap),
-                                               cap * tanhf(x.z / cap), cap * tanhf(x.w / cap)));
+                        st4(C + o, softcap4(x, cap));
                     } else if constexpr (EPI == EPI_RELU2_BWD) {
                         const float4 a = pre[PRE ? t : 0];
                         st4(C + o, make_float4(relu2_grad(a.x, x.x), relu2_grad(a.y, x.y), relu2_grad(a.z, x.z),
