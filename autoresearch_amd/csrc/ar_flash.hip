@@ -589,6 +589,143 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_k(RowOut out, const bf16*
     store_rows<HD>(at_head(out, b, h, T, HD), kw, T, acc, DO_DK ? scale : 1.0f, scratch, lane);
 }
 
+// dK and dV in one pass: S and dP are computed once per (key, query) tile,
+// P feeds dV^T += dO^T P and dS = P (dP - D) feeds dK^T += Q^T dS.  Both
+// accumulator sets (2 x 64 registers) stay live, so the next Q / dO tile
+// comes in by direct-to-LDS loads instead of through registers.
+template <int HD>
+__global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, RowOut out_v, const bf16* q,
+                                                               const bf16* k, const bf16* v, const bf16* dout,
+                                                               const float* lse, const float* dbuf, int B, int T,
+                                                               int H, int window, float scale_log2, float scale) {
+    using G = Geo<HD>;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    bf16* const lds = reinterpret_cast<bf16*>(smem_raw);
+    float* const sLD = reinterpret_cast<float*>(lds + 4 * G::TILE);
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int nkb = (T + kOwn - 1) / kOwn;
+    int bh, kblk;
+    block_coords(nkb, B * H, false, bh, kblk);
+    const int b = bh / H, h = bh % H;
+    const int k0 = kblk * kOwn, kw = k0 + wave * 32, my_k = kw + (lane & 31);
+    const int64_t rs = (int64_t)H * HD;
+    const int64_t boff = (int64_t)b * T * rs + (int64_t)h * HD;
+
+    bf16x8 kf[G::KSTEPS], vf[G::KSTEPS];
+    own_frags<HD>(kf, k + boff, rs, my_k, T, lane);
+    own_frags<HD>(vf, v + boff, rs, my_k, T, lane);
+
+    f32x16 adk[G::DT], adv[G::DT];
+#pragma unroll
+    for (int dt = 0; dt < G::DT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) adk[dt][e] = adv[dt][e] = 0.f;
+
+    const int qstart = (k0 / kTile) * kTile;
+    int qend = T;
+    if (window > 0 && k0 + kOwn - 1 + window + 1 < T) qend = k0 + kOwn - 1 + window + 1;
+    const int ntiles = qend > qstart ? (qend - qstart + kTile - 1) / kTile : 0;
+
+    // Direct-to-LDS tile load: slot id = i * kThreads + tid holds logical
+    // chunk (id % NCH) ^ swz(row) of row id / NCH, as TilePrefetch lays it
+    // out; rows past T repeat row T - 1 (their P and dS are masked to 0).
+    auto dma_tile = [&](bf16* dst, const bf16* base, int row0) {
+#pragma unroll
+        for (int i = 0; i < G::PER; ++i) {
+            const int id = i * kThreads + threadIdx.x;
+            const int r = id / G::NCH, c = (id % G::NCH) ^ G::swz(r);
+            const int row = row0 + r < T ? row0 + r : T - 1;
+            __builtin_amdgcn_global_load_lds(base + (int64_t)row * rs + c * 8,
+                                             (__attribute__((address_space(3))) void*)(dst + (i * kThreads + wave * kWave) * 8),
+                                             16, 0, 0);
+        }
+    };
+    float lv = 0.f, dl = 0.f;
+    auto load_ld = [&](int qt0) {
+        if (threadIdx.x < kTile) {
+            const int qq = qt0 + threadIdx.x;
+            const int64_t i = ((int64_t)b * T + (qq < T ? qq : 0)) * H + h;
+            lv = lse[i] * kLog2e;
+            dl = dbuf[i];
+        }
+    };
+    auto store_ld = [&](int stage) {
+        if (threadIdx.x < kTile) {
+            sLD[stage * 2 * kTile + threadIdx.x] = lv;
+            sLD[stage * 2 * kTile + kTile + threadIdx.x] = dl;
+        }
+    };
+    if (ntiles > 0) {
+        dma_tile(lds, q + boff, qstart);
+        dma_tile(lds + G::TILE, dout + boff, qstart);
+        load_ld(qstart);
+        store_ld(0);
+    }
+    wait_vmem();
+    __syncthreads();
+    for (int it = 0; it < ntiles; ++it) {
+        const int qt0 = qstart + it * kTile;
+        const int cur = it & 1;
+        const bool more = it + 1 < ntiles;
+        if (more) {
+            dma_tile(lds + (2 * (cur ^ 1)) * G::TILE, q + boff, qt0 + kTile);
+            dma_tile(lds + (2 * (cur ^ 1) + 1) * G::TILE, dout + boff, qt0 + kTile);
+            load_ld(qt0 + kTile);
+        }
+        const bf16* sQ = lds + (2 * cur) * G::TILE;
+        const bf16* sD = lds + (2 * cur + 1) * G::TILE;
+        const float* sL = sLD + cur * 2 * kTile;
+        const float* sDl = sL + kTile;
+        const bool skip = qt0 + kTile - 1 < kw || (window > 0 && qt0 > kw + 31 + window) || kw >= T;
+        if (!skip) {
+            const int lane = opaque_lane(threadIdx.x % kWave);
+            const bool full = qt0 >= kw + 31 && qt0 + kTile <= T && kw + 31 < T &&
+                              (window <= 0 || kw >= qt0 + kTile - 1 - window);
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                f32x16 s, dp;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.f;
+#pragma unroll
+                for (int ks = 0; ks < G::KSTEPS; ++ks) {
+                    s = mma(rowfrag<HD>(sQ, qb * 32 + (lane & 31), ks, lane), kf[ks], s);
+                    dp = mma(rowfrag<HD>(sD, qb * 32 + (lane & 31), ks, lane), vf[ks], dp);
+                }
+#pragma unroll
+                for (int a = 0; a < 4; ++a) {
+                    const int q4 = qb * 32 + 8 * a + 4 * (lane >> 5);
+                    const float4 l4 = *reinterpret_cast<const float4*>(sL + q4);
+                    const float4 d4 = *reinterpret_cast<const float4*>(sDl + q4);
+                    const float lvv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int e = 4 * a + j;
+                        const bool ok = full || (my_k < T && visible(my_k, qt0 + q4 + j, T, window));
+                        const float pv = ok ? exp2_fast(fmaf(s[e], scale_log2, -lvv[j])) : 0.f;
+                        s[e] = pv;
+                        dp[e] = pv * (dp[e] - dv4[j]);
+                    }
+                }
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    const bf16x8 fp = accfrag(s, st), fs = accfrag(dp, st);
+#pragma unroll
+                    for (int dt = 0; dt < G::DT; ++dt) {
+                        adv[dt] = mma(trfrag<HD>(sD, qb, st, dt, lane), fp, adv[dt]);
+                        adk[dt] = mma(trfrag<HD>(sQ, qb, st, dt, lane), fs, adk[dt]);
+                    }
+                }
+            }
+        }
+        if (more) store_ld(cur ^ 1);
+        wait_vmem();  // this thread's part of the next Q / dO tile has landed
+        __syncthreads();
+    }
+    float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 68;
+    store_rows<HD>(at_head(out_v, b, h, T, HD), kw, T, adv, 1.0f, scratch, lane);
+    store_rows<HD>(at_head(out_k, b, h, T, HD), kw, T, adk, scale, scratch, lane);
+}
+
 template <int HD>
 constexpr size_t fa2_lds(bool with_ld) {
     const size_t tiles = 4 * (size_t)Geo<HD>::TILE * sizeof(bf16) + (with_ld ? 4 * kTile * sizeof(float) : 0);
@@ -618,9 +755,7 @@ int32_t flash_hd(hipStream_t st, AttnOp op, float* o1, float* o2, const FlashOut
     }
     const RowOut ov{o2, fo.b2, rs, brs, nullptr, nullptr, 0, 1};
     const RowOut ok{o1, fo.b1, rs, brs, fo.cos_t, fo.sin_t, 0, period};
-    fa2_dkv_k<HD, kDV><<<grid, kThreads, fa2_lds<HD>(true), st>>>(ov, q, k, v, dout, lse, dbuf, B, T, H, window,
-                                                                  scale_log2, scale);
-    fa2_dkv_k<HD, kDK><<<grid, kThreads, fa2_lds<HD>(true), st>>>(ok, q, k, v, dout, lse, dbuf, B, T, H, window,
+    fa2_dkv_fused_k<HD><<<grid, kThreads, fa2_lds<HD>(true), st>>>(ok, ov, q, k, v, dout, lse, dbuf, B, T, H, window,
                                                                   scale_log2, scale);
     return check_launch("flash_attn_bwd_dkv (bf16 operands)");
 }
