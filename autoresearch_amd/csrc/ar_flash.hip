@@ -18,9 +18,9 @@
 //     logical chunk hit 16 different chunks (row fragments), and 4
 //     consecutive rows x 4 consecutive chunks hit 16 different chunks
 //     (transposed reads).
-//   * Double-buffered tiles: the next tile's global loads are issued into
-//     registers before the current tile's MFMAs and written to the other LDS
-//     stage after them (one barrier per tile).
+//   * Double-buffered tiles: the next tile goes from global memory straight
+//     into the other LDS stage (16-byte global_load_lds, no registers) while
+//     the current tile's MFMAs run; one wait + barrier per tile.
 //   * Blocks of one (batch, head) run on one XCD (K / V stay in its L2), and
 //     the causal work is issued heavy-first.
 //
@@ -110,28 +110,25 @@ __device__ __forceinline__ bf16x8 accfrag(const f32x16& a, int s) {
     return f;
 }
 
-// Global -> register prefetch of one 64-row tile (rows >= T read as zero).
+// Direct-to-LDS load of one 64-row tile into the swizzled natural layout
+// (16-byte slot id = i * kThreads + tid holds logical chunk
+// (id % NCH) ^ swz(row) of row id / NCH; a wave's 64 slots are one 1 KB
+// global_load_lds).  Rows past T repeat row T - 1: callers mask every score
+// of such a row to probability 0.
 template <int HD>
-struct TilePrefetch {
-    uint4 v[Geo<HD>::PER];
-    __device__ __forceinline__ void load(const bf16* base, int64_t rs, int row0, int T) {
+__device__ __forceinline__ void dma_tile(bf16* dst, const bf16* base, int64_t rs, int row0, int T) {
+    using G = Geo<HD>;
+    const int wave = threadIdx.x / kWave;
 #pragma unroll
-        for (int i = 0; i < Geo<HD>::PER; ++i) {
-            const int id = i * kThreads + threadIdx.x;
-            const int r = id / Geo<HD>::NCH, pos = id % Geo<HD>::NCH;
-            const int c = pos ^ Geo<HD>::swz(r);
-            v[i] = row0 + r < T ? *reinterpret_cast<const uint4*>(base + (int64_t)(row0 + r) * rs + c * 8)
-                                : make_uint4(0u, 0u, 0u, 0u);
-        }
+    for (int i = 0; i < G::PER; ++i) {
+        const int id = i * kThreads + threadIdx.x;
+        const int r = id / G::NCH, c = (id % G::NCH) ^ G::swz(r);
+        const int row = row0 + r < T ? row0 + r : T - 1;
+        __builtin_amdgcn_global_load_lds(base + (int64_t)row * rs + c * 8,
+                                         (__attribute__((address_space(3))) void*)(dst + (i * kThreads + wave * kWave) * 8),
+                                         16, 0, 0);
     }
-    __device__ __forceinline__ void store(bf16* tile) const {
-#pragma unroll
-        for (int i = 0; i < Geo<HD>::PER; ++i) {
-            const int id = i * kThreads + threadIdx.x;
-            *reinterpret_cast<uint4*>(tile + id * 8) = v[i];  // physical chunk order
-        }
-    }
-};
+}
 
 // B fragments of 32 own rows (row = row0 + lane % 32), read from global.
 template <int HD>
@@ -274,12 +271,9 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
     const int kend = (q0 + kOwn < T) ? q0 + kOwn : T;
     const int ntiles = kend > kstart ? (kend - kstart + kTile - 1) / kTile : 0;
 
-    TilePrefetch<HD> pk, pv;
     if (ntiles > 0) {
-        pk.load(k + boff, rs, kstart, T);
-        pv.load(v + boff, rs, kstart, T);
-        pk.store(lds);
-        pv.store(lds + G::TILE);
+        dma_tile<HD>(lds, k + boff, rs, kstart, T);
+        dma_tile<HD>(lds + G::TILE, v + boff, rs, kstart, T);
     }
     wait_vmem();
     __syncthreads();
@@ -288,8 +282,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
         const int cur = it & 1;
         const bool more = it + 1 < ntiles;
         if (more) {
-            pk.load(k + boff, rs, kv0 + kTile, T);
-            pv.load(v + boff, rs, kv0 + kTile, T);
+            dma_tile<HD>(lds + (2 * (cur ^ 1)) * G::TILE, k + boff, rs, kv0 + kTile, T);
+            dma_tile<HD>(lds + (2 * (cur ^ 1) + 1) * G::TILE, v + boff, rs, kv0 + kTile, T);
         }
         const bf16* sK = lds + (2 * cur) * G::TILE;
         const bf16* sV = lds + (2 * cur + 1) * G::TILE;
@@ -351,10 +345,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
                     for (int dt = 0; dt < G::DT; ++dt) o[dt] = mma(trfrag<HD>(sV, kb, st, dt, lane), ph, o[dt]);
                 }
         }
-        if (more) {
-            pk.store(lds + (2 * (cur ^ 1)) * G::TILE);
-            pv.store(lds + (2 * (cur ^ 1) + 1) * G::TILE);
-        }
+        wait_vmem();  // this thread's part of the next K / V tile has landed
         __syncthreads();
     }
     const float inv_l = l > 0.f ? 1.0f / l : 0.f;
@@ -399,12 +390,9 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
     const int kend = (q0 + kOwn < T) ? q0 + kOwn : T;
     const int ntiles = kend > kstart ? (kend - kstart + kTile - 1) / kTile : 0;
 
-    TilePrefetch<HD> pk, pv;
     if (ntiles > 0) {
-        pk.load(k + boff, rs, kstart, T);
-        pv.load(v + boff, rs, kstart, T);
-        pk.store(lds);
-        pv.store(lds + G::TILE);
+        dma_tile<HD>(lds, k + boff, rs, kstart, T);
+        dma_tile<HD>(lds + G::TILE, v + boff, rs, kstart, T);
     }
     wait_vmem();
     __syncthreads();
@@ -413,8 +401,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
         const int cur = it & 1;
         const bool more = it + 1 < ntiles;
         if (more) {
-            pk.load(k + boff, rs, kv0 + kTile, T);
-            pv.load(v + boff, rs, kv0 + kTile, T);
+            dma_tile<HD>(lds + (2 * (cur ^ 1)) * G::TILE, k + boff, rs, kv0 + kTile, T);
+            dma_tile<HD>(lds + (2 * (cur ^ 1) + 1) * G::TILE, v + boff, rs, kv0 + kTile, T);
         }
         const bf16* sK = lds + (2 * cur) * G::TILE;
         const bf16* sV = lds + (2 * cur + 1) * G::TILE;
@@ -448,10 +436,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
                 }
             }
         }
-        if (more) {
-            pk.store(lds + (2 * (cur ^ 1)) * G::TILE);
-            pv.store(lds + (2 * (cur ^ 1) + 1) * G::TILE);
-        }
+        wait_vmem();  // this thread's part of the next K / V tile has landed
         __syncthreads();
     }
     float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 68;
@@ -459,136 +444,6 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
 }
 
 // ============================ backward: dK, dV ============================
-// WHAT = kDV: S -> P -> dV^T += dO^T P; WHAT = kDK: S, dP -> dS ->
-// dK^T += Q^T dS.  Two kernels (each recomputing S) instead of one keep the
-// accumulators of each within 256 registers, so two workgroups share a CU.
-constexpr int kDV = 1, kDK = 2;
-template <int HD, int WHAT>
-__global__ __launch_bounds__(kThreads, 2) void fa2_dkv_k(RowOut out, const bf16* q, const bf16* k,
-                                                         const bf16* v, const bf16* dout, const float* lse,
-                                                         const float* dbuf, int B, int T, int H, int window,
-                                                         float scale_log2, float scale) {
-    constexpr bool DO_DV = (WHAT & kDV) != 0, DO_DK = (WHAT & kDK) != 0;
-    using G = Geo<HD>;
-    extern __shared__ __align__(16) unsigned char smem_raw[];
-    // stage s: Q at 2 s TILE, dO at (2 s + 1) TILE; then per stage 64 LSE + 64 D floats
-    bf16* const lds = reinterpret_cast<bf16*>(smem_raw);
-    float* const sLD = reinterpret_cast<float*>(lds + 4 * G::TILE);
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    const int nkb = (T + kOwn - 1) / kOwn;
-    int bh, kblk;
-    block_coords(nkb, B * H, false, bh, kblk);
-    const int b = bh / H, h = bh % H;
-    const int k0 = kblk * kOwn, kw = k0 + wave * 32, my_k = kw + (lane & 31);
-    const int64_t rs = (int64_t)H * HD;
-    const int64_t boff = (int64_t)b * T * rs + (int64_t)h * HD;
-
-    bf16x8 kf[G::KSTEPS], vf[DO_DK ? G::KSTEPS : 1];
-    own_frags<HD>(kf, k + boff, rs, my_k, T, lane);
-    if constexpr (DO_DK) own_frags<HD>(vf, v + boff, rs, my_k, T, lane);
-
-    f32x16 acc[G::DT];
-#pragma unroll
-    for (int dt = 0; dt < G::DT; ++dt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[dt][e] = 0.f;
-
-    const int qstart = (k0 / kTile) * kTile;
-    int qend = T;
-    if (window > 0 && k0 + kOwn - 1 + window + 1 < T) qend = k0 + kOwn - 1 + window + 1;
-    const int ntiles = qend > qstart ? (qend - qstart + kTile - 1) / kTile : 0;
-
-    TilePrefetch<HD> pq, pd;
-    float lv = 0.f, dl = 0.f;  // this thread's LSE / D prefetch (threads < 64)
-    auto load_ld = [&](int qt0) {
-        if (threadIdx.x < kTile) {
-            const int qq = qt0 + threadIdx.x;
-            const int64_t i = ((int64_t)b * T + (qq < T ? qq : 0)) * H + h;
-            lv = lse[i] * kLog2e;
-            dl = dbuf[i];
-        }
-    };
-    auto store_ld = [&](int stage) {
-        if (threadIdx.x < kTile) {
-            sLD[stage * 2 * kTile + threadIdx.x] = lv;
-            sLD[stage * 2 * kTile + kTile + threadIdx.x] = dl;
-        }
-    };
-    if (ntiles > 0) {
-        pq.load(q + boff, rs, qstart, T);
-        pd.load(dout + boff, rs, qstart, T);
-        load_ld(qstart);
-        pq.store(lds);
-        pd.store(lds + G::TILE);
-        store_ld(0);
-    }
-    wait_vmem();
-    __syncthreads();
-    for (int it = 0; it < ntiles; ++it) {
-        const int qt0 = qstart + it * kTile;
-        const int cur = it & 1;
-        const bool more = it + 1 < ntiles;
-        if (more) {
-            pq.load(q + boff, rs, qt0 + kTile, T);
-            pd.load(dout + boff, rs, qt0 + kTile, T);
-            load_ld(qt0 + kTile);
-        }
-        const bf16* sQ = lds + (2 * cur) * G::TILE;
-        const bf16* sD = lds + (2 * cur + 1) * G::TILE;
-        const float* sL = sLD + cur * 2 * kTile;
-        const float* sDl = sL + kTile;
-        const bool skip = qt0 + kTile - 1 < kw || (window > 0 && qt0 > kw + 31 + window) || kw >= T;
-        if (!skip) {
-            const int lane = opaque_lane(threadIdx.x % kWave);
-            // every (key, query) of the tile visible
-            const bool full = qt0 >= kw + 31 && qt0 + kTile <= T && kw + 31 < T &&
-                              (window <= 0 || kw >= qt0 + kTile - 1 - window);
-#pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-                f32x16 s, dp;
-#pragma unroll
-                for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.f;
-#pragma unroll
-                for (int ks = 0; ks < G::KSTEPS; ++ks) {
-                    s = mma(rowfrag<HD>(sQ, qb * 32 + (lane & 31), ks, lane), kf[ks], s);
-                    if constexpr (DO_DK) dp = mma(rowfrag<HD>(sD, qb * 32 + (lane & 31), ks, lane), vf[ks], dp);
-                }
-                // lane: key my_k; rows: queries qt0 + 32 qb + acc_row(e); s becomes P or dS.
-                // acc_row(4a + j) = 8a + 4 (lane / 32) + j: four consecutive rows per float4.
-#pragma unroll
-                for (int a = 0; a < 4; ++a) {
-                    const int q4 = qb * 32 + 8 * a + 4 * (lane >> 5);
-                    const float4 l4 = *reinterpret_cast<const float4*>(sL + q4);
-                    const float4 d4 = DO_DK ? *reinterpret_cast<const float4*>(sDl + q4) : make_float4(0.f, 0.f, 0.f, 0.f);
-                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int e = 4 * a + j;
-                        const bool ok = full || (my_k < T && visible(my_k, qt0 + q4 + j, T, window));
-                        const float pv = ok ? exp2_fast(s[e] * scale_log2 - lv[j]) : 0.f;
-                        s[e] = DO_DK ? pv * (dp[e] - dv4[j]) : pv;
-                    }
-                }
-#pragma unroll
-                for (int st = 0; st < 2; ++st) {
-                    const bf16x8 fb = accfrag(s, st);
-#pragma unroll
-                    for (int dt = 0; dt < G::DT; ++dt)
-                        acc[dt] = mma(trfrag<HD>(DO_DK ? sQ : sD, qb, st, dt, lane), fb, acc[dt]);
-                }
-            }
-        }
-        if (more) {
-            pq.store(lds + (2 * (cur ^ 1)) * G::TILE);
-            pd.store(lds + (2 * (cur ^ 1) + 1) * G::TILE);
-            store_ld(cur ^ 1);
-        }
-        __syncthreads();
-    }
-    float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 68;
-    store_rows<HD>(at_head(out, b, h, T, HD), kw, T, acc, DO_DK ? scale : 1.0f, scratch, lane);
-}
-
 // dK and dV in one pass: S and dP are computed once per (key, query) tile,
 // P feeds dV^T += dO^T P and dS = P (dP - D) feeds dK^T += Q^T dS.  Both
 // accumulator sets (2 x 64 registers) stay live, so the next Q / dO tile
@@ -626,20 +481,6 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
     if (window > 0 && k0 + kOwn - 1 + window + 1 < T) qend = k0 + kOwn - 1 + window + 1;
     const int ntiles = qend > qstart ? (qend - qstart + kTile - 1) / kTile : 0;
 
-    // Direct-to-LDS tile load: slot id = i * kThreads + tid holds logical
-    // chunk (id % NCH) ^ swz(row) of row id / NCH, as TilePrefetch lays it
-    // out; rows past T repeat row T - 1 (their P and dS are masked to 0).
-    auto dma_tile = [&](bf16* dst, const bf16* base, int row0) {
-#pragma unroll
-        for (int i = 0; i < G::PER; ++i) {
-            const int id = i * kThreads + threadIdx.x;
-            const int r = id / G::NCH, c = (id % G::NCH) ^ G::swz(r);
-            const int row = row0 + r < T ? row0 + r : T - 1;
-            __builtin_amdgcn_global_load_lds(base + (int64_t)row * rs + c * 8,
-                                             (__attribute__((address_space(3))) void*)(dst + (i * kThreads + wave * kWave) * 8),
-                                             16, 0, 0);
-        }
-    };
     float lv = 0.f, dl = 0.f;
     auto load_ld = [&](int qt0) {
         if (threadIdx.x < kTile) {
@@ -656,8 +497,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
         }
     };
     if (ntiles > 0) {
-        dma_tile(lds, q + boff, qstart);
-        dma_tile(lds + G::TILE, dout + boff, qstart);
+        dma_tile<HD>(lds, q + boff, rs, qstart, T);
+        dma_tile<HD>(lds + G::TILE, dout + boff, rs, qstart, T);
         load_ld(qstart);
         store_ld(0);
     }
@@ -668,8 +509,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
         const int cur = it & 1;
         const bool more = it + 1 < ntiles;
         if (more) {
-            dma_tile(lds + (2 * (cur ^ 1)) * G::TILE, q + boff, qt0 + kTile);
-            dma_tile(lds + (2 * (cur ^ 1) + 1) * G::TILE, dout + boff, qt0 + kTile);
+            dma_tile<HD>(lds + (2 * (cur ^ 1)) * G::TILE, q + boff, rs, qt0 + kTile, T);
+            dma_tile<HD>(lds + (2 * (cur ^ 1) + 1) * G::TILE, dout + boff, rs, qt0 + kTile, T);
             load_ld(qt0 + kTile);
         }
         const bf16* sQ = lds + (2 * cur) * G::TILE;
