@@ -115,13 +115,18 @@ __device__ __forceinline__ bf16x8 accfrag(const f32x16& a, int s) {
 // (id % NCH) ^ swz(row) of row id / NCH; a wave's 64 slots are one 1 KB
 // global_load_lds).  Rows past T repeat row T - 1: callers mask every score
 // of such a row to probability 0.
+// The thread index is made opaque per call, so the per-slot address math is
+// redone at each tile (a few VALU ops) rather than hoisted out of the tile
+// loop into registers that would spill.
 template <int HD>
 __device__ __forceinline__ void dma_tile(bf16* dst, const bf16* base, int64_t rs, int row0, int T) {
     using G = Geo<HD>;
-    const int wave = threadIdx.x / kWave;
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
 #pragma unroll
     for (int i = 0; i < G::PER; ++i) {
-        const int id = i * kThreads + threadIdx.x;
+        const int id = i * kThreads + tid;
         const int r = id / G::NCH, c = (id % G::NCH) ^ G::swz(r);
         const int row = row0 + r < T ? row0 + r : T - 1;
         __builtin_amdgcn_global_load_lds(base + (int64_t)row * rs + c * 8,
