@@ -110,7 +110,7 @@ __device__ __forceinline__ bf16x8 accfrag(const f32x16& a, int s) {
     return f;
 }
 
-// Direct-to-LDS load of one 64-row tile into the swizzled natural layout
+// Direct-to-LDS load of one ROWS-row tile into the swizzled natural layout
 // (16-byte slot id = i * kThreads + tid holds logical chunk
 // (id % NCH) ^ swz(row) of row id / NCH; a wave's 64 slots are one 1 KB
 // global_load_lds).  Rows past T repeat row T - 1: callers mask every score
@@ -118,15 +118,17 @@ __device__ __forceinline__ bf16x8 accfrag(const f32x16& a, int s) {
 // The thread index is made opaque per call, so the per-slot address math is
 // redone at each tile (a few VALU ops) rather than hoisted out of the tile
 // loop into registers that would spill.
-template <int HD>
+template <int HD, int ROWS = kTile>
 __device__ __forceinline__ void dma_tile(bf16* dst, const bf16* base, int64_t rs, int row0, int T) {
     using G = Geo<HD>;
+    constexpr int UNITS = ROWS * G::NCH;  // a multiple of 64: the guard below is wave-uniform
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
 #pragma unroll
-    for (int i = 0; i < G::PER; ++i) {
+    for (int i = 0; i < (UNITS + kThreads - 1) / kThreads; ++i) {
         const int id = i * kThreads + tid;
+        if (UNITS % kThreads != 0 && i * kThreads + wave * kWave >= UNITS) break;
         const int r = id / G::NCH, c = (id % G::NCH) ^ G::swz(r);
         const int row = row0 + r < T ? row0 + r : T - 1;
         __builtin_amdgcn_global_load_lds(base + (int64_t)row * rs + c * 8,
@@ -451,17 +453,33 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
 // ============================ backward: dK, dV ============================
 // dK and dV in one pass: S and dP are computed once per (key, query) tile,
 // P feeds dV^T += dO^T P and dS = P (dP - D) feeds dK^T += Q^T dS.  Both
-// accumulator sets (2 x 64 registers) stay live, so the next Q / dO tile
-// comes in by direct-to-LDS loads instead of through registers.
+// accumulator sets (2 x 64 registers at hd 128) and the own K fragments stay
+// in registers; the own V rows live in LDS (read as row fragments for dP), so
+// two workgroups still share a CU without spills.  Q / dO stream in 32-row
+// tiles (double-buffered, direct-to-LDS).
+constexpr int kDkvTile = 32;
+
+template <int HD>
+constexpr size_t dkv_fused_lds() {
+    const size_t tiles = 4 * (size_t)kDkvTile * HD * sizeof(bf16);  // Q, dO x 2 stages
+    const size_t own_v = (size_t)kOwn * HD * sizeof(bf16);
+    const size_t ld = 4 * kDkvTile * sizeof(float);                 // LSE, D x 2 stages
+    const size_t loop = tiles + own_v + ld;
+    const size_t stage = 4 * 32 * 68 * sizeof(float);               // store_rows staging
+    return loop > stage ? loop : stage;
+}
+
 template <int HD>
 __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, RowOut out_v, const bf16* q,
                                                                const bf16* k, const bf16* v, const bf16* dout,
                                                                const float* lse, const float* dbuf, int B, int T,
                                                                int H, int window, float scale_log2, float scale) {
     using G = Geo<HD>;
+    constexpr int KT = kDkvTile, TT = KT * HD;  // rows, bf16 elements per streamed tile
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    bf16* const lds = reinterpret_cast<bf16*>(smem_raw);
-    float* const sLD = reinterpret_cast<float*>(lds + 4 * G::TILE);
+    bf16* const lds = reinterpret_cast<bf16*>(smem_raw);  // stage s: Q at 2 s TT, dO at (2 s + 1) TT
+    bf16* const sV = lds + 4 * TT;                        // the workgroup's own 128 V rows
+    float* const sLD = reinterpret_cast<float*>(sV + kOwn * HD);
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int nkb = (T + kOwn - 1) / kOwn;
     int bh, kblk;
@@ -471,9 +489,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
     const int64_t rs = (int64_t)H * HD;
     const int64_t boff = (int64_t)b * T * rs + (int64_t)h * HD;
 
-    bf16x8 kf[G::KSTEPS], vf[G::KSTEPS];
+    bf16x8 kf[G::KSTEPS];
     own_frags<HD>(kf, k + boff, rs, my_k, T, lane);
-    own_frags<HD>(vf, v + boff, rs, my_k, T, lane);
 
     f32x16 adk[G::DT], adv[G::DT];
 #pragma unroll
@@ -481,14 +498,14 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
 #pragma unroll
         for (int e = 0; e < 16; ++e) adk[dt][e] = adv[dt][e] = 0.f;
 
-    const int qstart = (k0 / kTile) * kTile;
+    const int qstart = (k0 / KT) * KT;
     int qend = T;
     if (window > 0 && k0 + kOwn - 1 + window + 1 < T) qend = k0 + kOwn - 1 + window + 1;
-    const int ntiles = qend > qstart ? (qend - qstart + kTile - 1) / kTile : 0;
+    const int ntiles = qend > qstart ? (qend - qstart + KT - 1) / KT : 0;
 
-    float lv = 0.f, dl = 0.f;
+    float lv = 0.f, dl = 0.f;  // this thread's LSE / D prefetch (threads < KT)
     auto load_ld = [&](int qt0) {
-        if (threadIdx.x < kTile) {
+        if (threadIdx.x < KT) {
             const int qq = qt0 + threadIdx.x;
             const int64_t i = ((int64_t)b * T + (qq < T ? qq : 0)) * H + h;
             lv = lse[i] * kLog2e;
@@ -496,70 +513,69 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
         }
     };
     auto store_ld = [&](int stage) {
-        if (threadIdx.x < kTile) {
-            sLD[stage * 2 * kTile + threadIdx.x] = lv;
-            sLD[stage * 2 * kTile + kTile + threadIdx.x] = dl;
+        if (threadIdx.x < KT) {
+            sLD[stage * 2 * KT + threadIdx.x] = lv;
+            sLD[stage * 2 * KT + KT + threadIdx.x] = dl;
         }
     };
+    dma_tile<HD, kOwn>(sV, v + boff, rs, k0, T);
     if (ntiles > 0) {
-        dma_tile<HD>(lds, q + boff, rs, qstart, T);
-        dma_tile<HD>(lds + G::TILE, dout + boff, rs, qstart, T);
+        dma_tile<HD, KT>(lds, q + boff, rs, qstart, T);
+        dma_tile<HD, KT>(lds + TT, dout + boff, rs, qstart, T);
         load_ld(qstart);
         store_ld(0);
     }
     wait_vmem();
     __syncthreads();
     for (int it = 0; it < ntiles; ++it) {
-        const int qt0 = qstart + it * kTile;
+        const int qt0 = qstart + it * KT;
         const int cur = it & 1;
         const bool more = it + 1 < ntiles;
         if (more) {
-            dma_tile<HD>(lds + (2 * (cur ^ 1)) * G::TILE, q + boff, rs, qt0 + kTile, T);
-            dma_tile<HD>(lds + (2 * (cur ^ 1) + 1) * G::TILE, dout + boff, rs, qt0 + kTile, T);
-            load_ld(qt0 + kTile);
+            dma_tile<HD, KT>(lds + (2 * (cur ^ 1)) * TT, q + boff, rs, qt0 + KT, T);
+            dma_tile<HD, KT>(lds + (2 * (cur ^ 1) + 1) * TT, dout + boff, rs, qt0 + KT, T);
+            load_ld(qt0 + KT);
         }
-        const bf16* sQ = lds + (2 * cur) * G::TILE;
-        const bf16* sD = lds + (2 * cur + 1) * G::TILE;
-        const float* sL = sLD + cur * 2 * kTile;
-        const float* sDl = sL + kTile;
-        const bool skip = qt0 + kTile - 1 < kw || (window > 0 && qt0 > kw + 31 + window) || kw >= T;
+        const bf16* sQ = lds + (2 * cur) * TT;
+        const bf16* sD = lds + (2 * cur + 1) * TT;
+        const float* sL = sLD + cur * 2 * KT;
+        const float* sDl = sL + KT;
+        const bool skip = qt0 + KT - 1 < kw || (window > 0 && qt0 > kw + 31 + window) || kw >= T;
         if (!skip) {
             const int lane = opaque_lane(threadIdx.x % kWave);
-            const bool full = qt0 >= kw + 31 && qt0 + kTile <= T && kw + 31 < T &&
-                              (window <= 0 || kw >= qt0 + kTile - 1 - window);
+            const bool full = qt0 >= kw + 31 && qt0 + KT <= T && kw + 31 < T &&
+                              (window <= 0 || kw >= qt0 + KT - 1 - window);
+            f32x16 s, dp;
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-                f32x16 s, dp;
+            for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.f;
 #pragma unroll
-                for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.f;
+            for (int ks = 0; ks < G::KSTEPS; ++ks) {
+                s = mma(rowfrag<HD>(sQ, lane & 31, ks, lane), kf[ks], s);
+                dp = mma(rowfrag<HD>(sD, lane & 31, ks, lane), rowfrag<HD>(sV, wave * 32 + (lane & 31), ks, lane), dp);
+            }
+            // lane: key my_k; rows: queries qt0 + acc_row(e); s becomes P, dp becomes dS.
 #pragma unroll
-                for (int ks = 0; ks < G::KSTEPS; ++ks) {
-                    s = mma(rowfrag<HD>(sQ, qb * 32 + (lane & 31), ks, lane), kf[ks], s);
-                    dp = mma(rowfrag<HD>(sD, qb * 32 + (lane & 31), ks, lane), vf[ks], dp);
+            for (int a = 0; a < 4; ++a) {
+                const int q4 = 8 * a + 4 * (lane >> 5);
+                const float4 l4 = *reinterpret_cast<const float4*>(sL + q4);
+                const float4 d4 = *reinterpret_cast<const float4*>(sDl + q4);
+                const float lvv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int e = 4 * a + j;
+                    const bool ok = full || (my_k < T && visible(my_k, qt0 + q4 + j, T, window));
+                    const float pv = ok ? exp2_fast(fmaf(s[e], scale_log2, -lvv[j])) : 0.f;
+                    s[e] = pv;
+                    dp[e] = pv * (dp[e] - dv4[j]);
                 }
+            }
 #pragma unroll
-                for (int a = 0; a < 4; ++a) {
-                    const int q4 = qb * 32 + 8 * a + 4 * (lane >> 5);
-                    const float4 l4 = *reinterpret_cast<const float4*>(sL + q4);
-                    const float4 d4 = *reinterpret_cast<const float4*>(sDl + q4);
-                    const float lvv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+            for (int st = 0; st < 2; ++st) {
+                const bf16x8 fp = accfrag(s, st), fs = accfrag(dp, st);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int e = 4 * a + j;
-                        const bool ok = full || (my_k < T && visible(my_k, qt0 + q4 + j, T, window));
-                        const float pv = ok ? exp2_fast(fmaf(s[e], scale_log2, -lvv[j])) : 0.f;
-                        s[e] = pv;
-                        dp[e] = pv * (dp[e] - dv4[j]);
-                    }
-                }
-#pragma unroll
-                for (int st = 0; st < 2; ++st) {
-                    const bf16x8 fp = accfrag(s, st), fs = accfrag(dp, st);
-#pragma unroll
-                    for (int dt = 0; dt < G::DT; ++dt) {
-                        adv[dt] = mma(trfrag<HD>(sD, qb, st, dt, lane), fp, adv[dt]);
-                        adk[dt] = mma(trfrag<HD>(sQ, qb, st, dt, lane), fs, adk[dt]);
-                    }
+                for (int dt = 0; dt < G::DT; ++dt) {
+                    adv[dt] = mma(trfrag<HD>(sD, 0, st, dt, lane), fp, adv[dt]);
+                    adk[dt] = mma(trfrag<HD>(sQ, 0, st, dt, lane), fs, adk[dt]);
                 }
             }
         }
@@ -601,8 +617,8 @@ int32_t flash_hd(hipStream_t st, AttnOp op, float* o1, float* o2, const FlashOut
     }
     const RowOut ov{o2, fo.b2, rs, brs, nullptr, nullptr, 0, 1};
     const RowOut ok{o1, fo.b1, rs, brs, fo.cos_t, fo.sin_t, 0, period};
-    fa2_dkv_fused_k<HD><<<grid, kThreads, fa2_lds<HD>(true), st>>>(ok, ov, q, k, v, dout, lse, dbuf, B, T, H, window,
-                                                                  scale_log2, scale);
+    fa2_dkv_fused_k<HD><<<grid, kThreads, dkv_fused_lds<HD>(), st>>>(ok, ov, q, k, v, dout, lse, dbuf, B, T, H,
+                                                                    window, scale_log2, scale);
     return check_launch("flash_attn_bwd_dkv (bf16 operands)");
 }
 
