@@ -73,6 +73,11 @@ struct FlashOut {
     const float* cos_t = nullptr;
     const float* sin_t = nullptr;
     int64_t period = 0;
+    // DQ only: when set, D = rowsum(dO * O) is formed in the dQ kernel from O
+    // (fp32, [B, T, H, hd]) and the lane's own dO row, written to d_out for
+    // the dK / dV kernel, instead of being read from dbuf.
+    const float* o_for_d = nullptr;
+    float* d_out = nullptr;
 };
 int32_t flash_attn_bf16(hipStream_t st, AttnOp op, float* o1, float* o2, const FlashOut& fo, const bf16* q,
                         const bf16* k, const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int64_t B,

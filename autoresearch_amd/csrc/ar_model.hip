@@ -587,17 +587,21 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
                       false));
         AR_TRY(gemm_b(m, 2, 2, G(m, m->i_proj[i]), false, m->grad_xb, true, b.attn_out_b, true, BT, C, C, true));
         const int64_t ws = window_size(c, i);
-        AR_TRY(precompute_d_mixed(st, m->d_buf, b.attn_out, m->grad_attn_out_b, BT * H, hd));
         // dQ | dK | dV straight into the packed bf16 [BT, 3C] buffer, dQ / dK
-        // rotated back by the inverse rope (rope_bwd; Q6: q/k norm backward skipped)
+        // rotated back by the inverse rope (rope_bwd; Q6: q/k norm backward skipped).
+        // The dQ kernel also forms D = rowsum(dO * O) (precompute_d) into d_buf for dK / dV.
         FlashOut fo;
         fo.brs = 3 * C;
         fo.cos_t = m->rope_cos;
         fo.sin_t = m->rope_sin;
         fo.period = m->period;
         fo.b1 = m->grad_qkv;
+        fo.o_for_d = b.attn_out;
+        fo.d_out = m->d_buf;
         AR_TRY(attention_b(m, AttnOp::DQ, nullptr, nullptr, fo, b.q, b.k, b.v, m->grad_attn_out_b, b.lse, m->d_buf,
                            ws));
+        fo.o_for_d = nullptr;
+        fo.d_out = nullptr;
         fo.b1 = m->grad_qkv + C;
         fo.b2 = m->grad_qkv + 2 * C;
         AR_TRY(attention_b(m, AttnOp::DKV, nullptr, nullptr, fo, b.q, b.k, b.v, m->grad_attn_out_b, b.lse, m->d_buf,
