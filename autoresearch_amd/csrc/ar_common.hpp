@@ -74,6 +74,31 @@ template <typename T> __device__ __forceinline__ T from_f32(float v);
 template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf16)v; }
 
+// Direct global -> LDS loads (global_load_lds_dword{,x4}): lane i writes LDS
+// bytes [lds + size * i, +size), lds wave-uniform.  Issued from inline asm
+// so that the compiler does not treat later LDS reads as possibly aliasing
+// the in-flight copy (it would wait for every outstanding prefetch before
+// them); callers order the copies with an explicit s_waitcnt vmcnt and a
+// barrier.  Compiler-tracked global loads issued after one of these are
+// waited for with counts that ignore it, which waits for it too (loads
+// complete in order): keep such loads ahead of the copies they should not
+// wait for.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+    return (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+__device__ __forceinline__ void dma16(const void* g, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* g, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
+                 : "memory", "m0");
+}
+
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Grid for a flat element-wise kernel: grid-stride loops, capped so a launch

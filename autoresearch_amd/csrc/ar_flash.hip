@@ -131,9 +131,7 @@ __device__ __forceinline__ void dma_tile(bf16* dst, const bf16* base, int64_t rs
         if (UNITS % kThreads != 0 && i * kThreads + wave * kWave >= UNITS) break;
         const int r = id / G::NCH, c = (id % G::NCH) ^ G::swz(r);
         const int row = row0 + r < T ? row0 + r : T - 1;
-        __builtin_amdgcn_global_load_lds(base + (int64_t)row * rs + c * 8,
-                                         (__attribute__((address_space(3))) void*)(dst + (i * kThreads + wave * kWave) * 8),
-                                         16, 0, 0);
+        dma16(base + (int64_t)row * rs + c * 8, lds_addr(dst + (i * kThreads + wave * kWave) * 8));
     }
 }
 
@@ -524,27 +522,21 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
     if (window > 0 && k0 + kOwn - 1 + window + 1 < T) qend = k0 + kOwn - 1 + window + 1;
     const int ntiles = qend > qstart ? (qend - qstart + KT - 1) / KT : 0;
 
-    float lv = 0.f, dl = 0.f;  // this thread's LSE / D prefetch (threads < KT)
-    auto load_ld = [&](int qt0) {
-        if (threadIdx.x < KT) {
-            const int qq = qt0 + threadIdx.x;
+    // LSE / D of a query tile straight into LDS: wave 0, lanes 0..KT-1 the
+    // LSE values, lanes KT..2 KT-1 the D values (4-byte copies, rows past T
+    // repeat row 0; their scores are masked)
+    auto dma_ld = [&](int qt0, int stage) {
+        if (wave == 0) {
+            const int j = lane % KT, qq = qt0 + j;
             const int64_t i = ((int64_t)b * T + (qq < T ? qq : 0)) * H + h;
-            lv = lse[i] * kLog2e;
-            dl = dbuf[i];
-        }
-    };
-    auto store_ld = [&](int stage) {
-        if (threadIdx.x < KT) {
-            sLD[stage * 2 * KT + threadIdx.x] = lv;
-            sLD[stage * 2 * KT + KT + threadIdx.x] = dl;
+            dma4(lane < KT ? lse + i : dbuf + i, lds_addr(sLD + stage * 2 * KT));
         }
     };
     dma_tile<HD, kOwn>(sV, v + boff, rs, k0, T);
     if (ntiles > 0) {
         dma_tile<HD, KT>(lds, q + boff, rs, qstart, T);
         dma_tile<HD, KT>(lds + TT, dout + boff, rs, qstart, T);
-        load_ld(qstart);
-        store_ld(0);
+        dma_ld(qstart, 0);
     }
     wait_vmem();
     __syncthreads();
@@ -555,7 +547,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
         if (more) {
             dma_tile<HD, KT>(lds + (2 * (cur ^ 1)) * TT, q + boff, rs, qt0 + KT, T);
             dma_tile<HD, KT>(lds + (2 * (cur ^ 1) + 1) * TT, dout + boff, rs, qt0 + KT, T);
-            load_ld(qt0 + KT);
+            dma_ld(qt0 + KT, cur ^ 1);
         }
         const bf16* sQ = lds + (2 * cur) * TT;
         const bf16* sD = lds + (2 * cur + 1) * TT;
@@ -580,7 +572,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
                 const int q4 = 8 * a + 4 * (lane >> 5);
                 const float4 l4 = *reinterpret_cast<const float4*>(sL + q4);
                 const float4 d4 = *reinterpret_cast<const float4*>(sDl + q4);
-                const float lvv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+                const float lvv[4] = {l4.x * kLog2e, l4.y * kLog2e, l4.z * kLog2e, l4.w * kLog2e};
+                const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int e = 4 * a + j;
@@ -600,8 +593,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
                 }
             }
         }
-        if (more) store_ld(cur ^ 1);
-        wait_vmem();  // this thread's part of the next Q / dO tile has landed
+        wait_vmem();  // this thread's part of the next Q / dO tile (and its LSE / D) has landed
         __syncthreads();
     }
     float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 68;

@@ -483,18 +483,6 @@ __device__ __forceinline__ void vm_wait() {
     __builtin_amdgcn_s_waitcnt(N | 0x0F70);  // vmcnt(N), expcnt / lgkmcnt not waited
 }
 
-// One 16-byte global -> LDS load per lane (global_load_lds_dwordx4): lane i
-// writes LDS bytes [lds + 16 i, +16).  Issued from inline asm, so the
-// compiler does not treat later LDS reads as dependent on it (it would
-// otherwise wait for every in-flight prefetch before the epilogue's LDS
-// staging); the k-loop's explicit vmcnt wait + barrier orders the tiles.
-__device__ __forceinline__ void dma16(const void* g, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-                 :
-                 : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
-                 : "memory", "m0");
-}
-
 // Issues the DMA of one operand tile (4 wave-instructions per thread).
 template <bool KMAJ>
 __device__ __forceinline__ void pk_dma(unsigned char* dst, const bf16* g, int64_t ld, int64_t row0, int64_t k0,
@@ -510,7 +498,7 @@ __device__ __forceinline__ void pk_dma(unsigned char* dst, const bf16* g, int64_
             const int k = slot >> 5, c = (slot & 31) ^ tr_swz(k);
             src = g + (k0 + k) * ld + row0 + c * 8;
         }
-        dma16(src, (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)(dst + (j * 8 + wave) * 1024));
+        dma16(src, lds_addr(dst + (j * 8 + wave) * 1024));
     }
 }
 
