@@ -37,7 +37,8 @@ CFLAGS = [
     "-Wno-unused-function",
     "-Wno-unused-result",
     "-munsafe-fp-atomics",
-    # Packed-fp32 VALU ops are disabled on this pool.
+    # Packed-fp32 VALU ops (v_pk_*_f32) are kept out of every kernel: some of
+    # their forms have given silently wrong results on this hardware pool.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{os.path.join(ROOT, 'include')}",
 ]

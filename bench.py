@@ -52,7 +52,7 @@ def zipf_tokens(n: int, V: int, s: float, seed: int) -> np.ndarray:
 
 
 def step_flops(L, C, V, B, T, H, hd, windows, mats) -> float:
-    """Algorithmic FLOPs of one training step (SURVEY 8(d) formula):
+    """Algorithmic FLOPs of one training step (2 flop per multiply-add; backward = 2x forward):
     GEMMs 72*L*M*C^2 + 6*M*C*V, attention 14*B*H*hd*sum_layers sum_q keys(q),
     Muon 5*sum(4*l*s^2 + 2*s^3)."""
     M = B * T
