@@ -92,6 +92,14 @@ __device__ __forceinline__ void dma16(const void* g, unsigned lds) {
                  : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
                  : "memory", "m0");
 }
+// The same with a wave-uniform base address (an SGPR pair) plus a per-lane
+// 32-bit byte offset: no per-lane 64-bit address arithmetic per copy.
+__device__ __forceinline__ void dma16s(const void* base, unsigned voff, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(lds), "v"(voff), "s"(base)
+                 : "memory", "m0");
+}
 __device__ __forceinline__ void dma4(const void* g, unsigned lds) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
                  :

@@ -472,7 +472,9 @@ __global__ void splitk_reduce_k(TC* C, const float* partial, int64_t M, int64_t 
 //     k*32 + (c ^ tr_swz(k)), read with tr_frag as in gemm_k.
 // A lane's DMA slot is fixed (wave-instruction j of wave w fills slots
 // (8j + w)*64 + lane), so the swizzle is applied to the global address the
-// lane fetches.  The epilogue stages 16-row half strips (fp32) in a separate
+// lane fetches: a per-lane 32-bit offset fixed for the whole kernel, added to
+// a wave-uniform (SGPR) base that moves by one k-tile per copy and is set
+// once per tile, so a copy costs a few scalar instructions.  The epilogue stages 16-row half strips (fp32) in a separate
 // 32 KB region.  Shapes: M, N % 256, K (per split) % 64, lda/ldb % 8.
 constexpr int kPkThreads = 512, kPkBK = 64, kPkStage = 2 * 256 * kPkBK * 2;  // bytes per stage (A + B)
 constexpr int kPkLds = 2 * kPkStage + 8 * 16 * 64 * 4;                      // 160 KB
@@ -483,35 +485,34 @@ __device__ __forceinline__ void vm_wait() {
     __builtin_amdgcn_s_waitcnt(N | 0x0F70);  // vmcnt(N), expcnt / lgkmcnt not waited
 }
 
-// Issues the DMA of one operand tile (4 wave-instructions per thread).
+// Per-lane byte offsets of the 4 DMA wave-instructions that fill one operand
+// tile, relative to the tile's first element (row0, k0): slot (8j + w)*64 +
+// lane of wave w, swizzled as the tile layout above says.  Constant for the
+// whole kernel; the tile position goes into a wave-uniform base address.
 template <bool KMAJ>
-__device__ __forceinline__ void pk_dma(unsigned char* dst, const bf16* g, int64_t ld, int64_t row0, int64_t k0,
-                                       int wave, int lane) {
+__device__ __forceinline__ void pk_offsets(unsigned (&off)[4], int ld, int wave, int lane) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int slot = (j * 8 + wave) * 64 + lane;
-        const bf16* src;
         if constexpr (KMAJ) {
             const int r = slot >> 3, c = (slot & 7) ^ ((r >> 1) & 7);
-            src = g + (row0 + r) * ld + k0 + c * 8;
+            off[j] = (unsigned)(r * ld + c * 8) * 2u;
         } else {
             const int k = slot >> 5, c = (slot & 31) ^ tr_swz(k);
-            src = g + (k0 + k) * ld + row0 + c * 8;
+            off[j] = (unsigned)(k * ld + c * 8) * 2u;
         }
-        dma16(src, lds_addr(dst + (j * 8 + wave) * 1024));
     }
 }
 
 // Work item -> (split z, tile_m, tile_n); each XCD (workgroups are dispatched
 // round-robin over 8) owns a contiguous run of items.
-__device__ __forceinline__ void pk_item(int64_t lin, int64_t items, int64_t tiles_n, int64_t tiles_mn, int64_t& z,
-                                        int64_t& tm, int64_t& tn) {
-    int64_t id = lin;
+__device__ __forceinline__ void pk_item(int lin, int items, int tiles_n, int tiles_mn, int& z, int& tm, int& tn) {
+    int id = lin;
     if (items % 8 == 0 && gridDim.x % 8 == 0) id = (lin % 8) * (items / 8) + lin / 8;
     z = id / tiles_mn;
-    const int64_t r = id % tiles_mn;
+    const int r = id - z * tiles_mn;
     tm = r / tiles_n;
-    tn = r % tiles_n;
+    tn = r - tm * tiles_n;
 }
 
 template <bool AK, bool BKM, typename TC, int EPI>
@@ -524,20 +525,41 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
     const int lane = threadIdx.x % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int wm = wave >> 2, wn = wave & 3;
-    const int64_t tiles_n = N / 256, tiles_mn = (M / 256) * tiles_n, items = tiles_mn * splits;
-    const int64_t grid = gridDim.x, b = blockIdx.x;
+    const int tiles_n = (int)(N / 256), tiles_mn = (int)(M / 256) * tiles_n, items = tiles_mn * (int)splits;
+    const int grid = (int)gridDim.x, b = (int)blockIdx.x;
     const int nk = (int)(kps / kPkBK);
-    const int nmine = (int)((items - b + grid - 1) / grid);
+    const int nmine = (items - b + grid - 1) / grid;
     const int G = nmine * nk;  // k-tiles this workgroup streams
 
+    // DMA cursor: local item `di`, its k-tile `dkt`, and the byte addresses of
+    // that k-tile's first A / B elements (wave-uniform, advanced per k-tile)
+    unsigned aoffs[4], boffs[4];
+    pk_offsets<AK>(aoffs, (int)lda, wave, lane);
+    pk_offsets<BKM>(boffs, (int)ldb, wave, lane);
+    const int64_t astep = AK ? 2 * kPkBK : 2 * kPkBK * lda, bstep = BKM ? 2 * kPkBK : 2 * kPkBK * ldb;
+    const unsigned lds0 = lds_addr(smem_raw) + wave * 1024;
+    int di = 0, dkt = 0;
+    const char* pa = reinterpret_cast<const char*>(A);
+    const char* pb = reinterpret_cast<const char*>(B);
     auto issue = [&](int g) {
-        const int i = g / nk, kt = g - i * nk;
-        int64_t z, tm, tn;
-        pk_item(i * grid + b, items, tiles_n, tiles_mn, z, tm, tn);
-        unsigned char* st = smem_raw + (g & 1) * kPkStage;
-        const int64_t k0 = z * kps + (int64_t)kt * kPkBK;
-        pk_dma<AK>(st, A, lda, tm * 256, k0, wave, lane);
-        pk_dma<BKM>(st + OPB, B, ldb, tn * 256, k0, wave, lane);
+        if (dkt == 0) {
+            int z, tm, tn;
+            pk_item(di * grid + b, items, tiles_n, tiles_mn, z, tm, tn);
+            const int64_t k0 = (int64_t)z * kps;
+            pa = reinterpret_cast<const char*>(A) + 2 * (AK ? (int64_t)tm * 256 * lda + k0 : k0 * lda + tm * 256);
+            pb = reinterpret_cast<const char*>(B) + 2 * (BKM ? (int64_t)tn * 256 * ldb + k0 : k0 * ldb + tn * 256);
+        }
+        const unsigned st = lds0 + (g & 1) * kPkStage;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dma16s(pa, aoffs[j], st + j * 8192);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dma16s(pb, boffs[j], st + OPB + j * 8192);
+        pa += astep;
+        pb += bstep;
+        if (++dkt == nk) {
+            dkt = 0;
+            ++di;
+        }
     };
 
     // K-major fragment byte offsets per k-step (row swizzle depends on the lane only)
@@ -560,6 +582,9 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
 
     if (G > 0) issue(0);
     float* const strip = reinterpret_cast<float*>(smem_raw + 2 * kPkStage) + wave * 16 * 64;
+    // epilogue lane offsets: lane (lane/16, lane%16) owns row t*4 + lane/16, columns 4*(lane%16)..+3
+    const int lrow = lane >> 4, lcol = (lane & 15) * 4;
+    int ckt = 0, ci = 0;  // compute cursor: k-tile within the current item, local item
 
     for (int g = 0; g < G; ++g) {
         // vmcnt(0): this wave's DMA of k-tile g (and anything older) has
@@ -570,9 +595,7 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
         if (g + 1 < G) issue(g + 1);
         const unsigned char* sa = smem_raw + (g & 1) * kPkStage;
         const unsigned char* sb = sa + OPB;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            bf16x8 fa[4], fb[2];
+        auto frags = [&](int ks, bf16x8 (&fa)[4], bf16x8 (&fb)[2]) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 if constexpr (AK) fa[i] = *reinterpret_cast<const bf16x8*>(sa + aoff[ks] + i * 4096);
@@ -583,30 +606,41 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
                 if constexpr (BKM) fb[j] = *reinterpret_cast<const bf16x8*>(sb + boff[ks] + j * 4096);
                 else fb[j] = tr_frag<256>(reinterpret_cast<const bf16*>(sb), wn * 64 + j * 32, ks, lane);
             }
+        };
+        bf16x8 fa[2][4], fb[2][2];
+        frags(0, fa[0], fb[0]);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            if (ks < 3) frags(ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks & 1][i], fb[ks & 1][j], acc[i][j], 0, 0, 0);
         }
-        const int it = g / nk;
-        if (g - it * nk != nk - 1) continue;
+        if (++ckt != nk) continue;
+        ckt = 0;
+        const int it = ci++;
 
         // Epilogue of item `it`: per 32-row MFMA block i, two 16-row half
         // strips; lane (t, lane/16, lane%16) owns 4 consecutive columns.
-        int64_t z, tm, tn;
+        int z, tm, tn;
         pk_item(it * grid + b, items, tiles_n, tiles_mn, z, tm, tn);
-        const int64_t row0 = tm * 256 + wm * 128, col0 = tn * 256 + wn * 64;
+        const int64_t row0 = (int64_t)tm * 256 + wm * 128, col0 = (int64_t)tn * 256 + wn * 64;
+        // this wave's 128 x 64 block: element (r, c) at base + r * ld + c
+        const int64_t cbase = row0 * ldc + col0;
+        const int clo = lrow * (int)ldc + lcol;
         constexpr bool PRE = EPI == EPI_ACCUM || EPI == EPI_ADD || EPI == EPI_RELU2_BWD;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
+                const int64_t rb = cbase + (int64_t)(i * 32 + h * 16) * ldc;
                 float4 pre[PRE ? 4 : 1];
                 if constexpr (PRE) {
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
-                        const int64_t o = (row0 + i * 32 + h * 16 + t * 4 + (lane >> 4)) * ldc + col0 + (lane & 15) * 4;
+                        const int64_t o = rb + (int64_t)(t * 4) * ldc + clo;
                         if constexpr (EPI == EPI_ACCUM) pre[t] = ld4(C + o);
                         else if constexpr (EPI == EPI_ADD) pre[t] = ld4(static_cast<const float*>(aux) + o);
                         else pre[t] = ld4(static_cast<const TC*>(aux) + o);
@@ -625,12 +659,12 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    const int r = t * 4 + (lane >> 4), c4 = (lane & 15) * 4;
-                    const float4 x = *reinterpret_cast<const float4*>(strip + r * 64 + (c4 ^ (((r >> 2) & 1) << 5)));
-                    const int64_t row = row0 + i * 32 + h * 16 + r, col = col0 + c4;
-                    const int64_t o = row * ldc + col;
+                    const int r = t * 4 + lrow;
+                    const float4 x = *reinterpret_cast<const float4*>(strip + r * 64 + (lcol ^ (((r >> 2) & 1) << 5)));
+                    const int64_t o = rb + (int64_t)(t * 4) * ldc + clo;
                     if constexpr (EPI == EPI_PARTIAL) {
-                        *reinterpret_cast<float4*>(partial + (z * M + row) * N + col) = x;
+                        const int64_t row = row0 + i * 32 + h * 16 + r;
+                        *reinterpret_cast<float4*>(partial + ((int64_t)z * M + row) * N + col0 + lcol) = x;
                     } else if constexpr (EPI == EPI_STORE) {
                         st4(C + o, x);
                     } else if constexpr (EPI == EPI_ACCUM || EPI == EPI_ADD) {
@@ -772,7 +806,9 @@ static bool pk_shape(int64_t gm, int64_t gn, int64_t gk) {
 }
 static bool pk_ok(int64_t gm, int64_t gn, int64_t gk, int64_t lda, int64_t ldb, int64_t ldc, const void* A,
                   const void* B, const void* C) {
-    return pk_shape(gm, gn, gk) && lda % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 &&
+    // per-lane DMA / epilogue offsets and item indices are 32-bit
+    const bool fits = lda < (1 << 22) && ldb < (1 << 22) && ldc < (1 << 22) && (gm / 256) * (gn / 256) * gk / kPkBK < (1ll << 30);
+    return fits && pk_shape(gm, gn, gk) && lda % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 &&
            ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C)) & 15) == 0;
 }
 // Reduction splits: powers of two (each split a whole number of k-tiles and
