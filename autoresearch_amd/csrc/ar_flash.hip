@@ -239,8 +239,10 @@ __device__ __forceinline__ RowOut at_head(RowOut o, int b, int h, int T, int HD)
 }
 
 // visibility of key kp from query qp
+// (bitwise, not short-circuit: per-element masks compile to compares and
+// selects, not to exec-mask branches)
 __device__ __forceinline__ bool visible(int kp, int qp, int T, int window) {
-    return kp <= qp && qp < T && (window <= 0 || kp >= qp - window);
+    return (kp <= qp) & (qp < T) & ((window <= 0) | (kp >= qp - window));
 }
 
 // ============================ forward ============================
@@ -298,12 +300,21 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
             const bool full = kv0 + kTile - 1 <= qw && qw + 31 < T && (window <= 0 || kv0 >= qw + 31 - window);
             f32x16 s[2];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
+            // the two 32-key halves as independent MFMA chains, interleaved
 #pragma unroll
-                for (int ks = 0; ks < G::KSTEPS; ++ks)
+            for (int ks = 0; ks < G::KSTEPS; ++ks)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
                     s[kb] = mma(rowfrag<HD>(sK, kb * 32 + (lane & 31), ks, lane), qf[ks], s[kb]);
+            if (!full) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        s[kb][e] = visible(kv0 + kb * 32 + acc_row(e, lane), my_q, T, window) ? s[kb][e] : -INFINITY;
             }
             // running max in log2 units: max of the raw scores, scaled once
             // (the scale is positive), and p = 2^(s scale - m) as one fma
@@ -311,10 +322,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    if (!full && !visible(kv0 + kb * 32 + acc_row(e, lane), my_q, T, window)) s[kb][e] = -INFINITY;
-                    mt = fmaxf(mt, s[kb][e]);
-                }
+                for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[kb][e]);
             mt = fmaxf(mt, __shfl_xor(mt, 32, kWave)) * scale_log2;
             const float m_new = fmaxf(m, mt);
             const float m_use = m_new == -INFINITY ? 0.f : m_new;
@@ -449,7 +457,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
                 }
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const bool ok = full || visible(kv0 + kb * 32 + acc_row(e, lane), my_q, T, window);
+                    const bool ok = full | visible(kv0 + kb * 32 + acc_row(e, lane), my_q, T, window);
                     const float p = ok ? exp2_fast(s[e] * scale_log2 - my_lse2) : 0.f;
                     s[e] = p * (dp[e] - my_D);
                 }
@@ -577,7 +585,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int e = 4 * a + j;
-                    const bool ok = full || (my_k < T && visible(my_k, qt0 + q4 + j, T, window));
+                    const bool ok = full | ((my_k < T) & visible(my_k, qt0 + q4 + j, T, window));
                     const float pv = ok ? exp2_fast(fmaf(s[e], scale_log2, -lvv[j])) : 0.f;
                     s[e] = pv;
                     dp[e] = pv * (dp[e] - dv4[j]);
