@@ -115,18 +115,49 @@ __device__ __forceinline__ bf16x8 accfrag(const f32x16& a, int s) {
 // (id % NCH) ^ swz(row) of row id / NCH; a wave's 64 slots are one 1 KB
 // global_load_lds).  Rows past T repeat row T - 1: callers mask every score
 // of such a row to probability 0.
-// The thread index is made opaque per call, so the per-slot address math is
-// redone at each tile (a few VALU ops) rather than hoisted out of the tile
-// loop into registers that would spill.
-template <int HD, int ROWS = kTile>
-__device__ __forceinline__ void dma_tile(bf16* dst, const bf16* base, int64_t rs, int row0, int T) {
+template <int HD, int ROWS>
+struct TileU {  // 16-byte chunks per thread of a ROWS-row tile
+    static constexpr int N = (ROWS * Geo<HD>::NCH + kThreads - 1) / kThreads;
+};
+
+// This thread's chunk byte offsets from a tile's first row (row stride rs
+// elements), fixed for the kernel: a whole tile's DMA is then a wave-uniform
+// base address plus these offsets (no per-copy address arithmetic).
+template <int HD, int ROWS = kTile, int N>
+__device__ __forceinline__ void tile_offsets(unsigned (&off)[N], int64_t rs) {
     using G = Geo<HD>;
-    constexpr int UNITS = ROWS * G::NCH;  // a multiple of 64: the guard below is wave-uniform
+    static_assert(N == TileU<HD, ROWS>::N, "offset count");
+#pragma unroll
+    for (int i = 0; i < TileU<HD, ROWS>::N; ++i) {
+        const int id = i * kThreads + threadIdx.x;
+        const int r = id / G::NCH, c = (id % G::NCH) ^ G::swz(r);
+        off[i] = (unsigned)(r * (int)rs + c * 8) * 2u;
+    }
+}
+
+template <int HD, int ROWS = kTile, int N>
+__device__ __forceinline__ void dma_tile(bf16* dst, const bf16* base, int64_t rs, int row0, int T,
+                                         const unsigned (&off)[N]) {
+    using G = Geo<HD>;
+    static_assert(N == TileU<HD, ROWS>::N, "offset count");
+    constexpr int UNITS = ROWS * G::NCH;  // a multiple of 64: the guards below are wave-uniform
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    if (row0 + ROWS <= T) {
+        const bf16* tb = base + (int64_t)row0 * rs;
+#pragma unroll
+        for (int i = 0; i < TileU<HD, ROWS>::N; ++i) {
+            if (UNITS % kThreads != 0 && i * kThreads + wave * kWave >= UNITS) break;
+            dma16s(tb, off[i], lds_addr(dst + (i * kThreads + wave * kWave) * 8));
+        }
+        return;
+    }
+    // the sequence's last, partial tile: rows clamped per chunk.  The thread
+    // index is made opaque so that this rarely taken path's address math is
+    // not hoisted into registers for the whole kernel.
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
-    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
 #pragma unroll
-    for (int i = 0; i < (UNITS + kThreads - 1) / kThreads; ++i) {
+    for (int i = 0; i < TileU<HD, ROWS>::N; ++i) {
         const int id = i * kThreads + tid;
         if (UNITS % kThreads != 0 && i * kThreads + wave * kWave >= UNITS) break;
         const int r = id / G::NCH, c = (id % G::NCH) ^ G::swz(r);
@@ -278,9 +309,11 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
     const int kend = (q0 + kOwn < T) ? q0 + kOwn : T;
     const int ntiles = kend > kstart ? (kend - kstart + kTile - 1) / kTile : 0;
 
+    unsigned toff[TileU<HD, kTile>::N];
+    tile_offsets<HD>(toff, rs);
     if (ntiles > 0) {
-        dma_tile<HD>(lds, k + boff, rs, kstart, T);
-        dma_tile<HD>(lds + G::TILE, v + boff, rs, kstart, T);
+        dma_tile<HD>(lds, k + boff, rs, kstart, T, toff);
+        dma_tile<HD>(lds + G::TILE, v + boff, rs, kstart, T, toff);
     }
     wait_vmem();
     __syncthreads();
@@ -289,8 +322,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
         const int cur = it & 1;
         const bool more = it + 1 < ntiles;
         if (more) {
-            dma_tile<HD>(lds + (2 * (cur ^ 1)) * G::TILE, k + boff, rs, kv0 + kTile, T);
-            dma_tile<HD>(lds + (2 * (cur ^ 1) + 1) * G::TILE, v + boff, rs, kv0 + kTile, T);
+            dma_tile<HD>(lds + (2 * (cur ^ 1)) * G::TILE, k + boff, rs, kv0 + kTile, T, toff);
+            dma_tile<HD>(lds + (2 * (cur ^ 1) + 1) * G::TILE, v + boff, rs, kv0 + kTile, T, toff);
         }
         const bf16* sK = lds + (2 * cur) * G::TILE;
         const bf16* sV = lds + (2 * cur + 1) * G::TILE;
@@ -424,9 +457,11 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
     const int kend = (q0 + kOwn < T) ? q0 + kOwn : T;
     const int ntiles = kend > kstart ? (kend - kstart + kTile - 1) / kTile : 0;
 
+    unsigned toff[TileU<HD, kTile>::N];
+    tile_offsets<HD>(toff, rs);
     if (ntiles > 0) {
-        dma_tile<HD>(lds, k + boff, rs, kstart, T);
-        dma_tile<HD>(lds + G::TILE, v + boff, rs, kstart, T);
+        dma_tile<HD>(lds, k + boff, rs, kstart, T, toff);
+        dma_tile<HD>(lds + G::TILE, v + boff, rs, kstart, T, toff);
     }
     wait_vmem();
     __syncthreads();
@@ -435,8 +470,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
         const int cur = it & 1;
         const bool more = it + 1 < ntiles;
         if (more) {
-            dma_tile<HD>(lds + (2 * (cur ^ 1)) * G::TILE, k + boff, rs, kv0 + kTile, T);
-            dma_tile<HD>(lds + (2 * (cur ^ 1) + 1) * G::TILE, v + boff, rs, kv0 + kTile, T);
+            dma_tile<HD>(lds + (2 * (cur ^ 1)) * G::TILE, k + boff, rs, kv0 + kTile, T, toff);
+            dma_tile<HD>(lds + (2 * (cur ^ 1) + 1) * G::TILE, v + boff, rs, kv0 + kTile, T, toff);
         }
         const bf16* sK = lds + (2 * cur) * G::TILE;
         const bf16* sV = lds + (2 * cur + 1) * G::TILE;
@@ -540,10 +575,16 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
             dma4(lane < KT ? lse + i : dbuf + i, lds_addr(sLD + stage * 2 * KT));
         }
     };
-    dma_tile<HD, kOwn>(sV, v + boff, rs, k0, T);
+    {
+        unsigned voff[TileU<HD, kOwn>::N];
+        tile_offsets<HD, kOwn>(voff, rs);
+        dma_tile<HD, kOwn>(sV, v + boff, rs, k0, T, voff);
+    }
+    unsigned toff[TileU<HD, KT>::N];
+    tile_offsets<HD, KT>(toff, rs);
     if (ntiles > 0) {
-        dma_tile<HD, KT>(lds, q + boff, rs, qstart, T);
-        dma_tile<HD, KT>(lds + TT, dout + boff, rs, qstart, T);
+        dma_tile<HD, KT>(lds, q + boff, rs, qstart, T, toff);
+        dma_tile<HD, KT>(lds + TT, dout + boff, rs, qstart, T, toff);
         dma_ld(qstart, 0);
     }
     wait_vmem();
@@ -553,8 +594,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
         const int cur = it & 1;
         const bool more = it + 1 < ntiles;
         if (more) {
-            dma_tile<HD, KT>(lds + (2 * (cur ^ 1)) * TT, q + boff, rs, qt0 + KT, T);
-            dma_tile<HD, KT>(lds + (2 * (cur ^ 1) + 1) * TT, dout + boff, rs, qt0 + KT, T);
+            dma_tile<HD, KT>(lds + (2 * (cur ^ 1)) * TT, q + boff, rs, qt0 + KT, T, toff);
+            dma_tile<HD, KT>(lds + (2 * (cur ^ 1) + 1) * TT, dout + boff, rs, qt0 + KT, T, toff);
             dma_ld(qt0 + KT, cur ^ 1);
         }
         const bf16* sQ = lds + (2 * cur) * TT;
