@@ -309,91 +309,152 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
     const int kend = (q0 + kOwn < T) ? q0 + kOwn : T;
     const int ntiles = kend > kstart ? (kend - kstart + kTile - 1) / kTile : 0;
 
+    // Software pipeline: K runs one tile ahead of V, so iteration `it` holds
+    // K(it + 1) and V(it) and issues the score MFMAs of tile it + 1 in the
+    // same basic block as tile it's softmax (VALU), which the scheduler
+    // interleaves.  Buffers: K(t) in stage t & 1 slot 0, V(t) in stage t & 1
+    // slot 1; iteration it refills K(it + 2) and V(it + 1), whose previous
+    // contents were last read in iteration it - 1.
+    auto kbuf = [&](int t) { return lds + (2 * (t & 1)) * G::TILE; };
+    auto vbuf = [&](int t) { return lds + (2 * (t & 1) + 1) * G::TILE; };
+    // a tile is active for this wave unless the causal / window mask removes all of it
+    auto active = [&](int t) {
+        const int kv0 = kstart + t * kTile;
+        return !(kv0 > qw + 31 || (window > 0 && kv0 + kTile - 1 < qw - window) || qw >= T);
+    };
+    auto scores = [&](const bf16* sK, f32x16 (&sc)[2]) {
+        const int ln = opaque_lane(threadIdx.x % kWave);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sc[kb][e] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < G::KSTEPS; ++ks)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) sc[kb] = mma(rowfrag<HD>(sK, kb * 32 + (ln & 31), ks, ln), qf[ks], sc[kb]);
+    };
+    auto mask = [&](f32x16 (&sc)[2], int kv0) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                sc[kb][e] = visible(kv0 + kb * 32 + acc_row(e, lane), my_q, T, window) ? sc[kb][e] : -INFINITY;
+    };
+    auto is_full = [&](int kv0) {
+        return kv0 + kTile - 1 <= qw && qw + 31 < T && (window <= 0 || kv0 >= qw + 31 - window);
+    };
+    // softmax of tile scores sc (in place: p) with the running max / sum
+    // update, in three parts: the new reference max (m_use; m itself is
+    // moved by softmax_sum), the exponentials, the sum update
+    auto softmax_max = [&](const f32x16 (&sc)[2]) {
+        float mt = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) mt = fmaxf(mt, sc[kb][e]);
+        mt = fmaxf(mt, __shfl_xor(mt, 32, kWave)) * scale_log2;
+        const float m_new = fmaxf(m, mt);
+        return m_new == -INFINITY ? 0.f : m_new;
+    };
+    auto softmax_sum = [&](float rsum, float alpha, float m_use) {
+        rsum += __shfl_xor(rsum, 32, kWave);
+        l = l * alpha + rsum;
+        // m_use is 0 only while every score seen so far is masked (l = 0)
+        m = l > 0.f ? m_use : -INFINITY;
+    };
+    auto softmax = [&](f32x16 (&sc)[2]) {
+        const float m_use = softmax_max(sc);
+        const float alpha = exp2_fast(m - m_use);
+        float rsum = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float pp = exp2_fast(fmaf(sc[kb][e], scale_log2, -m_use));
+                sc[kb][e] = pp;
+                rsum += pp;
+            }
+        softmax_sum(rsum, alpha, m_use);
+        return alpha;
+    };
+    auto pv = [&](const f32x16 (&sc)[2], const bf16* sV, float alpha) {
+        // skip the rescale (a multiply by 1) when the max moved for no row of the wave
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+            for (int dt = 0; dt < G::DT; ++dt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+        }
+        // O^T += V^T P^T, P rounded to bf16 once (l keeps the fp32 sums)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const bf16x8 ph = accfrag(sc[kb], st);
+#pragma unroll
+                for (int dt = 0; dt < G::DT; ++dt) o[dt] = mma(trfrag<HD>(sV, kb, st, dt, lane), ph, o[dt]);
+            }
+    };
+
     unsigned toff[TileU<HD, kTile>::N];
     tile_offsets<HD>(toff, rs);
     if (ntiles > 0) {
-        dma_tile<HD>(lds, k + boff, rs, kstart, T, toff);
-        dma_tile<HD>(lds + G::TILE, v + boff, rs, kstart, T, toff);
+        dma_tile<HD>(kbuf(0), k + boff, rs, kstart, T, toff);
+        dma_tile<HD>(vbuf(0), v + boff, rs, kstart, T, toff);
+        if (ntiles > 1) dma_tile<HD>(kbuf(1), k + boff, rs, kstart + kTile, T, toff);
     }
     wait_vmem();
     __syncthreads();
-    for (int it = 0; it < ntiles; ++it) {
+    f32x16 sa[2], sb[2];  // scores of the current / next tile (the loop body runs twice per trip, roles swapped)
+    if (ntiles > 0 && active(0)) scores(kbuf(0), sa);
+    __syncthreads();  // every wave is done with K(0) before step 0 refills its buffer with K(2)
+    auto step = [&](int it, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
         const int kv0 = kstart + it * kTile;
-        const int cur = it & 1;
-        const bool more = it + 1 < ntiles;
-        if (more) {
-            dma_tile<HD>(lds + (2 * (cur ^ 1)) * G::TILE, k + boff, rs, kv0 + kTile, T, toff);
-            dma_tile<HD>(lds + (2 * (cur ^ 1) + 1) * G::TILE, v + boff, rs, kv0 + kTile, T, toff);
-        }
-        const bf16* sK = lds + (2 * cur) * G::TILE;
-        const bf16* sV = lds + (2 * cur + 1) * G::TILE;
-        const bool skip = kv0 > qw + 31 || (window > 0 && kv0 + kTile - 1 < qw - window) || qw >= T;
-        if (!skip) {
-            // every (key, query) of the tile visible: no per-element mask
-            const bool full = kv0 + kTile - 1 <= qw && qw + 31 < T && (window <= 0 || kv0 >= qw + 31 - window);
-            f32x16 s[2];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
-            // the two 32-key halves as independent MFMA chains, interleaved
-#pragma unroll
-            for (int ks = 0; ks < G::KSTEPS; ++ks)
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-                    s[kb] = mma(rowfrag<HD>(sK, kb * 32 + (lane & 31), ks, lane), qf[ks], s[kb]);
-            if (!full) {
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e)
-                        s[kb][e] = visible(kv0 + kb * 32 + acc_row(e, lane), my_q, T, window) ? s[kb][e] : -INFINITY;
-            }
-            // running max in log2 units: max of the raw scores, scaled once
-            // (the scale is positive), and p = 2^(s scale - m) as one fma
-            float mt = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[kb][e]);
-            mt = fmaxf(mt, __shfl_xor(mt, 32, kWave)) * scale_log2;
-            const float m_new = fmaxf(m, mt);
-            const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        if (it + 2 < ntiles) dma_tile<HD>(kbuf(it + 2), k + boff, rs, kv0 + 2 * kTile, T, toff);
+        if (it + 1 < ntiles) dma_tile<HD>(vbuf(it + 1), v + boff, rs, kv0 + kTile, T, toff);
+        const bool a_cur = active(it), a_nxt = it + 1 < ntiles && active(it + 1);
+        if (a_cur && !is_full(kv0)) mask(cur, kv0);
+        if (a_cur && a_nxt) {
+            // the next tile's score MFMAs interleaved in program order with
+            // this tile's softmax (exponentials two elements per MFMA)
+            const float m_use = softmax_max(cur);
             const float alpha = exp2_fast(m - m_use);
+            const bf16* sK = kbuf(it + 1);
+            const int ln = opaque_lane(threadIdx.x % kWave);
             float rsum = 0.f;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const float p = exp2_fast(fmaf(s[kb][e], scale_log2, -m_use));
-                    s[kb][e] = p;
-                    rsum += p;
+                for (int e = 0; e < 16; ++e) nxt[kb][e] = 0.f;
+            constexpr int EPM = 16 / G::KSTEPS;  // exponentials per MFMA: 32 per lane over 2 KSTEPS MFMAs
+#pragma unroll
+            for (int ks = 0; ks < G::KSTEPS; ++ks)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    nxt[kb] = mma(rowfrag<HD>(sK, kb * 32 + (ln & 31), ks, ln), qf[ks], nxt[kb]);
+#pragma unroll
+                    for (int j = 0; j < EPM; ++j) {
+                        const int flat = (ks * 2 + kb) * EPM + j, ckb = flat >> 4, ce = flat & 15;
+                        const float pp = exp2_fast(fmaf(cur[ckb][ce], scale_log2, -m_use));
+                        cur[ckb][ce] = pp;
+                        rsum += pp;
+                    }
                 }
-            rsum += __shfl_xor(rsum, 32, kWave);
-            l = l * alpha + rsum;
-            m = m_new;
-            // the running max moves on a few tiles only: skip the rescale
-            // (a multiply by 1) when it moved for no row of the wave
-            if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
-#pragma unroll
-                for (int dt = 0; dt < G::DT; ++dt)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
-            }
-            // O^T += V^T P^T, P rounded to bf16 once (the normaliser l keeps
-            // the fp32 row sums).
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int st = 0; st < 2; ++st) {
-                    const bf16x8 ph = accfrag(s[kb], st);
-#pragma unroll
-                    for (int dt = 0; dt < G::DT; ++dt) o[dt] = mma(trfrag<HD>(sV, kb, st, dt, lane), ph, o[dt]);
-                }
+            softmax_sum(rsum, alpha, m_use);
+            pv(cur, vbuf(it), alpha);
+        } else {
+            if (a_nxt) scores(kbuf(it + 1), nxt);
+            if (a_cur) pv(cur, vbuf(it), softmax(cur));
         }
-        wait_vmem();  // this thread's part of the next K / V tile has landed
+        wait_vmem();  // this thread's part of K(it + 2) / V(it + 1) has landed
         __syncthreads();
+    };
+    int it = 0;
+    for (; it + 1 < ntiles; it += 2) {
+        step(it, sa, sb);
+        step(it + 1, sb, sa);
     }
+    if (it < ntiles) step(it, sa, sb);
     const float inv_l = l > 0.f ? 1.0f / l : 0.f;
     if (lane < 32 && my_q < T) lse[((int64_t)b * T + my_q) * H + h] = l > 0.f ? (m + log2f(l)) * kLn2 : -INFINITY;
     float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 68;
@@ -409,7 +470,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
     using G = Geo<HD>;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     bf16* const lds = reinterpret_cast<bf16*>(smem_raw);  // stage s: K at 2 s TILE, V at (2 s + 1) TILE
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int nqb = (T + kOwn - 1) / kOwn;
     int bh, qb;
     block_coords(nqb, B * H, true, bh, qb);
@@ -542,7 +603,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
     bf16* const lds = reinterpret_cast<bf16*>(smem_raw);  // stage s: Q at 2 s TT, dO at (2 s + 1) TT
     bf16* const sV = lds + 4 * TT;                        // the workgroup's own 128 V rows
     float* const sLD = reinterpret_cast<float*>(sV + kOwn * HD);
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int nkb = (T + kOwn - 1) / kOwn;
     int bh, kblk;
     block_coords(nkb, B * H, false, bh, kblk);
