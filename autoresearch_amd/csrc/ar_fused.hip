@@ -342,11 +342,12 @@ __global__ __launch_bounds__(kBlock) void ve_bwd_k(VeBwdArgs a) {
 //   MODE 1: gx = gx + rmsnorm_bwd(gn, x, rms)                 (MLP norm)
 //   MODE 2: g = gx + rmsnorm_bwd(gn, x, rms); dots g.x, g.x0 into this
 //           wave's partial; gx = res[layer] * g               (attention norm)
-// and gxb = bf16(gx).  MODE 2 runs on a fixed grid of kNormBwdWaves waves.
+// and gxb = bf16(gx).  GB: gn is read from its bf16 copy gnb.  MODE 2 runs on a fixed grid of kNormBwdWaves waves.
 struct NormBwdArgs {
     float* gx;
     bf16* gxb;
     const float* gn;
+    const bf16* gnb;  // gn stored as bf16 (GB instantiations)
     const float* x;
     const float* rms;
     const float* x0;
@@ -355,7 +356,7 @@ struct NormBwdArgs {
     int64_t layer, rows, C;
 };
 
-template <int NC, int MODE>
+template <int NC, int MODE, bool GB>
 __global__ __launch_bounds__(kBlock) void norm_bwd_k(NormBwdArgs a) {
     const int lane = threadIdx.x % kWave;
     const int64_t C4 = a.C / 4;
@@ -363,13 +364,15 @@ __global__ __launch_bounds__(kBlock) void norm_bwd_k(NormBwdArgs a) {
     float p1 = 0.f, p2 = 0.f;
     for (int64_t r = wave_id(); r < a.rows; r += wave_count()) {
         const float4* g4 = reinterpret_cast<const float4*>((MODE == 0 ? a.gx : a.gn) + r * a.C);
+        const bf16* gb = a.gnb + r * a.C;
         const float4* x4 = reinterpret_cast<const float4*>(a.x + r * a.C);
         float4 g[NC], x[NC];
         float dot = 0.f;
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
             const int64_t i = lane + 64 * j;
-            g[j] = i < C4 ? g4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (GB) g[j] = i < C4 ? ld_bf16x4(gb + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            else g[j] = i < C4 ? g4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
             x[j] = i < C4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
             dot += dot4(g[j], x[j]);
         }
@@ -547,16 +550,21 @@ int32_t ve_bwd(hipStream_t st, float* gve, float* ggate, const bf16* gv, int64_t
 
 int32_t norm_bwd(hipStream_t st, int mode, float* gx, bf16* gxb, const float* gn, const float* x, const float* rms,
                  const float* x0, const float* res, int64_t layer, float* g_res, float* g_x0, float* partial,
-                 int64_t rows, int64_t C) {
+                 int64_t rows, int64_t C, const bf16* gnb) {
     if (C % 4 != 0 || C > 256 * 16) return set_error(AR_EUNSUPPORTED, "norm_bwd: n_embd %lld", (long long)C);
-    NormBwdArgs a{gx, gxb, gn, x, rms, x0, res, partial, layer, rows, C};
+    if (mode != 0 && (gn != nullptr) == (gnb != nullptr))
+        return set_error(AR_EINVAL, "norm_bwd: give the normed-input gradient once, fp32 or bf16");
+    NormBwdArgs a{gx, gxb, gn, gnb, x, rms, x0, res, partial, layer, rows, C};
     const int nc = (int)cdiv(C, 256);
     const unsigned grid = mode == 2 ? (unsigned)(kNormBwdWaves / (kBlock / kWave)) : wave_blocks(rows);
+    const bool gb = mode != 0 && gnb != nullptr;
 #define AR_NB(NC)                                                                            \
     do {                                                                                     \
-        if (mode == 0) norm_bwd_k<NC, 0><<<grid, kBlock, 0, st>>>(a);                        \
-        else if (mode == 1) norm_bwd_k<NC, 1><<<grid, kBlock, 0, st>>>(a);                   \
-        else norm_bwd_k<NC, 2><<<grid, kBlock, 0, st>>>(a);                                  \
+        if (mode == 0) norm_bwd_k<NC, 0, false><<<grid, kBlock, 0, st>>>(a);                 \
+        else if (mode == 1 && gb) norm_bwd_k<NC, 1, true><<<grid, kBlock, 0, st>>>(a);       \
+        else if (mode == 1) norm_bwd_k<NC, 1, false><<<grid, kBlock, 0, st>>>(a);            \
+        else if (gb) norm_bwd_k<NC, 2, true><<<grid, kBlock, 0, st>>>(a);                    \
+        else norm_bwd_k<NC, 2, false><<<grid, kBlock, 0, st>>>(a);                           \
     } while (0)
     if (nc <= 1) AR_NB(1);
     else if (nc <= 2) AR_NB(2);

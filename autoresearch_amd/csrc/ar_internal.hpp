@@ -111,11 +111,12 @@ int32_t ve_bwd(hipStream_t st, float* gve, float* ggate, const bf16* gv, int64_t
                const float* table, const int64_t* idx, int64_t nt, int64_t C, int64_t H, int64_t hd);
 // mode 0: gx = rmsnorm_bwd(gx); 1: gx += rmsnorm_bwd(gn); 2: g = gx +
 // rmsnorm_bwd(gn), g_res[l] += g.x, g_x0[l] += g.x0, gx = res[l] g.  gxb = bf16(gx).
+// Modes 1 and 2 take gn either fp32 (gn) or bf16 (gnb), not both.
 // partial: 2 * kNormBwdWaves floats (mode 2).
 constexpr int kNormBwdWaves = 4096;
 int32_t norm_bwd(hipStream_t st, int mode, float* gx, bf16* gxb, const float* gn, const float* x, const float* rms,
                  const float* x0, const float* res, int64_t layer, float* g_res, float* g_x0, float* partial,
-                 int64_t rows, int64_t C);
+                 int64_t rows, int64_t C, const bf16* gnb = nullptr);
 int32_t to_bf16(hipStream_t st, bf16* out, const float* in, int64_t n);
 // One matrix of a batched transpose: fp32 [rows, cols] at in + src becomes
 // bf16 [cols, rows] at out + dst; tile0 = 64 x 64 tiles of the entries before.

@@ -84,8 +84,8 @@ struct ar_gpt {
     int64_t wbt_tiles = 0;
     std::vector<LayerBufsB> LB;
     ar::bf16* qkv = nullptr;  // [BT, 3C] q | k | v GEMM output
-    ar::bf16 *x_final_b = nullptr, *grad_logits_b = nullptr, *grad_xb = nullptr, *grad_h = nullptr,
-         *grad_attn_out_b = nullptr, *grad_qkv = nullptr;
+    ar::bf16 *x_final_b = nullptr, *grad_logits_b = nullptr, *grad_xb = nullptr, *grad_x_norm_b = nullptr,
+             *grad_h = nullptr, *grad_attn_out_b = nullptr, *grad_qkv = nullptr;
     float grad_logits_scale = 0.f;  // loss_scale baked into grad_logits_b
     bool grad_logits_valid = false;
     // step-dependent optimizer scalars in device memory (StepScalars)
@@ -354,6 +354,7 @@ static int32_t gpt_build(ar_gpt* m) {
         AR_TRY(balloc(&m->x_final_b, BT * C));
         AR_TRY(balloc(&m->grad_logits_b, BT * V));
         AR_TRY(balloc(&m->grad_xb, BT * C));
+        AR_TRY(balloc(&m->grad_x_norm_b, BT * C));
         AR_TRY(balloc(&m->grad_h, BT * F));
         AR_TRY(balloc(&m->grad_attn_out_b, BT * C));
         AR_TRY(balloc(&m->grad_qkv, BT * 3 * C));
@@ -578,10 +579,11 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
         AR_TRY(gemm_e(m, 1, 0, GEMM_EPI_RELU2_BWD, m->grad_h, true, m->grad_xb, true, WbT(m, m->i_mlpp[i]), BT, F, C,
                       b.act, nullptr, 0.f));
         AR_TRY(gemm_b(m, 2, 2, G(m, m->i_mlpp[i]), false, m->grad_xb, true, b.act, true, BT, C, F, true));
-        AR_TRY(gemm_b(m, 1, 0, m->grad_x_norm, false, m->grad_h, true, WbT(m, m->i_fc[i]), true, BT, C, F, false));
+        // gradient of the normed MLP input in bf16 (as a bf16 linear's input gradient)
+        AR_TRY(gemm_b(m, 1, 0, m->grad_x_norm_b, true, m->grad_h, true, WbT(m, m->i_fc[i]), true, BT, C, F, false));
         AR_TRY(gemm_b(m, 2, 2, G(m, m->i_fc[i]), false, m->grad_h, true, b.xn_mlp, true, BT, F, C, true));
-        AR_TRY(norm_bwd(st, 1, m->grad_x, m->grad_xb, m->grad_x_norm, b.x, b.rms_mlp, nullptr, nullptr, 0, nullptr,
-                        nullptr, nullptr, BT, C));  // Q7: saved x of the layer
+        AR_TRY(norm_bwd(st, 1, m->grad_x, m->grad_xb, nullptr, b.x, b.rms_mlp, nullptr, nullptr, 0, nullptr, nullptr,
+                        nullptr, BT, C, m->grad_x_norm_b));  // Q7: saved x of the layer
         // attention output projection
         AR_TRY(gemm_b(m, 1, 0, m->grad_attn_out_b, true, m->grad_xb, true, WbT(m, m->i_proj[i]), true, BT, C, C,
                       false));
