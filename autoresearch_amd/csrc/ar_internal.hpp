@@ -52,6 +52,9 @@ constexpr int kGateBlocks = 256;
 // stride C, xn row stride ldx.
 int32_t ve_gate_bwd(hipStream_t st, float* gx, float* gw, const float* ggate, const float* gate, const float* xn,
                     const float* w, int64_t nt, int64_t nkv, int64_t gc, int64_t C, int64_t ldx, float* partial);
+// the same, adding into a bf16 gx (read, add in fp32, round)
+int32_t ve_gate_bwd(hipStream_t st, bf16* gx, float* gw, const float* ggate, const float* gate, const float* xn,
+                    const float* w, int64_t nt, int64_t nkv, int64_t gc, int64_t C, int64_t ldx, float* partial);
 constexpr int kGateMaxH = 16;
 
 // ---- attention (ar_attention.hip) ----

@@ -615,15 +615,16 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
         if (ve)
             AR_TRY(ar_embedding_bwd_sorted(AS(m), G(m, m->i_ve[i]), m->grad_ve, m->sorted_ids, m->sorted_tok, BT, kv,
                                            m->scratch));
-        AR_TRY(gemm_b(m, 1, 0, m->grad_x_norm, false, m->grad_qkv, true, WbT(m, m->i_q[i]), true, BT, C, 3 * C,
+        // gradient of the normed attention input in bf16 (as a bf16 linear's input gradient)
+        AR_TRY(gemm_b(m, 1, 0, m->grad_x_norm_b, true, m->grad_qkv, true, WbT(m, m->i_q[i]), true, BT, C, 3 * C,
                       false));
         AR_TRY(gemm_b(m, 2, 2, G(m, m->i_q[i]), false, m->grad_qkv, true, b.xn, true, BT, 3 * C, C, true));
         if (ve)
-            AR_TRY(ve_gate_bwd(st, m->grad_x_norm, G(m, m->i_gate[i]), m->grad_gate, b.gate, b.xg,
+            AR_TRY(ve_gate_bwd(st, m->grad_x_norm_b, G(m, m->i_gate[i]), m->grad_gate, b.gate, b.xg,
                                P(m, m->i_gate[i]), BT, H, kGateChannels, C, kGateChannels, m->scratch));
         // grad_x = res[i] * (grad_x + rmsnorm_bwd(.)), with the Q8 scalar dots (Q9: grad_x0 unused)
-        AR_TRY(norm_bwd(st, 2, m->grad_x, m->grad_xb, m->grad_x_norm, b.x, b.rms_attn, m->x0, P(m, m->i_res), i,
-                        G(m, m->i_res), G(m, m->i_x0), m->scratch, BT, C));
+        AR_TRY(norm_bwd(st, 2, m->grad_x, m->grad_xb, nullptr, b.x, b.rms_attn, m->x0, P(m, m->i_res), i,
+                        G(m, m->i_res), G(m, m->i_x0), m->scratch, BT, C, m->grad_x_norm_b));
     }
     // Q10: embedding norm backward skipped
     return ar_embedding_bwd_sorted(AS(m), G(m, m->i_wte), m->grad_x, m->sorted_ids, m->sorted_tok, BT, C, m->scratch);

@@ -242,8 +242,8 @@ __global__ void ve_apply_bwd_k(float* gve, float* ggate, const float* gv, const 
 // four tokens' loads issued together: gx[t,c] += sum_h dz[t,h] W[h,c] for
 // its tokens (no conflicts), and a per-block partial of
 // gW[h,c] = sum_t dz[t,h] x[t,c], reduced over j in LDS in j order.
-template <int CW>
-__global__ __launch_bounds__(256) void ve_gate_bwd_partial_k(float* gx, float* partial, const float* ggate,
+template <int CW, typename TG>
+__global__ __launch_bounds__(256) void ve_gate_bwd_partial_k(TG* gx, float* partial, const float* ggate,
                                                              const float* gate, const float* xn, const float* w,
                                                              int64_t nt, int64_t nkv, int64_t gc, int64_t C,
                                                              int64_t ldx) {
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(256) void ve_gate_bwd_partial_k(float* gx, float* p
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int64_t tt = t + u * NJ;
-                if (tt < t1) gx[tt * C + c] += ax[u];
+                if (tt < t1) gx[tt * C + c] = (TG)((float)gx[tt * C + c] + ax[u]);
             }
         }
     }
@@ -566,15 +566,27 @@ int32_t frob_normalize(hipStream_t st, float* data, int64_t n, float* scratch) {
     return check_launch("normalize_frobenius");
 }
 
-int32_t ve_gate_bwd(hipStream_t st, float* gx, float* gw, const float* ggate, const float* gate, const float* xn,
-                    const float* w, int64_t nt, int64_t nkv, int64_t gc, int64_t C, int64_t ldx, float* partial) {
+template <typename TG>
+static int32_t ve_gate_bwd_t(hipStream_t st, TG* gx, float* gw, const float* ggate, const float* gate,
+                             const float* xn, const float* w, int64_t nt, int64_t nkv, int64_t gc, int64_t C,
+                             int64_t ldx, float* partial) {
     if (nt == 0) return AR_OK;
     if (gc <= 32)
-        ve_gate_bwd_partial_k<32><<<kGateBlocks, 256, 0, st>>>(gx, partial, ggate, gate, xn, w, nt, nkv, gc, C, ldx);
+        ve_gate_bwd_partial_k<32, TG>
+            <<<kGateBlocks, 256, 0, st>>>(gx, partial, ggate, gate, xn, w, nt, nkv, gc, C, ldx);
     else
-        ve_gate_bwd_partial_k<64><<<kGateBlocks, 256, 0, st>>>(gx, partial, ggate, gate, xn, w, nt, nkv, gc, C, ldx);
+        ve_gate_bwd_partial_k<64, TG>
+            <<<kGateBlocks, 256, 0, st>>>(gx, partial, ggate, gate, xn, w, nt, nkv, gc, C, ldx);
     ve_gate_bwd_finish_k<<<1, 256, 0, st>>>(gw, partial, kGateBlocks, nkv * gc);
     return check_launch("ve_gate_bwd");
+}
+int32_t ve_gate_bwd(hipStream_t st, float* gx, float* gw, const float* ggate, const float* gate, const float* xn,
+                    const float* w, int64_t nt, int64_t nkv, int64_t gc, int64_t C, int64_t ldx, float* partial) {
+    return ve_gate_bwd_t(st, gx, gw, ggate, gate, xn, w, nt, nkv, gc, C, ldx, partial);
+}
+int32_t ve_gate_bwd(hipStream_t st, bf16* gx, float* gw, const float* ggate, const float* gate, const float* xn,
+                    const float* w, int64_t nt, int64_t nkv, int64_t gc, int64_t C, int64_t ldx, float* partial) {
+    return ve_gate_bwd_t(st, gx, gw, ggate, gate, xn, w, nt, nkv, gc, C, ldx, partial);
 }
 }  // namespace ar
 
