@@ -230,13 +230,25 @@ __global__ __launch_bounds__(kBlock) void qkv_post_k(QkvArgs a) {
 // ce_fused: block per token row.  loss = lse - l[target] (0 for an ignored
 // target, < 0 or >= V); grad = (softmax - onehot) * scale as bf16 (0 rows for ignored
 // targets).  NV4 > 0: the row is held in registers (NV4 float4 per thread).
-template <int NV4>
-__global__ __launch_bounds__(kBlock) void ce_fused_k(float* loss, bf16* grad, const float* logits,
+template <typename TL>
+__device__ __forceinline__ float4 ld_logit4(const TL* p);
+template <>
+__device__ __forceinline__ float4 ld_logit4<float>(const float* p) {
+    return *reinterpret_cast<const float4*>(p);
+}
+template <>
+__device__ __forceinline__ float4 ld_logit4<bf16>(const bf16* p) {
+    return ld_bf16x4(p);
+}
+
+template <int NV4, typename TL>
+__global__ __launch_bounds__(kBlock) void ce_fused_k(float* loss, bf16* grad, const TL* logits,
                                                      const int64_t* targets, int64_t V, float scale) {
     __shared__ float red[kBlock / kWave];
     const int64_t t = blockIdx.x;
     const int64_t tg = targets[t];
-    const float4* row = reinterpret_cast<const float4*>(logits + t * V);
+    const TL* rowp = logits + t * V;
+    auto row_at = [&](int64_t i) { return ld_logit4<TL>(rowp + 4 * i); };
     const int64_t V4 = V / 4;
     constexpr int R = NV4 > 0 ? NV4 : 1;
     float4 x[R];
@@ -245,12 +257,12 @@ __global__ __launch_bounds__(kBlock) void ce_fused_k(float* loss, bf16* grad, co
 #pragma unroll
         for (int j = 0; j < R; ++j) {
             const int64_t i = threadIdx.x + (int64_t)kBlock * j;
-            x[j] = i < V4 ? row[i] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+            x[j] = i < V4 ? row_at(i) : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
             m = fmaxf(m, fmaxf(fmaxf(x[j].x, x[j].y), fmaxf(x[j].z, x[j].w)));
         }
     } else {
         for (int64_t i = threadIdx.x; i < V4; i += kBlock) {
-            const float4 y = row[i];
+            const float4 y = row_at(i);
             m = fmaxf(m, fmaxf(fmaxf(y.x, y.y), fmaxf(y.z, y.w)));
         }
     }
@@ -262,13 +274,13 @@ __global__ __launch_bounds__(kBlock) void ce_fused_k(float* loss, bf16* grad, co
             s += __expf(x[j].x - m) + __expf(x[j].y - m) + __expf(x[j].z - m) + __expf(x[j].w - m);
     } else {
         for (int64_t i = threadIdx.x; i < V4; i += kBlock) {
-            const float4 y = row[i];
+            const float4 y = row_at(i);
             s += __expf(y.x - m) + __expf(y.y - m) + __expf(y.z - m) + __expf(y.w - m);
         }
     }
     s = block_sum(s, red);
     const bool live = tg >= 0 && tg < V;  // other targets are ignored rows
-    if (loss && threadIdx.x == 0) loss[t] = live ? -logits[t * V + tg] + (m + logf(s)) : 0.f;
+    if (loss && threadIdx.x == 0) loss[t] = live ? -(float)logits[t * V + tg] + (m + logf(s)) : 0.f;
     bf16* g = grad + t * V;
     auto emit = [&](int64_t i, float4 y) {
         float4 o;
@@ -292,7 +304,7 @@ __global__ __launch_bounds__(kBlock) void ce_fused_k(float* loss, bf16* grad, co
             if (i < V4) emit(i, x[j]);
         }
     } else {
-        for (int64_t i = threadIdx.x; i < V4; i += kBlock) emit(i, row[i]);
+        for (int64_t i = threadIdx.x; i < V4; i += kBlock) emit(i, row_at(i));
     }
 }
 
@@ -520,19 +532,28 @@ int32_t qkv_post(hipStream_t st, bf16* q, bf16* k, bf16* v, const bf16* qkv, con
     return check_launch("qkv_post");
 }
 
-int32_t ce_fused(hipStream_t st, float* loss, bf16* grad, const float* logits, const int64_t* targets, int64_t rows,
-                 int64_t V, float scale) {
+template <typename TL>
+static int32_t ce_fused_t(hipStream_t st, float* loss, bf16* grad, const TL* logits, const int64_t* targets,
+                          int64_t rows, int64_t V, float scale) {
     if (V % 4 != 0) return set_error(AR_EUNSUPPORTED, "ce_fused: vocab %lld not a multiple of 4", (long long)V);
     if (rows == 0) return AR_OK;
     if (rows > 0x7fffffff) return set_error(AR_EINVAL, "ce_fused: too many rows");
     const int64_t nv4 = cdiv(V, 4 * kBlock);
     const unsigned grid = (unsigned)rows;
-    if (nv4 <= 2) ce_fused_k<2><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
-    else if (nv4 <= 4) ce_fused_k<4><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
-    else if (nv4 <= 8) ce_fused_k<8><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
-    else if (nv4 <= 16) ce_fused_k<16><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
-    else ce_fused_k<0><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
+    if (nv4 <= 2) ce_fused_k<2, TL><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
+    else if (nv4 <= 4) ce_fused_k<4, TL><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
+    else if (nv4 <= 8) ce_fused_k<8, TL><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
+    else if (nv4 <= 16) ce_fused_k<16, TL><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
+    else ce_fused_k<0, TL><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
     return check_launch("ce_fused");
+}
+int32_t ce_fused(hipStream_t st, float* loss, bf16* grad, const float* logits, const int64_t* targets, int64_t rows,
+                 int64_t V, float scale) {
+    return ce_fused_t(st, loss, grad, logits, targets, rows, V, scale);
+}
+int32_t ce_fused(hipStream_t st, float* loss, bf16* grad, const bf16* logits, const int64_t* targets, int64_t rows,
+                 int64_t V, float scale) {
+    return ce_fused_t(st, loss, grad, logits, targets, rows, V, scale);
 }
 
 int32_t ve_bwd(hipStream_t st, float* gve, float* ggate, const bf16* gv, int64_t ldv, const float* gate,

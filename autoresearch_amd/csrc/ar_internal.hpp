@@ -109,6 +109,9 @@ int32_t qkv_post(hipStream_t st, bf16* q, bf16* k, bf16* v, const bf16* qkv, con
 // loss (may be null) and bf16 grad = (softmax - onehot) * scale per row.
 int32_t ce_fused(hipStream_t st, float* loss, bf16* grad, const float* logits, const int64_t* targets, int64_t rows,
                  int64_t V, float scale);
+// the same from bf16 (softcapped) logits
+int32_t ce_fused(hipStream_t st, float* loss, bf16* grad, const bf16* logits, const int64_t* targets, int64_t rows,
+                 int64_t V, float scale);
 // gve = gate * dv, ggate = per-head sum of table[idx] * dv (dv bf16, row stride ldv).
 int32_t ve_bwd(hipStream_t st, float* gve, float* ggate, const bf16* gv, int64_t ldv, const float* gate,
                const float* table, const int64_t* idx, int64_t nt, int64_t C, int64_t H, int64_t hd);

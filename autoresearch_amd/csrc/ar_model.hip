@@ -146,6 +146,8 @@ inline float* P(ar_gpt* m, int64_t i) { return m->params + m->t[i].offset; }
 inline float* G(ar_gpt* m, int64_t i) { return m->grads + m->t[i].offset; }
 inline const bf16* Wb(ar_gpt* m, int64_t i) { return m->wb + m->t[i].offset; }
 inline const bf16* WbT(ar_gpt* m, int64_t i) { return m->wbt + m->t[i].offset; }
+// the bf16 step's logits: bf16 values in the first half of the fp32 logits buffer
+inline bf16* LogitsB(ar_gpt* m) { return reinterpret_cast<bf16*>(m->logits); }
 
 inline ar_stream_t AS(ar_gpt* m) { return reinterpret_cast<ar_stream_t>(m->st); }
 
@@ -547,10 +549,11 @@ static int32_t forward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* tar
     }
     AR_TRY(resid_norm(st, 2, nullptr, nullptr, m->rms_final, m->x_final_b, nullptr, nullptr, m->x, nullptr, nullptr,
                       nullptr, nullptr, nullptr, 0, nullptr, 0, 0, BT, C));
-    AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_SOFTCAP, m->logits, false, m->x_final_b, true, Wb(m, m->i_lm), BT, V, C, nullptr,
+    // softcapped logits stored as bf16 (in the fp32 logits buffer), as a bf16 lm_head's output is
+    AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_SOFTCAP, LogitsB(m), true, m->x_final_b, true, Wb(m, m->i_lm), BT, V, C, nullptr,
                   nullptr, kSoftcap));
     // loss, and the loss gradient for loss_scale 1 while the row is loaded
-    AR_TRY(ce_fused(st, m->loss, m->grad_logits_b, m->logits, targets, BT, V, 1.0f));
+    AR_TRY(ce_fused(st, m->loss, m->grad_logits_b, LogitsB(m), targets, BT, V, 1.0f));
     m->grad_logits_scale = 1.0f;
     m->grad_logits_valid = true;
     return fixed_sum(st, m->mean_loss, m->loss, nullptr, BT, 0, 0, 0, m->scratch);
@@ -562,7 +565,7 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
     const int64_t F = kMlpExpansion * C;
     hipStream_t st = m->st;
     if (!m->grad_logits_valid || m->grad_logits_scale != loss_scale) {
-        AR_TRY(ce_fused(st, nullptr, m->grad_logits_b, m->logits, targets, BT, V, loss_scale));
+        AR_TRY(ce_fused(st, nullptr, m->grad_logits_b, LogitsB(m), targets, BT, V, loss_scale));
         m->grad_logits_scale = loss_scale;
         m->grad_logits_valid = true;
     }
