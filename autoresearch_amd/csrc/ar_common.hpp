@@ -82,7 +82,12 @@ template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf
 // barrier.  Compiler-tracked global loads issued after one of these are
 // waited for with counts that ignore it, which waits for it too (loads
 // complete in order): keep such loads ahead of the copies they should not
-// wait for.
+// wait for.  m0 is clobbered: the kernels that use these keep nothing of
+// their own in m0 (their ISA has no other m0 reference), so clang's warning
+// that a reserved register in a clobber list may not be preserved is
+// silenced here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ unsigned lds_addr(const void* p) {
     return (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
@@ -106,6 +111,8 @@ __device__ __forceinline__ void dma4(const void* g, unsigned lds) {
                  : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
                  : "memory", "m0");
 }
+
+#pragma clang diagnostic pop
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
