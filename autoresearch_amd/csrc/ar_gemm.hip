@@ -418,6 +418,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
                 *reinterpret_cast<float4*>(partial + (z * M + row) * N + col) = x;
             } else if constexpr (EPI == EPI_STORE) {
                 st4(C + o, x);
+                if (aux_out) st4(static_cast<bf16*>(aux_out) + bt * sC + o, x);  // bf16 copy (batched Muon)
             } else if constexpr (EPI == EPI_ACCUM || EPI == EPI_ADD) {
                 st4(C + o, add4(pre[PRE ? t : 0], x));
             } else if constexpr (EPI == EPI_RELU2) {
@@ -431,8 +432,10 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
                                        relu2_grad(a.w, x.w)));
             } else if constexpr (EPI == EPI_AXPBY) {
                 const float4 y = pre[PRE ? t : 0];
-                st4(C + o, make_float4(cap * x.x + beta * y.x, cap * x.y + beta * y.y, cap * x.z + beta * y.z,
-                                       cap * x.w + beta * y.w));
+                const float4 r = make_float4(cap * x.x + beta * y.x, cap * x.y + beta * y.y, cap * x.z + beta * y.z,
+                                             cap * x.w + beta * y.w);
+                st4(C + o, r);
+                if (aux_out) st4(static_cast<bf16*>(aux_out) + bt * sC + o, r);  // bf16 copy (batched Muon)
             }
         }
         __syncthreads();
@@ -931,6 +934,23 @@ int64_t gemm_partial_elems(int layout, int64_t M, int64_t N, int64_t K, int64_t 
 // Batched, GEMM-space form used by Muon: C_b[mo,no] = sum_r A_b(mo,r) B_b(no,r)
 // with A/B K-major (ak/bk) or MN-major, operand b at base + b * stride.  No
 // reduction split: the batch supplies the parallelism.
+// The same with bf16 operands in memory (copies of fp32 matrices, rounded as
+// the fp32-operand form rounds them on load, so the products are identical),
+// and an optional bf16 copy Cb of the fp32 result (same strides as C).
+int32_t gemm_batched_bf16(hipStream_t st, bool ak, bool bk, float* C, bf16* Cb, const bf16* A, const bf16* B,
+                          int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch,
+                          int64_t sA, int64_t sB, int64_t sC, const float* aux, float alpha, float beta) {
+    const int epi = aux ? EPI_AXPBY : -1;
+#define AR_GB(AKv, BKv)                                                                                          \
+    gemm_launch<bf16, bf16, float, AKv, BKv, true>(st, C, A, B, M, N, K, lda, ldb, ldc, false, 1, nullptr,         \
+                                                   "gemm_batched_bf16", batch, sA, sB, sC, epi, aux, Cb, alpha, beta)
+    if (ak && bk) return AR_GB(true, true);
+    if (ak && !bk) return AR_GB(true, false);
+    if (!ak && !bk) return AR_GB(false, false);
+    return AR_GB(false, true);
+#undef AR_GB
+}
+
 int32_t gemm_batched_f32(hipStream_t st, bool bf, bool ak, bool bk, float* C, const float* A, const float* B,
                          int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch,
                          int64_t sA, int64_t sB, int64_t sC, const float* aux, float alpha, float beta) {

@@ -38,6 +38,12 @@ int32_t gemm_batched_f32(hipStream_t st, bool bf16, bool ak, bool bk, float* C, 
                          int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch,
                          int64_t sA, int64_t sB, int64_t sC, const float* aux = nullptr, float alpha = 1.f,
                          float beta = 0.f);
+// The same with bf16 operands in memory and an optional bf16 copy Cb of the
+// fp32 result (same strides as C).
+int32_t gemm_batched_bf16(hipStream_t st, bool ak, bool bk, float* C, bf16* Cb, const bf16* A, const bf16* B,
+                          int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch,
+                          int64_t sA, int64_t sB, int64_t sC, const float* aux = nullptr, float alpha = 1.f,
+                          float beta = 0.f);
 
 // ---- reductions (ar_reduce.hip) ----
 constexpr int kSumBlocks = 512;

@@ -66,12 +66,17 @@ __global__ void norm_finish_k(float* scale, const float* partial) {
     scale[j] = 1.0f / (sqrtf(s) * 1.02f + 1e-6f);
 }
 
-__global__ void scale_multi_k(float* X, int64_t size, const float* scale) {
+// X_j *= scale_j, and Xb (if set) = bf16(X)
+__global__ void scale_multi_k(float* X, bf16* Xb, int64_t size, const float* scale) {
     const int j = blockIdx.y;
     const float sc = scale[j];
     float* x = X + (int64_t)j * size;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size; i += (int64_t)gridDim.x * blockDim.x)
-        x[i] = x[i] * sc;
+    bf16* xb = Xb ? Xb + (int64_t)j * size : nullptr;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size; i += (int64_t)gridDim.x * blockDim.x) {
+        const float v = x[i] * sc;
+        x[i] = v;
+        if (xb) xb[i] = (bf16)v;
+    }
 }
 
 // p -= lr (X + wd p [X p >= 0])  (optimizer.mojo:197-210)
@@ -100,10 +105,11 @@ double muon_lr_factor(int64_t rows, int64_t cols) {
 }
 
 int64_t muon_scratch_elems(int64_t rows, int64_t cols, bool bf16, int64_t n) {
-    (void)bf16;
     const int64_t size = rows * cols;
     const int64_t small = rows >= cols ? cols : rows;
-    return align64(n * kNormBlocks) + align64(n) + 2 * align64(n * size) + 2 * align64(n * small * small);
+    const int64_t f32 = align64(n * kNormBlocks) + align64(n) + 2 * align64(n * size) + 2 * align64(n * small * small);
+    // bf16 operand copies of X, Y, A, Bm (two per float)
+    return bf16 ? f32 + 2 * align64((n * size + 1) / 2) + 2 * align64((n * small * small + 1) / 2) : f32;
 }
 
 int32_t muon_group_step(hipStream_t st, float* const* params, const float* const* grads, float* const* mbufs, int n,
@@ -121,6 +127,13 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
     float* Y = X + align64(n * size);
     float* A = Y + align64(n * size);
     float* Bm = A + align64(n * ss);
+    // bf16 step: the products read bf16 copies of their operands, written by
+    // the kernel that produces each operand (the same rounding the fp32-operand
+    // products apply on load, so the results are the same)
+    ::ar::bf16* Xb = bf16 ? reinterpret_cast<::ar::bf16*>(Bm + align64(n * ss)) : nullptr;
+    ::ar::bf16* Yb = bf16 ? Xb + 2 * align64((n * size + 1) / 2) : nullptr;
+    ::ar::bf16* Ab = bf16 ? Yb + 2 * align64((n * size + 1) / 2) : nullptr;
+    ::ar::bf16* Bmb = bf16 ? Ab + 2 * align64((n * ss + 1) / 2) : nullptr;
 
     GroupTable t{};
     for (int j = 0; j < n; ++j) {
@@ -133,7 +146,7 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
     nesterov_multi_k<<<eg, 256, 0, st>>>(t, X, size, (float)momentum, dev.dsc ? dev.dsc + dev.mu_i : nullptr,
                                          partial);
     norm_finish_k<<<1, n, 0, st>>>(scale, partial);
-    scale_multi_k<<<eg, 256, 0, st>>>(X, size, scale);
+    scale_multi_k<<<eg, 256, 0, st>>>(X, Xb, size, scale);
     int32_t r = check_launch("muon: normalise");
     if (r) return r;
     ar_stream_t s = reinterpret_cast<ar_stream_t>(st);
@@ -142,7 +155,35 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
     // in the last product's epilogue, written to the other of X / Y.
     float* Xc = X;
     float* Yc = Y;
-    for (int it = 0; it < 5; ++it) {
+    ::ar::bf16* Xbc = Xb;
+    ::ar::bf16* Ybc = Yb;
+    for (int it = 0; it < 5 && bf16; ++it) {
+        const float ca = (float)kPolarA[it], cb = (float)kPolarB[it], cc = (float)kPolarC[it];
+        if (tall)
+            r = gemm_batched_bf16(st, false, false, A, Ab, Xbc, Xbc, cols, cols, rows, cols, cols, cols, n, size, size,
+                                  ss);
+        else
+            r = gemm_batched_bf16(st, true, true, A, Ab, Xbc, Xbc, rows, rows, cols, cols, cols, rows, n, size, size,
+                                  ss);
+        if (r) return r;
+        if ((r = gemm_batched_bf16(st, true, false, Bm, Bmb, Ab, Ab, sm, sm, sm, sm, sm, sm, n, ss, ss, ss, A, cc,
+                                   cb)))
+            return r;
+        if (tall)
+            r = gemm_batched_bf16(st, true, false, Yc, Ybc, Xbc, Bmb, rows, cols, cols, cols, cols, cols, n, size, ss,
+                                  size, Xc, 1.0f, ca);
+        else
+            r = gemm_batched_bf16(st, true, false, Yc, Ybc, Bmb, Xbc, rows, cols, rows, rows, cols, cols, n, ss, size,
+                                  size, Xc, 1.0f, ca);
+        if (r) return r;
+        float* tmp = Xc;
+        Xc = Yc;
+        Yc = tmp;
+        ::ar::bf16* tb = Xbc;
+        Xbc = Ybc;
+        Ybc = tb;
+    }
+    for (int it = 0; it < 5 && !bf16; ++it) {
         const float ca = (float)kPolarA[it], cb = (float)kPolarB[it], cc = (float)kPolarC[it];
         if (tall)  // A = X^T X : mo = c1, no = c2, r = row (both operands MN-major)
             r = gemm_batched_f32(st, bf16, false, false, A, Xc, Xc, cols, cols, rows, cols, cols, cols, n, size, size,
