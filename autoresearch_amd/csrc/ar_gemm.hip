@@ -685,7 +685,7 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
                     const int64_t o = rb + (int64_t)(t * 4) * ldc + clo;
                     if constexpr (EPI == EPI_PARTIAL) {
                         const int64_t row = row0 + i * 32 + h * 16 + r;
-                        *reinterpret_cast<float4*>(partial + ((int64_t)z * M + row) * N + col0 + lcol) = x;
+                        st4nt(partial + ((int64_t)z * M + row) * N + col0 + lcol, x);
                     } else if constexpr (EPI == EPI_STORE) {
                         st4nt(C + o, x);
                     } else if constexpr (EPI == EPI_ACCUM || EPI == EPI_ADD) {
