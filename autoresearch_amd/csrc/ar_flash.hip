@@ -208,6 +208,19 @@ struct RowOut {
     int64_t tok0, period;
 };
 
+// Output rows are stored with the nontemporal hint: they are not read again
+// by this kernel, and streaming them past L2 keeps the K / V (or Q / dO)
+// tiles that other workgroups of the same head still read resident there.
+__device__ __forceinline__ void st_nt(float* p, float4 x) {
+    __builtin_nontemporal_store(x.x, p);
+    __builtin_nontemporal_store(x.y, p + 1);
+    __builtin_nontemporal_store(x.z, p + 2);
+    __builtin_nontemporal_store(x.w, p + 3);
+}
+__device__ __forceinline__ void st_nt(bf16* p, bf16x4 v) {
+    __builtin_nontemporal_store(__builtin_bit_cast(unsigned long long, v), reinterpret_cast<unsigned long long*>(p));
+}
+
 template <int HD>
 __device__ __forceinline__ void store_rows(const RowOut& o, int row_base, int T, const f32x16 (&acc)[HD / 32],
                                            float colscale, float* scratch, int lane) {
@@ -234,8 +247,8 @@ __device__ __forceinline__ void store_rows(const RowOut& o, int row_base, int T,
             float4 x2 = *reinterpret_cast<const float4*>(scratch + r * LDS_ + (DT >= 2 ? 32 : 16) + c4);
             const int d1 = (DT >= 2 ? p * 32 : 0) + c4, d2 = d1 + HALF;
             if (o.of) {
-                *reinterpret_cast<float4*>(o.of + (int64_t)row * o.rsf + d1) = x1;
-                *reinterpret_cast<float4*>(o.of + (int64_t)row * o.rsf + d2) = x2;
+                st_nt(o.of + (int64_t)row * o.rsf + d1, x1);
+                st_nt(o.of + (int64_t)row * o.rsf + d2, x2);
             }
             if (o.ob) {
                 if (o.cos_t) {
@@ -253,8 +266,8 @@ __device__ __forceinline__ void store_rows(const RowOut& o, int row_base, int T,
                 bf16x4 b1, b2;
                 b1[0] = (bf16)x1.x; b1[1] = (bf16)x1.y; b1[2] = (bf16)x1.z; b1[3] = (bf16)x1.w;
                 b2[0] = (bf16)x2.x; b2[1] = (bf16)x2.y; b2[2] = (bf16)x2.z; b2[3] = (bf16)x2.w;
-                *reinterpret_cast<bf16x4*>(o.ob + (int64_t)row * o.rsb + d1) = b1;
-                *reinterpret_cast<bf16x4*>(o.ob + (int64_t)row * o.rsb + d2) = b2;
+                st_nt(o.ob + (int64_t)row * o.rsb + d1, b1);
+                st_nt(o.ob + (int64_t)row * o.rsb + d2, b2);
             }
         }
         __syncthreads();
