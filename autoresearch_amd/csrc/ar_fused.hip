@@ -33,13 +33,22 @@ namespace {
 constexpr int kBlock = 256;
 constexpr float kNormEps = 1e-5f;  // ops.mojo:61-104
 
+// Row outputs are stored with the nontemporal hint: these kernels stream
+// their rows once, and their outputs (up to 1 GB for the logits gradient)
+// would otherwise flush the L2 of data other waves are still reading.
 __device__ __forceinline__ void st_bf16x4(bf16* p, float4 v) {
     bf16x4 o;
     o[0] = (bf16)v.x;
     o[1] = (bf16)v.y;
     o[2] = (bf16)v.z;
     o[3] = (bf16)v.w;
-    *reinterpret_cast<bf16x4*>(p) = o;
+    __builtin_nontemporal_store(__builtin_bit_cast(unsigned long long, o), reinterpret_cast<unsigned long long*>(p));
+}
+__device__ __forceinline__ void st_f4(float4* p, float4 v) {
+    __builtin_nontemporal_store(v.x, &p->x);
+    __builtin_nontemporal_store(v.y, &p->y);
+    __builtin_nontemporal_store(v.z, &p->z);
+    __builtin_nontemporal_store(v.w, &p->w);
 }
 __device__ __forceinline__ float4 ld_bf16x4(const bf16* p) {
     const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
@@ -116,7 +125,7 @@ __global__ __launch_bounds__(kBlock) void resid_norm_k(NormArgs a) {
             for (int j = 0; j < NC; ++j) {
                 const int64_t i = lane + 64 * j;
                 v[j] = div4(v[j], rms0);
-                if (i < C4) reinterpret_cast<float4*>(a.x0_out + r * a.C)[i] = v[j];
+                if (i < C4) st_f4(reinterpret_cast<float4*>(a.x0_out + r * a.C) + i, v[j]);
                 v[j] = axpby4(sa, v[j], sb, v[j]);
             }
         } else {
@@ -133,7 +142,7 @@ __global__ __launch_bounds__(kBlock) void resid_norm_k(NormArgs a) {
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
             const int64_t i = lane + 64 * j;
-            if (MODE != 2 && i < C4) reinterpret_cast<float4*>(a.x_out + r * a.C)[i] = v[j];
+            if (MODE != 2 && i < C4) st_f4(reinterpret_cast<float4*>(a.x_out + r * a.C) + i, v[j]);
             ss += dot4(v[j], v[j]);
         }
         ss = wave_sum(ss);
@@ -404,7 +413,7 @@ __global__ __launch_bounds__(kBlock) void norm_bwd_k(NormBwdArgs a) {
                 p2 += dot4(o, reinterpret_cast<const float4*>(a.x0 + r * a.C)[i]);
                 o = mul4(o, scale);
             }
-            o4[i] = o;
+            st_f4(o4 + i, o);
             st_bf16x4(a.gxb + r * a.C + 4 * i, o);
         }
     }
