@@ -276,11 +276,16 @@ __global__ __launch_bounds__(kBlock) void ce_fused_k(float* loss, bf16* grad, co
         }
     }
     m = block_max(m, red);
+    // exp(x - m) once per element: the register-resident row keeps it for the
+    // gradient pass, which then scales by 1/s (a multiply, not a division).
+    auto ex4 = [&](float4 y) { return make_float4(__expf(y.x - m), __expf(y.y - m), __expf(y.z - m), __expf(y.w - m)); };
     float s = 0.f;
     if (NV4 > 0) {
 #pragma unroll
-        for (int j = 0; j < R; ++j)
-            s += __expf(x[j].x - m) + __expf(x[j].y - m) + __expf(x[j].z - m) + __expf(x[j].w - m);
+        for (int j = 0; j < R; ++j) {
+            x[j] = ex4(x[j]);
+            s += (x[j].x + x[j].y) + (x[j].z + x[j].w);
+        }
     } else {
         for (int64_t i = threadIdx.x; i < V4; i += kBlock) {
             const float4 y = row_at(i);
@@ -291,12 +296,14 @@ __global__ __launch_bounds__(kBlock) void ce_fused_k(float* loss, bf16* grad, co
     const bool live = tg >= 0 && tg < V;  // other targets are ignored rows
     if (loss && threadIdx.x == 0) loss[t] = live ? -(float)logits[t * V + tg] + (m + logf(s)) : 0.f;
     bf16* g = grad + t * V;
-    auto emit = [&](int64_t i, float4 y) {
+    const float rs = 1.0f / s;
+    // e = exp(logit - m) for four consecutive columns starting at 4 i
+    auto emit = [&](int64_t i, float4 e) {
         float4 o;
         if (!live) {
             o = make_float4(0.f, 0.f, 0.f, 0.f);
         } else {
-            o = make_float4(__expf(y.x - m) / s, __expf(y.y - m) / s, __expf(y.z - m) / s, __expf(y.w - m) / s);
+            o = mul4(e, rs);
             const int64_t e = tg - 4 * i;
             if (e == 0) o.x -= 1.0f;
             if (e == 1) o.y -= 1.0f;
@@ -313,7 +320,7 @@ __global__ __launch_bounds__(kBlock) void ce_fused_k(float* loss, bf16* grad, co
             if (i < V4) emit(i, x[j]);
         }
     } else {
-        for (int64_t i = threadIdx.x; i < V4; i += kBlock) emit(i, row_at(i));
+        for (int64_t i = threadIdx.x; i < V4; i += kBlock) emit(i, ex4(row_at(i)));
     }
 }
 

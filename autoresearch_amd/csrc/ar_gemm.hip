@@ -138,10 +138,11 @@ __device__ __forceinline__ float4 add4(float4 a, float4 b) {
 }
 // cap * tanh(x / cap) from the hardware exp2 and reciprocal:
 // tanh(y) = sign(y) (1 - 2 / (2^(2 |y| log2 e) + 1)), absolute error ~1e-7
-// (times cap); |y| large gives 2^inf = inf and exactly +-1.
+// (times cap); |y| large gives 2^inf = inf and exactly +-1.  The scale
+// 2 log2(e) / cap does not depend on x, so its division is hoisted out of the
+// epilogue loops: per element there is no IEEE division sequence (~10 VALU).
 __device__ __forceinline__ float softcap(float x, float cap) {
-    const float y = fabsf(x) / cap;
-    const float e = __builtin_amdgcn_exp2f(2.8853900817779268f * y);  // 2 log2(e) y
+    const float e = __builtin_amdgcn_exp2f(fabsf(x) * (2.8853900817779268f / cap));  // 2^(2 log2(e) |x| / cap)
     const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
     return copysignf(cap * t, x);
 }
@@ -149,7 +150,11 @@ __device__ __forceinline__ float4 softcap4(float4 x, float cap) {
     return make_float4(softcap(x.x, cap), softcap(x.y, cap), softcap(x.z, cap), softcap(x.w, cap));
 }
 // d/dh relu(h)^2 times g, from the activation a = relu(h)^2: 2 sqrt(a) g (0 where a == 0).
-__device__ __forceinline__ float relu2_grad(float a, float g) { return a > 0.f ? 2.f * sqrtf(a) * g : 0.f; }
+// The hardware square root (1 ulp) instead of sqrtf's correctly rounded
+// sequence (~15 VALU): a is a rounded activation, far coarser than 1 ulp.
+__device__ __forceinline__ float relu2_grad(float a, float g) {
+    return a > 0.f ? 2.f * __builtin_amdgcn_sqrtf(a) * g : 0.f;
+}
 
 template <typename T, int N>
 __device__ __forceinline__ void vload(T (&dst)[N], const T* src) {
