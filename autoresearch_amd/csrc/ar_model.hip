@@ -93,6 +93,13 @@ struct ar_gpt {
     // graph replay of the step (ar_gpt_train_step_graph)
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
+    // Muon's three shape groups (square, c_fc, mlp_proj) are independent:
+    // the c_fc and mlp_proj groups run on two side streams (default
+    // priority) forked from and joined back into st, each with its own
+    // region of scratch starting at muon_off[group].
+    hipStream_t side[2] = {nullptr, nullptr};
+    hipEvent_t fork_ev = nullptr, join_ev[2] = {nullptr, nullptr};
+    int64_t muon_off[3] = {0, 0, 0};
     hipGraphNode_t graph_scalars = nullptr;
     const int64_t *graph_in = nullptr, *graph_tg = nullptr;
     // scratch (sequential users on one stream)
@@ -405,14 +412,24 @@ static int32_t gpt_build(ar_gpt* m) {
         upd(gemm_partial_elems(2, BT, s[0], s[1], gemm_auto_splits(2, m->bf16, BT, s[0], s[1])));
     const int64_t groups = (4 * Lr + kMuonMaxGroup - 1) / kMuonMaxGroup;
     const int64_t sq = (4 * Lr + groups - 1) / groups;  // square matrices per launch group
-    upd(muon_scratch_elems(C, C, m->bf16, sq));
-    upd(muon_scratch_elems(F, C, m->bf16, Lr < kMuonMaxGroup ? Lr : kMuonMaxGroup));
-    upd(muon_scratch_elems(C, F, m->bf16, Lr < kMuonMaxGroup ? Lr : kMuonMaxGroup));
+    // the three Muon shape groups run concurrently: disjoint scratch regions
+    const int64_t lg = Lr < kMuonMaxGroup ? Lr : kMuonMaxGroup;
+    // (each size is a whole number of 64-float blocks)
+    m->muon_off[1] = muon_scratch_elems(C, C, m->bf16, sq);
+    m->muon_off[2] = m->muon_off[1] + muon_scratch_elems(F, C, m->bf16, lg);
+    upd(m->muon_off[2] + muon_scratch_elems(C, F, m->bf16, lg));
     upd(BT * (C > kv ? C : kv));                  // embedding scatter partials
     upd((int64_t)kGateBlocks * H * kGateChannels);  // ve gate partials
     upd(2 * (int64_t)kNormBwdWaves);                // learned-scalar gradient partials
     m->scratch_elems = need;
     FALLOC(m->scratch, need);
+    for (int i = 0; i < 2; ++i) {
+        if (hipStreamCreateWithFlags(&m->side[i], hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&m->join_ev[i], hipEventDisableTiming) != hipSuccess)
+            return set_error(AR_EHIP, "gpt_create: side stream / event");
+    }
+    if (hipEventCreateWithFlags(&m->fork_ev, hipEventDisableTiming) != hipSuccess)
+        return set_error(AR_EHIP, "gpt_create: fork event");
     int bits = 1;
     while ((int64_t(1) << bits) < V) ++bits;
     m->sort_bits = bits;
@@ -459,6 +476,12 @@ extern "C" int32_t ar_gpt_create(ar_gpt** out, const ar_gpt_config* cfg, int64_t
 extern "C" int32_t ar_gpt_destroy(ar_gpt* m) {
     if (!m) return AR_OK;
     hipStreamSynchronize(m->st);
+    for (int i = 0; i < 2; ++i) {
+        if (m->side[i]) hipStreamSynchronize(m->side[i]);
+        if (m->side[i]) hipStreamDestroy(m->side[i]);
+        if (m->join_ev[i]) hipEventDestroy(m->join_ev[i]);
+    }
+    if (m->fork_ev) hipEventDestroy(m->fork_ev);
     if (m->graph_exec) hipGraphExecDestroy(m->graph_exec);
     if (m->graph) hipGraphDestroy(m->graph);
     for (hipEvent_t e : m->ev) hipEventDestroy(e);
@@ -859,7 +882,19 @@ static int32_t optimizer_kernels(ar_gpt* m) {
         fc.push_back(m->i_fc[i]);
         mp.push_back(m->i_mlpp[i]);
     }
+    // Profiling runs keep every group on st, in order, so that each group's
+    // events bracket only its own kernels.
+    const bool fork = !m->prof;
+    if (fork) {
+        if (hipEventRecord(m->fork_ev, m->st) != hipSuccess || hipStreamWaitEvent(m->side[0], m->fork_ev, 0) != hipSuccess ||
+            hipStreamWaitEvent(m->side[1], m->fork_ev, 0) != hipSuccess)
+            return set_error(AR_EHIP, "optimizer: fork");
+    }
+    int gi = 0;
     for (const std::vector<int64_t>* grp : {&sq, &fc, &mp}) {
+        const hipStream_t gst = fork && gi > 0 ? m->side[gi - 1] : m->st;
+        float* const gscratch = m->scratch + m->muon_off[gi];
+        ++gi;
         const int64_t total = (int64_t)grp->size();
         const int64_t ngroups = (total + kMuonMaxGroup - 1) / kMuonMaxGroup;
         const int64_t per = (total + ngroups - 1) / ngroups;
@@ -881,12 +916,18 @@ static int32_t optimizer_kernels(ar_gpt* m) {
             dev.mu_i = kScMu;
             dev.wd_i = kScWd;
             const int e = prof_begin(m);
-            AR_TRY(muon_group_step(m->st, ps, gs, ms, n, t0.rows, t0.cols, 0.04, 1.0, 0.0, 0.0, m->bf16, m->scratch,
+            AR_TRY(muon_group_step(gst, ps, gs, ms, n, t0.rows, t0.cols, 0.04, 1.0, 0.0, 0.0, m->bf16, gscratch,
                                    dev));
             const double smd = (double)(t0.rows < t0.cols ? t0.rows : t0.cols);
             const double lgd = (double)(t0.rows < t0.cols ? t0.cols : t0.rows);
             prof_end(m, e, 6, n * 5.0 * (4.0 * lgd * smd * smd + 2.0 * smd * smd * smd));
         }
+    }
+    if (fork) {
+        for (int i = 0; i < 2; ++i)
+            if (hipEventRecord(m->join_ev[i], m->side[i]) != hipSuccess ||
+                hipStreamWaitEvent(m->st, m->join_ev[i], 0) != hipSuccess)
+                return set_error(AR_EHIP, "optimizer: join");
     }
     return AR_OK;
 }
