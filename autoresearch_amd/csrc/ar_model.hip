@@ -858,9 +858,20 @@ static StepScalars step_scalars(ar_gpt* m, double progress) {
 // The optimizer's kernels, all scalars read from m->dsc.
 static int32_t optimizer_kernels(ar_gpt* m) {
     const ar_gpt_config& c = m->c;
+    // Profiling runs keep every kernel on st, in order, so that each Muon
+    // group's events bracket only its own kernels.  Otherwise the AdamW
+    // updates and the mlp_proj Muon group share side stream 1 and the c_fc
+    // group runs on side stream 0, beside the square group on st.
+    const bool fork = !m->prof;
+    if (fork) {
+        if (hipEventRecord(m->fork_ev, m->st) != hipSuccess || hipStreamWaitEvent(m->side[0], m->fork_ev, 0) != hipSuccess ||
+            hipStreamWaitEvent(m->side[1], m->fork_ev, 0) != hipSuccess)
+            return set_error(AR_EHIP, "optimizer: fork");
+    }
+    const hipStream_t ast = fork ? m->side[1] : m->st;
     auto adam = [&](int64_t ti, int lr_i, int bc1_i, float b1) -> int32_t {
         const Tensor& t = m->t[ti];
-        return adamw_dev(m->st, m->params + t.offset, m->grads + t.offset, m->adam_m + t.offset,
+        return adamw_dev(ast, m->params + t.offset, m->grads + t.offset, m->adam_m + t.offset,
                          m->adam_v + t.offset, t.size, m->dsc, lr_i, bc1_i, kScBc2, b1, 0.95f, 1e-10f, 0.0f);
     };
     AR_TRY(adam(m->i_lm, kScLrLm, kScBc1Default, 0.8f));
@@ -881,14 +892,6 @@ static int32_t optimizer_kernels(ar_gpt* m) {
         sq.push_back(m->i_proj[i]);
         fc.push_back(m->i_fc[i]);
         mp.push_back(m->i_mlpp[i]);
-    }
-    // Profiling runs keep every group on st, in order, so that each group's
-    // events bracket only its own kernels.
-    const bool fork = !m->prof;
-    if (fork) {
-        if (hipEventRecord(m->fork_ev, m->st) != hipSuccess || hipStreamWaitEvent(m->side[0], m->fork_ev, 0) != hipSuccess ||
-            hipStreamWaitEvent(m->side[1], m->fork_ev, 0) != hipSuccess)
-            return set_error(AR_EHIP, "optimizer: fork");
     }
     int gi = 0;
     for (const std::vector<int64_t>* grp : {&sq, &fc, &mp}) {
