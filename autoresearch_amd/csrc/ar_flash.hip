@@ -28,6 +28,8 @@
 // [B, T, H] fp32; outputs O, dQ, dK, dV in fp32 and / or bf16 (any row
 // stride: the bf16 step writes dQ | dK | dV into one [B*T, 3C] buffer, dQ and
 // dK already rotated back by the inverse rope).
+#include <type_traits>
+
 #include "ar_internal.hpp"
 
 namespace ar {
@@ -65,6 +67,20 @@ __device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
 template <int HD>
 __device__ __forceinline__ bf16x8 rowfrag(const bf16* tile, int r, int ks, int lane) {
     return *reinterpret_cast<const bf16x8*>(tile + Geo<HD>::off(r, 2 * ks + (lane >> 5)));
+}
+
+// The same fragment as rowfrag(tile + 32 kb HD, lane % 32, ks, lane), from
+// base = rowbase(lane): chunk 2 ks + lane / 32 of a row sits at
+// ((2 ks + lane / 32) ^ swz) * 16 = (((lane / 32) ^ swz) * 16) ^ (ks * 32)
+// bytes into the row (2 ks is even, and the row's 2 HD bytes are a power of
+// two above every chunk offset), so each k-step's address is one XOR.
+template <int HD>
+__device__ __forceinline__ unsigned rowbase(int lane) {
+    return 2u * (unsigned)Geo<HD>::off(lane & 31, lane >> 5);
+}
+template <int HD>
+__device__ __forceinline__ bf16x8 rowfrag_x(const bf16* tile, unsigned base, int ks) {
+    return *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(tile) + (base ^ (unsigned)(ks << 5)));
 }
 
 // Transposed fragment of a natural tile for 32-row block rb, k-step s and
@@ -336,7 +352,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
         return !(kv0 > qw + 31 || (window > 0 && kv0 + kTile - 1 < qw - window) || qw >= T);
     };
     auto scores = [&](const bf16* sK, f32x16 (&sc)[2]) {
-        const int ln = opaque_lane(threadIdx.x % kWave);
+        const unsigned rb = rowbase<HD>(opaque_lane(threadIdx.x % kWave));
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -344,7 +360,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
 #pragma unroll
         for (int ks = 0; ks < G::KSTEPS; ++ks)
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) sc[kb] = mma(rowfrag<HD>(sK, kb * 32 + (ln & 31), ks, ln), qf[ks], sc[kb]);
+            for (int kb = 0; kb < 2; ++kb) sc[kb] = mma(rowfrag_x<HD>(sK + kb * 32 * HD, rb, ks), qf[ks], sc[kb]);
     };
     auto mask = [&](f32x16 (&sc)[2], int kv0) {
 #pragma unroll
@@ -433,7 +449,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
             const float m_use = softmax_max(cur);
             const float alpha = exp2_fast(m - m_use);
             const bf16* sK = kbuf(it + 1);
-            const int ln = opaque_lane(threadIdx.x % kWave);
+            const unsigned rb = rowbase<HD>(opaque_lane(threadIdx.x % kWave));
             float rsum = 0.f;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
@@ -444,7 +460,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
             for (int ks = 0; ks < G::KSTEPS; ++ks)
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
-                    nxt[kb] = mma(rowfrag<HD>(sK, kb * 32 + (ln & 31), ks, ln), qf[ks], nxt[kb]);
+                    nxt[kb] = mma(rowfrag_x<HD>(sK + kb * 32 * HD, rb, ks), qf[ks], nxt[kb]);
 #pragma unroll
                     for (int j = 0; j < EPM; ++j) {
                         const int flat = (ks * 2 + kb) * EPM + j, ckb = flat >> 4, ce = flat & 15;
@@ -552,6 +568,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
         const bool skip = kv0 > qw + 31 || (window > 0 && kv0 + kTile - 1 < qw - window) || qw >= T;
         if (!skip) {
             const int lane = opaque_lane(threadIdx.x % kWave);
+            const unsigned rb = rowbase<HD>(lane);
             const bool full = kv0 + kTile - 1 <= qw && qw + 31 < T && (window <= 0 || kv0 >= qw + 31 - window);
             // one 32-key half at a time keeps only one S / dP pair live
 #pragma unroll
@@ -561,15 +578,23 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
                 for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.f;
 #pragma unroll
                 for (int ks = 0; ks < G::KSTEPS; ++ks) {
-                    s = mma(rowfrag<HD>(sK, kb * 32 + (lane & 31), ks, lane), qf[ks], s);
-                    dp = mma(rowfrag<HD>(sV, kb * 32 + (lane & 31), ks, lane), df[ks], dp);
+                    s = mma(rowfrag_x<HD>(sK + kb * 32 * HD, rb, ks), qf[ks], s);
+                    dp = mma(rowfrag_x<HD>(sV + kb * 32 * HD, rb, ks), df[ks], dp);
                 }
+                // full tiles skip the per-element mask (a wave-uniform branch)
+                auto ds = [&](auto masked) {
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const bool ok = full | visible(kv0 + kb * 32 + acc_row(e, lane), my_q, T, window);
-                    const float p = ok ? exp2_fast(s[e] * scale_log2 - my_lse2) : 0.f;
-                    s[e] = p * (dp[e] - my_D);
-                }
+                    for (int e = 0; e < 16; ++e) {
+                        const bool ok = !decltype(masked)::value ||
+                                        visible(kv0 + kb * 32 + acc_row(e, lane), my_q, T, window);
+                        const float p = ok ? exp2_fast(s[e] * scale_log2 - my_lse2) : 0.f;
+                        s[e] = p * (dp[e] - my_D);
+                    }
+                };
+                if (full)
+                    ds(std::false_type{});
+                else
+                    ds(std::true_type{});
                 // dQ^T += K^T dS^T
 #pragma unroll
                 for (int st = 0; st < 2; ++st) {
@@ -679,6 +704,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
         const bool skip = qt0 + KT - 1 < kw || (window > 0 && qt0 > kw + 31 + window) || kw >= T;
         if (!skip) {
             const int lane = opaque_lane(threadIdx.x % kWave);
+            const unsigned rb = rowbase<HD>(lane);
             const bool full = qt0 >= kw + 31 && qt0 + KT <= T && kw + 31 < T &&
                               (window <= 0 || kw >= qt0 + KT - 1 - window);
             f32x16 s, dp;
@@ -686,26 +712,34 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
             for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.f;
 #pragma unroll
             for (int ks = 0; ks < G::KSTEPS; ++ks) {
-                s = mma(rowfrag<HD>(sQ, lane & 31, ks, lane), kf[ks], s);
-                dp = mma(rowfrag<HD>(sD, lane & 31, ks, lane), rowfrag<HD>(sV, wave * 32 + (lane & 31), ks, lane), dp);
+                s = mma(rowfrag_x<HD>(sQ, rb, ks), kf[ks], s);
+                dp = mma(rowfrag_x<HD>(sD, rb, ks), rowfrag_x<HD>(sV + wave * 32 * HD, rb, ks), dp);
             }
             // lane: key my_k; rows: queries qt0 + acc_row(e); s becomes P, dp becomes dS.
+            // Full tiles skip the per-element mask (a wave-uniform branch).
+            auto ds = [&](auto masked) {
 #pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                const int q4 = 8 * a + 4 * (lane >> 5);
-                const float4 l4 = *reinterpret_cast<const float4*>(sL + q4);
-                const float4 d4 = *reinterpret_cast<const float4*>(sDl + q4);
-                const float lvv[4] = {l4.x * kLog2e, l4.y * kLog2e, l4.z * kLog2e, l4.w * kLog2e};
-                const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+                for (int a = 0; a < 4; ++a) {
+                    const int q4 = 8 * a + 4 * (lane >> 5);
+                    const float4 l4 = *reinterpret_cast<const float4*>(sL + q4);
+                    const float4 d4 = *reinterpret_cast<const float4*>(sDl + q4);
+                    const float lvv[4] = {l4.x * kLog2e, l4.y * kLog2e, l4.z * kLog2e, l4.w * kLog2e};
+                    const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int e = 4 * a + j;
-                    const bool ok = full | ((my_k < T) & visible(my_k, qt0 + q4 + j, T, window));
-                    const float pv = ok ? exp2_fast(fmaf(s[e], scale_log2, -lvv[j])) : 0.f;
-                    s[e] = pv;
-                    dp[e] = pv * (dp[e] - dv4[j]);
+                    for (int j = 0; j < 4; ++j) {
+                        const int e = 4 * a + j;
+                        const bool ok = !decltype(masked)::value ||
+                                        ((my_k < T) & visible(my_k, qt0 + q4 + j, T, window));
+                        const float pv = ok ? exp2_fast(fmaf(s[e], scale_log2, -lvv[j])) : 0.f;
+                        s[e] = pv;
+                        dp[e] = pv * (dp[e] - dv4[j]);
+                    }
                 }
-            }
+            };
+            if (full)
+                ds(std::false_type{});
+            else
+                ds(std::true_type{});
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
                 const bf16x8 fp = accfrag(s, st), fs = accfrag(dp, st);
