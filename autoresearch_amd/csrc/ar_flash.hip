@@ -99,6 +99,27 @@ __device__ __forceinline__ bf16x8 trfrag(const bf16* tile, int rb, int s, int ct
     return __builtin_bit_cast(bf16x8, both);
 }
 
+// trfrag's two reads from per-lane byte bases tb0 / tb1 (those of rb = s =
+// ct = 0): a lane's row swizzle depends only on its row within the 16-row
+// group, rb and s move the reads by whole rows, and column block ct enters the
+// chunk index as 4 ct, which the swizzle's XOR carries to 64 ct bytes.
+template <int HD>
+__device__ __forceinline__ void trbase(int lane, unsigned& tb0, unsigned& tb1) {
+    const int g = lane >> 4, src = lane & 15;
+    const int row = 4 * (g >> 1) + (src >> 2);
+    const int col = 16 * (g & 1) + 4 * (src & 3);
+    tb0 = 2u * (unsigned)(Geo<HD>::off(row, col >> 3) + (col & 7));
+    tb1 = 2u * (unsigned)(Geo<HD>::off(row + 8, col >> 3) + (col & 7));
+}
+template <int HD>
+__device__ __forceinline__ bf16x8 trfrag_x(const bf16* tile, unsigned tb0, unsigned tb1, int rb, int s, int ct) {
+    const char* t = reinterpret_cast<const char*>(tile + (32 * rb + 16 * s) * HD);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + (tb0 ^ (unsigned)(64 * ct))));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + (tb1 ^ (unsigned)(64 * ct))));
+    const s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(bf16x8, both);
+}
+
 // 2^x with the hardware's v_exp_f32: results below 2^-126 (probabilities
 // that change no fp32 sum they enter) flush to zero, and 2^-inf = 0.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -569,6 +590,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
         if (!skip) {
             const int lane = opaque_lane(threadIdx.x % kWave);
             const unsigned rb = rowbase<HD>(lane);
+            unsigned tb0, tb1;
+            trbase<HD>(lane, tb0, tb1);
             const bool full = kv0 + kTile - 1 <= qw && qw + 31 < T && (window <= 0 || kv0 >= qw + 31 - window);
             // one 32-key half at a time keeps only one S / dP pair live
 #pragma unroll
@@ -587,7 +610,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
                     for (int e = 0; e < 16; ++e) {
                         const bool ok = !decltype(masked)::value ||
                                         visible(kv0 + kb * 32 + acc_row(e, lane), my_q, T, window);
-                        const float p = ok ? exp2_fast(s[e] * scale_log2 - my_lse2) : 0.f;
+                        const float p = ok ? exp2_fast(fmaf(s[e], scale_log2, -my_lse2)) : 0.f;
                         s[e] = p * (dp[e] - my_D);
                     }
                 };
@@ -600,7 +623,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
                 for (int st = 0; st < 2; ++st) {
                     const bf16x8 db = accfrag(s, st);
 #pragma unroll
-                    for (int dt = 0; dt < G::DT; ++dt) acc[dt] = mma(trfrag<HD>(sK, kb, st, dt, lane), db, acc[dt]);
+                    for (int dt = 0; dt < G::DT; ++dt) acc[dt] = mma(trfrag_x<HD>(sK, tb0, tb1, kb, st, dt), db, acc[dt]);
                 }
             }
         }
@@ -705,6 +728,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
         if (!skip) {
             const int lane = opaque_lane(threadIdx.x % kWave);
             const unsigned rb = rowbase<HD>(lane);
+            unsigned tb0, tb1;
+            trbase<HD>(lane, tb0, tb1);
             const bool full = qt0 >= kw + 31 && qt0 + KT <= T && kw + 31 < T &&
                               (window <= 0 || kw >= qt0 + KT - 1 - window);
             f32x16 s, dp;
@@ -745,8 +770,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
                 const bf16x8 fp = accfrag(s, st), fs = accfrag(dp, st);
 #pragma unroll
                 for (int dt = 0; dt < G::DT; ++dt) {
-                    adv[dt] = mma(trfrag<HD>(sD, 0, st, dt, lane), fp, adv[dt]);
-                    adk[dt] = mma(trfrag<HD>(sQ, 0, st, dt, lane), fs, adk[dt]);
+                    adv[dt] = mma(trfrag_x<HD>(sD, tb0, tb1, 0, st, dt), fp, adv[dt]);
+                    adk[dt] = mma(trfrag_x<HD>(sQ, tb0, tb1, 0, st, dt), fs, adk[dt]);
                 }
             }
         }
