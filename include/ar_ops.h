@@ -236,7 +236,12 @@ typedef struct ar_gpt ar_gpt;
 /* Allocates weights, gradients, optimizer state and activation buffers
  * (ModelWeights, ForwardBuffers, AdamWState, MuonState).  rope_period: 0 =
  * reference table indexing (row = flat token b*T+t; needs B*T <= 2048 like
- * the reference's table), T = per-sequence positions.  precision: AR_PREC_*. */
+ * the reference's table), T = per-sequence positions.  precision: AR_PREC_*.
+ * Every call on the model is ordered on `stream`; the optimizer step also
+ * forks work onto two library-owned streams (default priority) and joins
+ * them back into `stream` before it returns control of the ordering, so a
+ * caller sees stream-ordered semantics (and a graph capture of `stream`
+ * records the fork and join). */
 int32_t ar_gpt_create(ar_gpt** out, const ar_gpt_config* cfg, int64_t B, int64_t T, int32_t precision,
                       int64_t rope_period, ar_stream_t stream);
 int32_t ar_gpt_destroy(ar_gpt* model);
