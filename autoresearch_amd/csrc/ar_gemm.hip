@@ -839,9 +839,13 @@ static bool pk_ok(int64_t gm, int64_t gn, int64_t gk, int64_t lda, int64_t ldb, 
 }
 // Reduction splits: powers of two (each split a whole number of k-tiles and
 // at least 4 of them) until there are >= 256 work items.
+// Split count of the persistent kernel: the largest power of two whose work
+// items still fit one round of the 256 workgroups.  One more doubling would
+// spill items into a second round, which costs the same k-steps on the
+// busiest workgroup plus one more partial epilogue and twice the partials.
 static int64_t pk_splits(int64_t tiles, int64_t gk) {
     int64_t s = 1;
-    while (tiles * s < 256 && gk % (2 * s * kPkBK) == 0 && gk / (2 * s) >= 4 * kPkBK) s *= 2;
+    while (tiles * 2 * s <= 256 && gk % (2 * s * kPkBK) == 0 && gk / (2 * s) >= 4 * kPkBK) s *= 2;
     return s;
 }
 static int pk_cus() {
@@ -934,18 +938,16 @@ static int64_t gemm_k_splits(bool bf16, int64_t gm, int64_t gn, int64_t gk) {
     return bf16 ? choose_splits<true>(tiles, gk, 0, kps, target) : choose_splits<false>(tiles, gk, 0, kps, target);
 }
 
-// The larger of the two kernels' split counts, so that scratch sized with it
-// serves whichever kernel a TN call of this shape runs on.
+// Split count of a TN call: the persistent kernel's for the bf16 shapes it
+// runs, otherwise gemm_k's; scratch sized with it serves either kernel.
 int64_t gemm_auto_splits(int layout, bool bf16, int64_t M, int64_t N, int64_t K) {
     if (layout != 2) return 1;
     int64_t gm, gn, gk;
     gemm_space(layout, M, N, K, gm, gn, gk);
-    int64_t s = gemm_k_splits(bf16, gm, gn, gk);
-    if (bf16 && pk_shape(gm, gn, gk)) {
-        const int64_t p = pk_splits((gm / 256) * (gn / 256), gk);
-        if (p > s) s = p;
-    }
-    return s;
+    // bf16 shapes of the persistent kernel run there; its split count also
+    // serves gemm_k, which takes the count as given if it runs instead
+    if (bf16 && pk_shape(gm, gn, gk)) return pk_splits((gm / 256) * (gn / 256), gk);
+    return gemm_k_splits(bf16, gm, gn, gk);
 }
 
 int64_t gemm_partial_elems(int layout, int64_t M, int64_t N, int64_t K, int64_t splits) {
