@@ -143,11 +143,17 @@ class Model:
         self.B, self.T = B, T
         self.h = L.orc_model_create(ct.byref(self.cfg), B, T, rope_period)
         self.n = L.orc_model_num_params(self.h)
+        # held by the instance: at interpreter exit the module globals (lib,
+        # _lib) may already be gone when __del__ runs
+        self._destroy = L.orc_model_destroy
+
+    def close(self):
+        if getattr(self, "h", None):
+            self._destroy(self.h)
+            self.h = None
 
     def __del__(self):
-        if getattr(self, "h", None):
-            lib().orc_model_destroy(self.h)
-            self.h = None
+        self.close()
 
     def init_weights(self, seed0: int = 42):
         lib().orc_model_init_weights(self.h, seed0)

@@ -399,3 +399,17 @@ def test_model_lm_head_gradient_finite_difference():
         p[o + j] = old
         fd = (lp - lm) / (2 * h)
         assert abs(fd - g[j]) <= 2e-3 * max(1.0, abs(g[j])), (j, fd, g[j])
+
+
+def test_model_released_cleanly_at_interpreter_exit():
+    """An oracle Model still alive when the interpreter exits is destroyed
+    without an 'Exception ignored' report (module globals may already be gone)."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = ("from oracle import oracle as orc\n"
+            "m = orc.Model(dict(sequence_len=64, vocab_size=512, n_layer=2, n_head=2, n_kv_head=2, n_embd=128,"
+            " head_dim=64, kv_dim=128), 2, 64, 0)\n")
+    r = subprocess.run([sys.executable, "-c", code], cwd=root, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert "Exception ignored" not in r.stderr, r.stderr
