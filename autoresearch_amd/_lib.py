@@ -22,6 +22,7 @@ _TYPES = {
     "uint64_t": ct.c_uint64,
     "float": ct.c_float,
     "double": ct.c_double,
+    "size_t": ct.c_size_t,
     "void": None,
     "const char*": ct.c_char_p,
     "ar_stream_t": ct.c_void_p,

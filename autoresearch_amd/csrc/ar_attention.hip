@@ -596,7 +596,7 @@ extern "C" int32_t ar_flash_attn_fwd(ar_stream_t stream, float* output, float* l
 namespace {
 int32_t to_bf16_ws(ar_stream_t stream, const float* const* src, int n, int64_t elems, ar::bf16** dst) {
     int32_t st;
-    ar::bf16* w = (ar::bf16*)ar::workspace((size_t)n * (size_t)elems * sizeof(ar::bf16), &st);
+    ar::bf16* w = (ar::bf16*)ar::workspace(S(stream), (size_t)n * (size_t)elems * sizeof(ar::bf16), &st);
     if (!w) return st;
     for (int i = 0; i < n; ++i) {
         dst[i] = w + (int64_t)i * elems;

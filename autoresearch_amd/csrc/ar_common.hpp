@@ -22,15 +22,15 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
-// ---- error plumbing (ar_errors.cpp) ----
+// ---- error plumbing and workspaces (ar_runtime.hip) ----
 int32_t set_error(int32_t code, const char* fmt, ...);
 int32_t check_launch(const char* what);
 inline hipStream_t S(ar_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
-// Library-owned device workspace, grown on demand (ar_errors.cpp).  Kernels
-// queued earlier on any stream may still read the old buffer, so growth
-// synchronises the device before freeing it.
-void* workspace(size_t bytes, int32_t* status);
+// The scratch of the workspace the caller bound to stream st on the current
+// device (ar_workspace_bind), if it holds at least `bytes`; otherwise null and
+// *status = AR_ENOMEM with a message naming the bytes needed.  Never allocates.
+void* workspace(hipStream_t st, size_t bytes, int32_t* status);
 
 // ---- device helpers ----
 __device__ __forceinline__ float wave_sum(float v) {

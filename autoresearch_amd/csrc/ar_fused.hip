@@ -5,21 +5,21 @@
 // same fp32 value inside every consumer.  The small element-wise steps of the
 // reference around each GEMM are folded into single passes over a row:
 //
-//   resid_norm    scaled_add_fwd + rmsnorm_fwd (ops.mojo:61-104, 566-579),
+//   resid_norm    scaled_add_fwd + rmsnorm_fwd (ops.mojo:579-594, 61-104),
 //                 on layer 0 also embedding_fwd + its rmsnorm (model.mojo:
-//                 598-603), on value-embedding layers also ve_gate_fwd
+//                 605-615), on value-embedding layers also ve_gate_fwd
 //                 (ops.mojo:516-541) from the fp32 normalised row
-//   qkv_post      rope_fwd of q and k (ops.mojo:386-419), their per-head
-//                 rmsnorm (model.mojo:661-668), ve_apply_fwd on v
-//                 (ops.mojo:543-564), written as bf16 attention operands
+//   qkv_post      rope_fwd of q and k (ops.mojo:209-238), their per-head
+//                 rmsnorm (model.mojo:679-687), ve_apply_fwd on v
+//                 (ops.mojo:544-560), written as bf16 attention operands
 //   ce_fused      cross_entropy_fwd + cross_entropy_softcap_bwd (ops.mojo:
-//                 713-864) from one read of the logits row
+//                 672-740, 778-864) from one read of the logits row
 //   ve_bwd        ve_apply_bwd (ops.mojo:1193-1237) from the bf16 dV that the
 //                 attention backward writes into the packed [dq | dk | dv]
 //                 buffer (it also applies rope_bwd to dq / dk there)
 //   norm_bwd      rmsnorm_bwd (ops.mojo:1039-1085) + add_residual, and on the
 //                 attention norm the two learned-scalar gradient dots
-//                 (ops.mojo:1277-1308) and scaled_add_bwd (ops.mojo:1311-1336)
+//                 (ops.mojo:1277-1308) and scaled_add_bwd (ops.mojo:1170-1190)
 //
 // Per element the arithmetic is the reference kernels'; only the order of
 // the row sums (wave reductions) differs.  All reductions are fixed-order.
@@ -640,3 +640,26 @@ int32_t precompute_d_mixed(hipStream_t st, float* d, const float* o, const bf16*
 }
 
 }  // namespace ar
+
+// The bf16 step's LM-head loss as one C-ABI call (the same two launches the
+// training step runs: the SOFTCAP-epilogue GEMM, then ce_fused).
+extern "C" int32_t ar_lm_head_softcap_ce_bf16(ar_stream_t stream, float* loss_out, void* grad_logits, void* logits,
+                                              const void* input, const void* weight, const int64_t* targets,
+                                              int64_t num_tokens, int64_t vocab_size, int64_t embd_dim, float cap,
+                                              float loss_scale) {
+    AR_CHECK_ARG(grad_logits && logits && input && weight && targets, "lm_head_softcap_ce: null pointer");
+    AR_CHECK_ARG(num_tokens >= 0 && vocab_size > 0 && embd_dim > 0, "lm_head_softcap_ce: bad sizes");
+    AR_CHECK_ARG(((num_tokens | vocab_size | embd_dim) & 7) == 0,
+                 "lm_head_softcap_ce: num_tokens, vocab_size and embd_dim must be multiples of 8");
+    AR_CHECK_ARG(((reinterpret_cast<uintptr_t>(grad_logits) | reinterpret_cast<uintptr_t>(logits) |
+                   reinterpret_cast<uintptr_t>(input) | reinterpret_cast<uintptr_t>(weight)) & 15) == 0,
+                 "lm_head_softcap_ce: operands must be 16-byte aligned");
+    AR_CHECK_ARG(cap > 0.f, "lm_head_softcap_ce: cap must be positive");
+    if (num_tokens == 0) return AR_OK;
+    const hipStream_t st = ar::S(stream);
+    const int32_t r = ar::gemm_epilogue(st, 0, ar::GEMM_EPI_SOFTCAP, logits, 1, input, 1, weight, 1, num_tokens,
+                                        vocab_size, embd_dim, nullptr, nullptr, cap);
+    if (r != AR_OK) return r;
+    return ar::ce_fused(st, loss_out, static_cast<ar::bf16*>(grad_logits), static_cast<const ar::bf16*>(logits),
+                        targets, num_tokens, vocab_size, loss_scale);
+}

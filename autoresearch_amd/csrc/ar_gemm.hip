@@ -837,17 +837,6 @@ static bool pk_ok(int64_t gm, int64_t gn, int64_t gk, int64_t lda, int64_t ldb, 
     return fits && pk_shape(gm, gn, gk) && lda % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 &&
            ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C)) & 15) == 0;
 }
-// Reduction splits: powers of two (each split a whole number of k-tiles and
-// at least 4 of them) until there are >= 256 work items.
-// Split count of the persistent kernel: the largest power of two whose work
-// items still fit one round of the 256 workgroups.  One more doubling would
-// spill items into a second round, which costs the same k-steps on the
-// busiest workgroup plus one more partial epilogue and twice the partials.
-static int64_t pk_splits(int64_t tiles, int64_t gk) {
-    int64_t s = 1;
-    while (tiles * 2 * s <= 256 && gk % (2 * s * kPkBK) == 0 && gk / (2 * s) >= 4 * kPkBK) s *= 2;
-    return s;
-}
 static int pk_cus() {
     static int cus[64] = {0};
     int dev = 0;
@@ -858,6 +847,17 @@ static int pk_cus() {
         cus[dev] = n;
     }
     return cus[dev];
+}
+// Split count of the persistent kernel: the largest power of two (each split
+// a whole number of k-tiles, at least 4 of them) whose work items still fit
+// one round of the persistent workgroups, one per CU.  One more doubling
+// would spill items into a second round, which costs the same k-steps on the
+// busiest workgroup plus one more partial epilogue and twice the partials.
+static int64_t pk_splits(int64_t tiles, int64_t gk) {
+    const int64_t wgs = pk_cus();
+    int64_t s = 1;
+    while (tiles * 2 * s <= wgs && gk % (2 * s * kPkBK) == 0 && gk / (2 * s) >= 4 * kPkBK) s *= 2;
+    return s;
 }
 
 // C (+)= A . B^T in GEMM space with gemm_pk (operands checked by pk_ok).
@@ -938,15 +938,16 @@ static int64_t gemm_k_splits(bool bf16, int64_t gm, int64_t gn, int64_t gk) {
     return bf16 ? choose_splits<true>(tiles, gk, 0, kps, target) : choose_splits<false>(tiles, gk, 0, kps, target);
 }
 
-// Split count of a TN call: the persistent kernel's for the bf16 shapes it
-// runs, otherwise gemm_k's; scratch sized with it serves either kernel.
-int64_t gemm_auto_splits(int layout, bool bf16, int64_t M, int64_t N, int64_t K) {
+// Split count of a TN call: the persistent kernel's for the shapes it runs
+// (bf16 operands in memory, whole tiles), otherwise gemm_k's; scratch sized
+// with it serves either kernel.
+int64_t gemm_auto_splits(int layout, bool bf16, bool bf16_operands, int64_t M, int64_t N, int64_t K) {
     if (layout != 2) return 1;
     int64_t gm, gn, gk;
     gemm_space(layout, M, N, K, gm, gn, gk);
-    // bf16 shapes of the persistent kernel run there; its split count also
-    // serves gemm_k, which takes the count as given if it runs instead
-    if (bf16 && pk_shape(gm, gn, gk)) return pk_splits((gm / 256) * (gn / 256), gk);
+    // its split count also serves gemm_k, which takes the count as given if
+    // it runs instead (a misaligned operand)
+    if (bf16 && bf16_operands && pk_shape(gm, gn, gk)) return pk_splits((gm / 256) * (gn / 256), gk);
     return gemm_k_splits(bf16, gm, gn, gk);
 }
 
@@ -1019,7 +1020,8 @@ static int32_t gemm_typed(hipStream_t st, int layout, TC* C, const TX* X, const 
     if (layout == 1)
         return gemm_launch<TX, TW, TC, true, false, true>(st, C, X, W, M, K, N, N, K, K, accumulate, 1, nullptr,
                                                           "linear_bwd_dx");
-    if (splits < 1) splits = gemm_auto_splits(2, true, M, N, K);
+    if (splits < 1)
+        splits = gemm_auto_splits(2, true, std::is_same<TX, bf16>::value && std::is_same<TW, bf16>::value, M, N, K);
     return gemm_launch<TX, TW, TC, false, false, true>(st, C, X, W, N, K, M, N, K, K, accumulate, splits, partial,
                                                        "linear_bwd_dw");
 }
@@ -1091,7 +1093,7 @@ int32_t gemm_f32(hipStream_t st, int layout, bool bf, float* C, const float* X, 
                                                                     nullptr, "linear_bwd_dx");
     }
     // TN: GEMM (mo=N, no=K, r=M): A(mo=n, r=m) = dY[m][n] MN-major, B(no=k, r=m) = X[m][k] MN-major.
-    if (splits < 1) splits = gemm_auto_splits(2, bf, M, N, K);
+    if (splits < 1) splits = gemm_auto_splits(2, bf, false, M, N, K);
     if (bf)
         return gemm_launch<float, float, float, false, false, true>(st, C, X, W, N, K, M, N, K, K, accumulate,
                                                                     splits, partial, "linear_bwd_dw");
@@ -1109,11 +1111,8 @@ static int32_t check_gemm_args(const void* C, const void* A, const void* B, int6
                                const char* nm) {
     if (!C || !A || !B) return set_error(AR_EINVAL, "%s: null pointer", nm);
     if (M < 0 || N < 0 || K < 0) return set_error(AR_EINVAL, "%s: negative dimension", nm);
-    if ((M | N | K) & 7)
-        return set_error(AR_EINVAL, "%s: M, N, K must be multiples of 8 (got %lld, %lld, %lld)", nm, (long long)M,
-                         (long long)N, (long long)K);
-    if ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C)) & 15)
-        return set_error(AR_EINVAL, "%s: operands must be 16-byte aligned", nm);
+    if ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C)) & 3)
+        return set_error(AR_EINVAL, "%s: operands must be 4-byte aligned floats", nm);
     return AR_OK;
 }
 
@@ -1122,50 +1121,143 @@ static inline bool overlaps(const void* a, size_t abytes, const void* b, size_t 
     return pa < pb + bbytes && pb < pa + abytes;
 }
 
+// The matrix-core kernels take dimensions in multiples of 8 and 16-byte
+// aligned operands.  Other calls run the same kernels on zero-padded copies
+// in the workspace (the padding adds zero products only) and copy the valid
+// region back: the tail path of the reference's bounds-checked tiles
+// (ops.mojo:150-168).
+static bool gemm_direct(const void* C, const void* A, const void* B, int64_t M, int64_t N, int64_t K) {
+    return ((M | N | K) & 7) == 0 &&
+           ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C)) & 15) == 0;
+}
+static inline int64_t r8(int64_t x) { return (x + 7) & ~int64_t(7); }
+static inline size_t al256(size_t b) { return (b + 255) & ~size_t(255); }
+
+namespace {
+// dst[r][c] (row stride ldd) = src[r][c] (row stride lds) inside rows x
+// cols, 0 elsewhere in the drows x dcols destination.
+__global__ void copy2d_k(float* dst, int64_t ldd, const float* src, int64_t lds, int64_t rows, int64_t cols,
+                         int64_t drows, int64_t dcols) {
+    const int64_t n = drows * dcols;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / dcols, c = i - r * dcols;
+        dst[r * ldd + c] = (r < rows && c < cols) ? src[r * lds + c] : 0.f;
+    }
+}
+}  // namespace
+
+static int32_t copy2d(hipStream_t st, float* dst, int64_t ldd, const float* src, int64_t lds, int64_t rows,
+                      int64_t cols, int64_t drows, int64_t dcols) {
+    if (drows * dcols == 0) return AR_OK;
+    copy2d_k<<<flat_grid(drows * dcols, 256), 256, 0, st>>>(dst, ldd, src, lds, rows, cols, drows, dcols);
+    return check_launch("gemm pad copy");
+}
+
+// layout 0: C[M,N] = X[M,K] W[N,K]^T; 1: C[M,K] = X[M,N] W[N,K]; 2: C[N,K] += X[M,N]^T W[M,K].
+// Operand shapes (rows, cols) per layout, in that order: X, W, C.
+static void gemm_operand_shapes(int layout, int64_t M, int64_t N, int64_t K, int64_t sh[3][2]) {
+    const int64_t x[3][2] = {{M, K}, {M, N}, {M, N}};
+    const int64_t w[3][2] = {{N, K}, {N, K}, {M, K}};
+    const int64_t c[3][2] = {{M, N}, {M, K}, {N, K}};
+    for (int i = 0; i < 2; ++i) {
+        sh[0][i] = x[layout][i];
+        sh[1][i] = w[layout][i];
+        sh[2][i] = c[layout][i];
+    }
+}
+
+static size_t gemm_pad_bytes(int layout, bool bf, int64_t M, int64_t N, int64_t K) {
+    int64_t sh[3][2];
+    gemm_operand_shapes(layout, r8(M), r8(N), r8(K), sh);
+    size_t b = 0;
+    for (int i = 0; i < 3; ++i) b += al256((size_t)sh[i][0] * sh[i][1] * sizeof(float));
+    if (layout == 2) {
+        const int64_t s = ar::gemm_auto_splits(2, bf, false, r8(M), r8(N), r8(K));
+        if (s > 1) b += al256((size_t)ar::gemm_partial_elems(2, r8(M), r8(N), r8(K), s) * sizeof(float));
+    }
+    return b;
+}
+
+// Workspace bytes of one linear_* call (0 when it needs none).
+static size_t gemm_ws_bytes(int layout, bool bf, const void* C, const void* X, const void* W, int64_t M, int64_t N,
+                            int64_t K) {
+    if (!gemm_direct(C, X, W, M, N, K)) return gemm_pad_bytes(layout, bf, M, N, K);
+    size_t b = 0;
+    if (layout == 1 && overlaps(C, M * K * 4, X, M * N * 4)) b += al256((size_t)M * N * sizeof(float));
+    if (layout == 2) {
+        const int64_t s = ar::gemm_auto_splits(2, bf, false, M, N, K);
+        if (s > 1) b += al256((size_t)ar::gemm_partial_elems(2, M, N, K, s) * sizeof(float));
+    }
+    return b;
+}
+
+static int32_t gemm_padded(hipStream_t st, int layout, bool bf, float* C, const float* X, const float* W, int64_t M,
+                           int64_t N, int64_t K, char* ws) {
+    int64_t sh[3][2], ph[3][2];
+    gemm_operand_shapes(layout, M, N, K, sh);
+    gemm_operand_shapes(layout, r8(M), r8(N), r8(K), ph);
+    float* xp = (float*)ws;
+    float* wp = (float*)(ws + al256((size_t)ph[0][0] * ph[0][1] * 4));
+    float* cp = (float*)((char*)wp + al256((size_t)ph[1][0] * ph[1][1] * 4));
+    float* part = (float*)((char*)cp + al256((size_t)ph[2][0] * ph[2][1] * 4));
+    // the copies read all of X before C is written: alias-safe (linear_bwd_dx in place)
+    int32_t r = copy2d(st, xp, ph[0][1], X, sh[0][1], sh[0][0], sh[0][1], ph[0][0], ph[0][1]);
+    if (!r) r = copy2d(st, wp, ph[1][1], W, sh[1][1], sh[1][0], sh[1][1], ph[1][0], ph[1][1]);
+    if (!r && layout == 2) r = copy2d(st, cp, ph[2][1], C, sh[2][1], sh[2][0], sh[2][1], ph[2][0], ph[2][1]);
+    if (r) return r;
+    const int64_t splits = layout == 2 ? ar::gemm_auto_splits(2, bf, false, r8(M), r8(N), r8(K)) : 1;
+    r = ar::gemm_f32(st, layout, bf, cp, xp, wp, r8(M), r8(N), r8(K), layout == 2, splits, part);
+    if (r) return r;
+    return copy2d(st, C, sh[2][1], cp, ph[2][1], sh[2][0], sh[2][1], sh[2][0], sh[2][1]);
+}
+
+static int32_t linear_call(ar_stream_t s, int layout, bool bf, float* C, const float* X, const float* W, int64_t M,
+                           int64_t N, int64_t K, const char* nm) {
+    int32_t st = check_gemm_args(C, X, W, M, N, K, nm);
+    if (st) return st;
+    int64_t sh[3][2];
+    gemm_operand_shapes(layout, M, N, K, sh);
+    const size_t cb = (size_t)sh[2][0] * sh[2][1] * 4;
+    if (sh[2][0] * sh[2][1] == 0) return AR_OK;
+    if (overlaps(C, cb, W, (size_t)sh[1][0] * sh[1][1] * 4) ||
+        (layout != 1 && overlaps(C, cb, X, (size_t)sh[0][0] * sh[0][1] * 4)))
+        return set_error(AR_EINVAL, "%s: output overlaps an input", nm);
+    const int64_t red = layout == 0 ? K : (layout == 1 ? N : M);  // reduction length
+    if (red == 0) return layout == 2 ? AR_OK : ar_zero_buffer(s, C, sh[2][0] * sh[2][1]);
+    const size_t need = gemm_ws_bytes(layout, bf, C, X, W, M, N, K);
+    char* ws = nullptr;
+    if (need) {
+        ws = (char*)ar::workspace(S(s), need, &st);
+        if (!ws) return st;
+    }
+    if (!gemm_direct(C, X, W, M, N, K)) return gemm_padded(S(s), layout, bf, C, X, W, M, N, K, ws);
+    const float* src = X;
+    if (layout == 1 && overlaps(C, cb, X, (size_t)M * N * 4)) {
+        // model.mojo:906 calls this in place; read all of dY first (copy).
+        if (hipMemcpyAsync(ws, X, (size_t)M * N * sizeof(float), hipMemcpyDeviceToDevice, S(s)) != hipSuccess)
+            return set_error(AR_EHIP, "linear_bwd_dx: alias copy failed");
+        src = (const float*)ws;
+    }
+    int64_t splits = 1;
+    float* partial = nullptr;
+    if (layout == 2) {
+        splits = ar::gemm_auto_splits(2, bf, false, M, N, K);
+        if (splits > 1) partial = (float*)ws;
+    }
+    return ar::gemm_f32(S(s), layout, bf, C, src, W, M, N, K, layout == 2, splits, partial);
+}
+
 static int32_t linear_fwd_impl(ar_stream_t s, float* out, const float* in, const float* w, int64_t M, int64_t N,
                                int64_t K, bool bf) {
-    int32_t st = check_gemm_args(out, in, w, M, N, K, "linear_fwd");
-    if (st) return st;
-    if (M == 0 || N == 0) return AR_OK;
-    if (overlaps(out, M * N * 4, in, M * K * 4) || overlaps(out, M * N * 4, w, N * K * 4))
-        return set_error(AR_EINVAL, "linear_fwd: output overlaps an input");
-    if (K == 0) return ar_zero_buffer(s, out, M * N);
-    return ar::gemm_f32(S(s), 0, bf, out, in, w, M, N, K, false, 1, nullptr);
+    return linear_call(s, 0, bf, out, in, w, M, N, K, "linear_fwd");
 }
-
 static int32_t linear_bwd_dx_impl(ar_stream_t s, float* dx, const float* dy, const float* w, int64_t M, int64_t N,
                                   int64_t K, bool bf) {
-    int32_t st = check_gemm_args(dx, dy, w, M, N, K, "linear_bwd_dx");
-    if (st) return st;
-    if (M == 0 || K == 0) return AR_OK;
-    if (overlaps(dx, M * K * 4, w, N * K * 4)) return set_error(AR_EINVAL, "linear_bwd_dx: grad_input overlaps weight");
-    if (N == 0) return ar_zero_buffer(s, dx, M * K);
-    const float* src = dy;
-    if (overlaps(dx, M * K * 4, dy, M * N * 4)) {
-        // model.mojo:906 calls this in place; read all of dY first (copy).
-        float* tmp = (float*)ar::workspace((size_t)M * N * sizeof(float), &st);
-        if (!tmp) return st;
-        if (hipMemcpyAsync(tmp, dy, (size_t)M * N * sizeof(float), hipMemcpyDeviceToDevice, S(s)) != hipSuccess)
-            return set_error(AR_EHIP, "linear_bwd_dx: alias copy failed");
-        src = tmp;
-    }
-    return ar::gemm_f32(S(s), 1, bf, dx, src, w, M, N, K, false, 1, nullptr);
+    return linear_call(s, 1, bf, dx, dy, w, M, N, K, "linear_bwd_dx");
 }
-
 static int32_t linear_bwd_dw_impl(ar_stream_t s, float* dw, const float* dy, const float* x, int64_t M, int64_t N,
                                   int64_t K, bool bf) {
-    int32_t st = check_gemm_args(dw, dy, x, M, N, K, "linear_bwd_dw");
-    if (st) return st;
-    if (N == 0 || K == 0 || M == 0) return AR_OK;
-    if (overlaps(dw, N * K * 4, dy, M * N * 4) || overlaps(dw, N * K * 4, x, M * K * 4))
-        return set_error(AR_EINVAL, "linear_bwd_dw: grad_weight overlaps an input");
-    const int64_t splits = ar::gemm_auto_splits(2, bf, M, N, K);
-    float* partial = nullptr;
-    if (splits > 1) {
-        partial = (float*)ar::workspace((size_t)ar::gemm_partial_elems(2, M, N, K, splits) * sizeof(float), &st);
-        if (!partial) return st;
-    }
-    return ar::gemm_f32(S(s), 2, bf, dw, dy, x, M, N, K, true, splits, partial);
+    return linear_call(s, 2, bf, dw, dy, x, M, N, K, "linear_bwd_dw");
 }
 
 extern "C" int32_t ar_linear_fwd(ar_stream_t stream, float* output, const float* input, const float* weight,
@@ -1201,12 +1293,14 @@ extern "C" int32_t ar_gemm_mixed(ar_stream_t stream, int32_t layout, void* C, in
                                  int32_t accumulate) {
     int32_t st = check_gemm_args(C, X, W, M, N, K, "gemm_mixed");
     if (st) return st;
+    if (!gemm_direct(C, X, W, M, N, K))
+        return set_error(AR_EINVAL, "gemm_mixed: M, N, K must be multiples of 8 and operands 16-byte aligned");
     if (layout < 0 || layout > 2) return set_error(AR_EINVAL, "gemm_mixed: layout must be 0 (NT), 1 (NN) or 2 (TN)");
     if (M == 0 || N == 0 || K == 0) return AR_OK;
-    const int64_t splits = layout == 2 ? ar::gemm_auto_splits(2, true, M, N, K) : 1;
+    const int64_t splits = layout == 2 ? ar::gemm_auto_splits(2, true, x_bf16 && w_bf16, M, N, K) : 1;
     float* partial = nullptr;
     if (splits > 1) {
-        partial = (float*)ar::workspace((size_t)ar::gemm_partial_elems(2, M, N, K, splits) * sizeof(float), &st);
+        partial = (float*)ar::workspace(S(stream), (size_t)ar::gemm_partial_elems(2, M, N, K, splits) * sizeof(float), &st);
         if (!partial) return st;
     }
     return ar::gemm_bf16io(S(stream), layout, C, c_bf16, X, x_bf16, W, w_bf16, M, N, K, accumulate != 0, splits,

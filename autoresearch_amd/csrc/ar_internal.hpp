@@ -16,7 +16,8 @@ namespace ar {
 // splits: 1 = no reduction split; 0 = choose automatically (TN only).
 // partial: fp32 scratch of at least gemm_partial_elems(...) elements when the
 // chosen split count is > 1 (may be null otherwise).
-int64_t gemm_auto_splits(int layout, bool bf16, int64_t M, int64_t N, int64_t K);
+// bf16_operands: both operands stored as bf16 (the persistent kernel's case).
+int64_t gemm_auto_splits(int layout, bool bf16, bool bf16_operands, int64_t M, int64_t N, int64_t K);
 int64_t gemm_partial_elems(int layout, int64_t M, int64_t N, int64_t K, int64_t splits);
 int32_t gemm_f32(hipStream_t st, int layout, bool bf16, float* C, const float* X, const float* W, int64_t M,
                  int64_t N, int64_t K, bool accumulate, int64_t splits, float* partial);

@@ -409,7 +409,7 @@ static int32_t gpt_build(ar_gpt* m) {
     auto upd = [&](int64_t n) { if (n > need) need = n; };
     const int64_t dw_shapes[][2] = {{C, C}, {kv, C}, {F, C}, {C, F}, {V, C}, {3 * C, C}};
     for (auto& s : dw_shapes)
-        upd(gemm_partial_elems(2, BT, s[0], s[1], gemm_auto_splits(2, m->bf16, BT, s[0], s[1])));
+        upd(gemm_partial_elems(2, BT, s[0], s[1], gemm_auto_splits(2, m->bf16, m->bf16, BT, s[0], s[1])));
     const int64_t groups = (4 * Lr + kMuonMaxGroup - 1) / kMuonMaxGroup;
     const int64_t sq = (4 * Lr + groups - 1) / groups;  // square matrices per launch group
     // the three Muon shape groups run concurrently: disjoint scratch regions
@@ -547,7 +547,7 @@ static int32_t forward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* tar
     for (int64_t i = 0; i < c.n_layer; ++i) {
         LayerBufsB& b = m->LB[i];
         const bool ve = has_ve(c, i);
-        // layer 0: x0 = norm(wte[idx]) (model.mojo:598-603); x = res*x_in + x0l*x0; xn = norm(x)
+        // layer 0: x0 = norm(wte[idx]) (model.mojo:605-618); x = res*x_in + x0l*x0; xn = norm(x)
         AR_TRY(resid_norm(st, i == 0 ? 0 : 1, m->x0, b.x, b.rms_attn, b.xn, ve ? b.xg : nullptr,
                           ve ? b.gate : nullptr, m->x, m->x0, P(m, m->i_wte), inputs, P(m, m->i_res), P(m, m->i_x0),
                           i, ve ? P(m, m->i_gate[i]) : nullptr, H, kGateChannels, BT, C));
@@ -855,19 +855,11 @@ static StepScalars step_scalars(ar_gpt* m, double progress) {
     return s;
 }
 
-// The optimizer's kernels, all scalars read from m->dsc.
-static int32_t optimizer_kernels(ar_gpt* m) {
+// The optimizer's kernels, all scalars read from m->dsc; fork: the AdamW
+// updates and the mlp_proj Muon group on side stream 1, the c_fc group on
+// side stream 0, the square group on st.
+static int32_t optimizer_body(ar_gpt* m, bool fork) {
     const ar_gpt_config& c = m->c;
-    // Profiling runs keep every kernel on st, in order, so that each Muon
-    // group's events bracket only its own kernels.  Otherwise the AdamW
-    // updates and the mlp_proj Muon group share side stream 1 and the c_fc
-    // group runs on side stream 0, beside the square group on st.
-    const bool fork = !m->prof;
-    if (fork) {
-        if (hipEventRecord(m->fork_ev, m->st) != hipSuccess || hipStreamWaitEvent(m->side[0], m->fork_ev, 0) != hipSuccess ||
-            hipStreamWaitEvent(m->side[1], m->fork_ev, 0) != hipSuccess)
-            return set_error(AR_EHIP, "optimizer: fork");
-    }
     const hipStream_t ast = fork ? m->side[1] : m->st;
     auto adam = [&](int64_t ti, int lr_i, int bc1_i, float b1) -> int32_t {
         const Tensor& t = m->t[ti];
@@ -926,13 +918,27 @@ static int32_t optimizer_kernels(ar_gpt* m) {
             prof_end(m, e, 6, n * 5.0 * (4.0 * lgd * smd * smd + 2.0 * smd * smd * smd));
         }
     }
-    if (fork) {
-        for (int i = 0; i < 2; ++i)
-            if (hipEventRecord(m->join_ev[i], m->side[i]) != hipSuccess ||
-                hipStreamWaitEvent(m->st, m->join_ev[i], 0) != hipSuccess)
-                return set_error(AR_EHIP, "optimizer: join");
-    }
     return AR_OK;
+}
+
+static int32_t optimizer_kernels(ar_gpt* m) {
+    // Profiling runs keep every kernel on st, in order, so that each Muon
+    // group's events bracket only its own kernels.
+    const bool fork = !m->prof;
+    if (!fork) return optimizer_body(m, false);
+    if (hipEventRecord(m->fork_ev, m->st) != hipSuccess || hipStreamWaitEvent(m->side[0], m->fork_ev, 0) != hipSuccess ||
+        hipStreamWaitEvent(m->side[1], m->fork_ev, 0) != hipSuccess)
+        return set_error(AR_EHIP, "optimizer: fork");
+    // The side streams are joined back into st on every path, also after a
+    // failed launch: st then still orders after everything queued on them
+    // (and a capture of st ends with every forked stream joined).
+    const int32_t r = optimizer_body(m, true);
+    int32_t rj = AR_OK;
+    for (int i = 0; i < 2; ++i)
+        if (hipEventRecord(m->join_ev[i], m->side[i]) != hipSuccess ||
+            hipStreamWaitEvent(m->st, m->join_ev[i], 0) != hipSuccess)
+            rj = set_error(AR_EHIP, "optimizer: join");
+    return r != AR_OK ? r : rj;
 }
 
 // train.mojo:246-281
@@ -960,7 +966,7 @@ extern "C" int32_t ar_gpt_train_step(ar_gpt* m, const int64_t* inputs, const int
 }
 
 // ar_gpt_train_step from a HIP graph: [set scalars] -> [zero_grads, forward,
-// backward without the sort, optimizer kernels].  The scalar node's kernel
+// token-id sort, backward, optimizer kernels].  The scalar node's kernel
 // arguments are replaced before each launch (hipGraphExecKernelNodeSetParams
 // copies them), so the host never races a pending replay.
 extern "C" int32_t ar_gpt_train_step_graph(ar_gpt* m, const int64_t* inputs, const int64_t* targets,
@@ -989,6 +995,7 @@ extern "C" int32_t ar_gpt_train_step_graph(ar_gpt* m, const int64_t* inputs, con
             return set_error(AR_EHIP, "gpt_train_step_graph: begin capture failed");
         int32_t r = ar_zero_buffer(AS(m), m->grads, m->nparams);
         if (!r) r = m->bf16 ? forward_bf16(m, inputs, targets) : forward_fp32(m, inputs, targets);
+        if (!r) r = sort_tokens(m, inputs);
         if (!r) r = m->bf16 ? backward_bf16(m, inputs, targets, 1.0f) : backward_fp32(m, inputs, targets, 1.0f);
         if (!r) r = optimizer_kernels(m);
         const hipError_t ec = hipStreamEndCapture(m->st, &body);
@@ -1016,7 +1023,6 @@ extern "C" int32_t ar_gpt_train_step_graph(ar_gpt* m, const int64_t* inputs, con
     } else if (hipGraphExecKernelNodeSetParams(m->graph_exec, m->graph_scalars, &kp) != hipSuccess) {
         return set_error(AR_EHIP, "gpt_train_step_graph: scalar update failed");
     }
-    AR_TRY(sort_tokens(m, inputs));
     if (hipGraphLaunch(m->graph_exec, m->st) != hipSuccess) return set_error(AR_EHIP, "gpt_train_step_graph: launch failed");
     if (loss_host) {
         if (hipMemcpyAsync(loss_host, m->mean_loss, sizeof(float), hipMemcpyDeviceToHost, m->st) != hipSuccess ||

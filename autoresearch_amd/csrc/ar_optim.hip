@@ -221,7 +221,7 @@ extern "C" int32_t ar_muon_step(ar_stream_t stream, float* params, float* grads,
     AR_CHECK_ARG(rows > 0 && cols > 0 && rows % 8 == 0 && cols % 8 == 0, "muon_step: rows, cols must be multiples of 8");
     const bool bf = precision == AR_PREC_BF16;
     int32_t st;
-    float* scratch = (float*)ar::workspace((size_t)ar::muon_scratch_elems(rows, cols, bf, 1) * sizeof(float), &st);
+    float* scratch = (float*)ar::workspace(ar::S(stream), (size_t)ar::muon_scratch_elems(rows, cols, bf, 1) * sizeof(float), &st);
     if (!scratch) return st;
     float* p[1] = {params};
     const float* g[1] = {grads};

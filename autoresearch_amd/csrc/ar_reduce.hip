@@ -7,8 +7,6 @@
 // partials in a fixed assignment and a second kernel adds them in a fixed
 // order, so every result is run-to-run deterministic (the reference's float
 // atomics, ops.mojo:1160-1164 / 1267-1274 / 1307-1308, are not).
-#include <hipcub/hipcub.hpp>
-
 #include "ar_internal.hpp"
 
 using namespace ar;
@@ -323,10 +321,105 @@ __global__ void ve_gate_bwd_finish_k(float* gw, const float* partial, int nblock
 // then each id's row is G[v] = ((G[v] + chunk_0) + chunk_1) + ... in order.
 constexpr int kEmbChunk = 64;
 
-__global__ void emb_keys_k(uint32_t* keys, int32_t* vals, const int64_t* idx, int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-        keys[i] = (uint32_t)idx[i];
-        vals[i] = (int32_t)i;
+// Stable LSD counting sort of the token ids (pairs id -> token position).
+// Each pass sorts by one digit of at most kSortMaxBits bits:
+//   sort_hist_k     per tile of kSortTile positions, the count of each digit
+//                   (LDS integer atomics: the counts do not depend on order),
+//                   stored digit-major: hist[d * ntiles + tile];
+//   sort_scan_k     one workgroup turns hist into exclusive offsets in that
+//                   order (all of digit 0 over the tiles in order, then digit
+//                   1, ...), i.e. the first output slot of (digit, tile);
+//   sort_scatter_k  one wave per tile walks its positions in order, 64 at a
+//                   time: the lanes holding the same digit are found with one
+//                   ballot per digit bit, ranked by lane, and placed after the
+//                   (digit, tile) offset advanced by the earlier rounds.
+// Tiles, rounds and lanes are visited in position order, so equal digits keep
+// their input order (stable), and the result is the same on every run.
+constexpr int kSortTile = 2048;
+constexpr int kSortMaxBits = 11;
+
+__global__ __launch_bounds__(256) void sort_hist_k(int32_t* hist, const int64_t* ids, const uint32_t* keys, int64_t n,
+                                                    int shift, int bits, int64_t ntiles) {
+    __shared__ int32_t cnt[1 << kSortMaxBits];
+    const int bins = 1 << bits;
+    for (int d = threadIdx.x; d < bins; d += 256) cnt[d] = 0;
+    __syncthreads();
+    const int64_t t0 = (int64_t)blockIdx.x * kSortTile;
+    for (int i = threadIdx.x; i < kSortTile; i += 256) {
+        const int64_t p = t0 + i;
+        if (p < n) {
+            const uint32_t k = ids ? (uint32_t)ids[p] : keys[p];
+            atomicAdd(&cnt[(k >> shift) & (uint32_t)(bins - 1)], 1);
+        }
+    }
+    __syncthreads();
+    for (int d = threadIdx.x; d < bins; d += 256) hist[(int64_t)d * ntiles + blockIdx.x] = cnt[d];
+}
+
+// Exclusive scan of total int32 values in place by one 1024-thread
+// workgroup: thread t owns a contiguous run, the runs' sums are scanned in
+// LDS, then each run is rewritten from its offset.
+__global__ __launch_bounds__(1024) void sort_scan_k(int32_t* v, int64_t total) {
+    __shared__ int32_t part[1024];
+    const int t = threadIdx.x;
+    const int64_t per = (total + 1023) / 1024;
+    const int64_t a = (int64_t)t * per, b = a + per < total ? a + per : total;
+    int32_t s = 0;
+    for (int64_t i = a; i < b; ++i) s += v[i];
+    part[t] = s;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {  // inclusive Hillis-Steele scan of the run sums
+        const int32_t x = t >= o ? part[t - o] : 0;
+        __syncthreads();
+        part[t] += x;
+        __syncthreads();
+    }
+    int32_t run = part[t] - s;
+    for (int64_t i = a; i < b; ++i) {
+        const int32_t c = v[i];
+        v[i] = run;
+        run += c;
+    }
+}
+
+__global__ __launch_bounds__(64) void sort_scatter_k(uint32_t* keys_out, int32_t* vals_out, const int64_t* ids,
+                                                     const uint32_t* keys_in, const int32_t* vals_in,
+                                                     const int32_t* hist, int64_t n, int shift, int bits,
+                                                     int64_t ntiles) {
+    __shared__ int32_t base[1 << kSortMaxBits];
+    const int lane = threadIdx.x;
+    const int bins = 1 << bits;
+    for (int d = lane; d < bins; d += 64) base[d] = hist[(int64_t)d * ntiles + blockIdx.x];
+    __syncthreads();
+    const int64_t t0 = (int64_t)blockIdx.x * kSortTile;
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    for (int r = 0; r < kSortTile && t0 + r < n; r += 64) {  // wave-uniform bounds
+        const int64_t p = t0 + r + lane;
+        const bool valid = p < n;
+        uint32_t k = 0;
+        int32_t v = 0;
+        if (valid) {
+            k = ids ? (uint32_t)ids[p] : keys_in[p];
+            v = ids ? (int32_t)p : vals_in[p];
+        }
+        const uint32_t d = (k >> shift) & (uint32_t)(bins - 1);
+        uint64_t peers = __ballot(valid);
+        for (int bit = 0; bit < bits; ++bit) {
+            const bool on = (d >> bit) & 1u;
+            const uint64_t bal = __ballot(on);
+            peers &= on ? bal : ~bal;
+        }
+        // peers: the valid lanes holding digit d (this lane included when valid)
+        const int leader = valid ? __ffsll((unsigned long long)peers) - 1 : lane;
+        int32_t b0 = (valid && lane == leader) ? base[d] : 0;
+        b0 = __shfl(b0, leader, 64);
+        if (valid) {
+            const int32_t pos = b0 + __popcll(peers & below);
+            keys_out[pos] = k;
+            vals_out[pos] = v;
+            if (lane == leader) base[d] = b0 + __popcll(peers);
+        }
+        __syncthreads();  // the next round's leaders read the advanced offsets
     }
 }
 
@@ -593,7 +686,7 @@ int32_t ve_gate_bwd(hipStream_t st, bf16* gx, float* gw, const float* ggate, con
 static int32_t ws_sum(ar_stream_t stream, float* out, const float* a, const float* b, int64_t n, int mi, int mo,
                       int64_t idx) {
     int32_t st;
-    float* partial = (float*)workspace(kSumBlocks * sizeof(float), &st);
+    float* partial = (float*)workspace(S(stream), kSumBlocks * sizeof(float), &st);
     if (!partial) return st;
     return ar::fixed_sum(S(stream), out, a, b, n, mi, mo, idx, partial);
 }
@@ -613,7 +706,7 @@ extern "C" int32_t ar_normalize_frobenius(ar_stream_t stream, float* data, int64
     AR_CHECK_ARG(data && size >= 0, "normalize_frobenius: bad argument");
     if (size == 0) return AR_OK;
     int32_t st;
-    float* ws = (float*)workspace((kSumBlocks + 64) * sizeof(float), &st);
+    float* ws = (float*)workspace(S(stream), (kSumBlocks + 64) * sizeof(float), &st);
     if (!ws) return st;
     return ar::frob_normalize(S(stream), data, size, ws);
 }
@@ -677,7 +770,7 @@ extern "C" int32_t ar_ve_gate_bwd(ar_stream_t stream, float* grad_x_norm_out, fl
     if (num_tokens == 0) return AR_OK;
     int32_t st;
     const int64_t n = n_kv_head * gate_channels;
-    float* partial = (float*)workspace((size_t)kGateBlocks * n * sizeof(float), &st);
+    float* partial = (float*)workspace(S(stream), (size_t)kGateBlocks * n * sizeof(float), &st);
     if (!partial) return st;
     return ar::ve_gate_bwd(S(stream), grad_x_norm_out, grad_gate_weight, grad_gate, gate, x_norm, gate_weight,
                            num_tokens, n_kv_head, gate_channels, embd_dim, embd_dim, partial);
@@ -706,28 +799,52 @@ extern "C" int32_t ar_embedding_bwd_sorted(ar_stream_t stream, float* grad_weigh
     return AR_LAUNCH_CHECK("embedding_bwd");
 }
 
-// Stable sort of token ids: sorted_ids/sorted_tokens (n each).  end_bit bounds
-// the radix passes (32 when the vocabulary size is unknown).
+// Stable sort of token ids: sorted_ids/sorted_tokens (n each), ids taken
+// as their low end_bit bits (32 when the vocabulary size is unknown).  The
+// passes ping-pong between the outputs and a scratch pair, ordered so that
+// the last pass writes the outputs.
+static void sort_plan(int32_t end_bit, int& npass, int& bits) {
+    if (end_bit < 1) end_bit = 1;
+    npass = (end_bit + kSortMaxBits - 1) / kSortMaxBits;
+    bits = (end_bit + npass - 1) / npass;
+}
+
 extern "C" int32_t ar_embedding_sort(ar_stream_t stream, uint32_t* sorted_ids, int32_t* sorted_tokens,
                                      const int64_t* indices, int64_t num_tokens, int32_t end_bit, void* scratch,
                                      size_t scratch_bytes, size_t* scratch_needed) {
     const int64_t n = num_tokens;
-    size_t cub_bytes = 0;
-    hipcub::DeviceRadixSort::SortPairs(nullptr, cub_bytes, (const uint32_t*)nullptr, (uint32_t*)nullptr,
-                                       (const int32_t*)nullptr, (int32_t*)nullptr, (int)n, 0, end_bit, S(stream));
+    AR_CHECK_ARG(n >= 0 && n < ((int64_t)1 << 31) && end_bit >= 1 && end_bit <= 32, "embedding_sort: bad arguments");
+    int npass, bits;
+    sort_plan(end_bit, npass, bits);
+    const int64_t ntiles = cdiv(n, kSortTile) > 0 ? cdiv(n, kSortTile) : 1;
     const size_t keys_bytes = ((size_t)n * 4 + 255) & ~size_t(255);
-    const size_t need = 2 * keys_bytes + cub_bytes;
+    const size_t hist_bytes = ((size_t)(1 << bits) * ntiles * 4 + 255) & ~size_t(255);
+    const size_t need = 2 * keys_bytes + hist_bytes;
     if (scratch_needed) *scratch_needed = need;
     if (!scratch) return AR_OK;
     if (scratch_bytes < need) return set_error(AR_EINVAL, "embedding_sort: scratch too small");
+    AR_CHECK_ARG(sorted_ids && sorted_tokens && indices, "embedding_sort: null pointer");
+    if (n == 0) return AR_OK;
     char* base = (char*)scratch;
-    uint32_t* keys = (uint32_t*)base;
-    int32_t* vals = (int32_t*)(base + keys_bytes);
-    void* cub_tmp = base + 2 * keys_bytes;
-    emb_keys_k<<<flat_grid(n, kBlock), kBlock, 0, S(stream)>>>(keys, vals, indices, n);
-    if (hipcub::DeviceRadixSort::SortPairs(cub_tmp, cub_bytes, keys, sorted_ids, vals, sorted_tokens, (int)n, 0,
-                                           end_bit, S(stream)) != hipSuccess)
-        return set_error(AR_EHIP, "embedding_sort: radix sort failed");
+    uint32_t* tk = (uint32_t*)base;
+    int32_t* tv = (int32_t*)(base + keys_bytes);
+    int32_t* hist = (int32_t*)(base + 2 * keys_bytes);
+    const hipStream_t st = S(stream);
+    const uint32_t* kin = nullptr;
+    const int32_t* vin = nullptr;
+    for (int p = 0; p < npass; ++p) {
+        const int shift = p * bits;
+        const int pb = end_bit - shift < bits ? end_bit - shift : bits;
+        const bool to_out = ((npass - 1 - p) % 2) == 0;
+        uint32_t* kout = to_out ? sorted_ids : tk;
+        int32_t* vout = to_out ? sorted_tokens : tv;
+        const int64_t* ids = p == 0 ? indices : nullptr;
+        sort_hist_k<<<(unsigned)ntiles, 256, 0, st>>>(hist, ids, kin, n, shift, pb, ntiles);
+        sort_scan_k<<<1, 1024, 0, st>>>(hist, (int64_t)(1 << pb) * ntiles);
+        sort_scatter_k<<<(unsigned)ntiles, 64, 0, st>>>(kout, vout, ids, kin, vin, hist, n, shift, pb, ntiles);
+        kin = kout;
+        vin = vout;
+    }
     return AR_LAUNCH_CHECK("embedding_sort");
 }
 
@@ -741,7 +858,7 @@ extern "C" int32_t ar_embedding_bwd(ar_stream_t stream, float* grad_weight, cons
     if (st) return st;
     const size_t ids_bytes = ((size_t)num_tokens * 4 + 255) & ~size_t(255);
     const size_t part_bytes = (size_t)num_tokens * embd_dim * sizeof(float);
-    char* ws = (char*)workspace(2 * ids_bytes + sort_bytes + part_bytes, &st);
+    char* ws = (char*)workspace(S(stream), 2 * ids_bytes + sort_bytes + part_bytes, &st);
     if (!ws) return st;
     uint32_t* sids = (uint32_t*)ws;
     int32_t* stok = (int32_t*)(ws + ids_bytes);

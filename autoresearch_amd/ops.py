@@ -13,7 +13,7 @@ import torch
 from ._lib import check, load
 
 __all__ = [
-    "embedding_fwd", "rmsnorm_fwd", "linear_fwd", "rope_fwd", "flash_attn_fwd",
+    "Workspace", "embedding_fwd", "rmsnorm_fwd", "linear_fwd", "rope_fwd", "flash_attn_fwd",
     "flash_attn_bwd_precompute_d", "flash_attn_bwd_dq", "flash_attn_bwd_dkv", "relu_squared_fwd",
     "softcap_fwd", "ve_gate_fwd", "ve_apply_fwd", "add_residual_fwd", "scaled_add_fwd", "softmax_fwd",
     "cross_entropy_fwd", "mean_reduce", "cross_entropy_softcap_bwd", "linear_bwd_dx", "linear_bwd_dw",
@@ -27,6 +27,43 @@ __all__ = [
 
 def _stream():
     return torch.cuda.current_stream().cuda_stream
+
+
+class Workspace:
+    """Device scratch for the entry points that need some (ar_workspace_*).
+
+    Created once by the host (it is the one allocation), then bound to the
+    streams whose per-op calls should use it.  Calls on a stream with no
+    workspace bound, or one too small, raise ``ArError`` naming the bytes
+    they need; no call allocates behind the caller's back."""
+
+    def __init__(self, nbytes: int):
+        import ctypes as ct
+        self._lib = load()
+        h = ct.c_void_p()
+        check(self._lib.ar_workspace_create(ct.byref(h), int(nbytes)), "workspace_create")
+        self.h = h
+
+    @property
+    def nbytes(self) -> int:
+        return int(self._lib.ar_workspace_bytes(self.h))
+
+    def bind(self, stream=None):
+        """Bind to `stream` (a torch stream, a raw handle, or None = torch's current stream)."""
+        s = _stream() if stream is None else getattr(stream, "cuda_stream", stream)
+        check(self._lib.ar_workspace_bind(s, self.h), "workspace_bind")
+        return self
+
+    def close(self):
+        if getattr(self, "h", None):
+            check(self._lib.ar_workspace_destroy(self.h), "workspace_destroy")
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def _p(t: torch.Tensor | None):

@@ -25,14 +25,22 @@
  *     writing dX.
  *   - `_bf16` variants take the same fp32 buffers and compute on the bf16
  *     matrix cores (operands rounded to bf16, fp32 accumulation, fp32 out).
- *   - Thread safety: entry points may be called from several host threads;
- *     the library-owned workspace (split-K partials, alias copies, Muon
- *     temporaries) is shared, so calls that use it must be serialised on one
- *     stream, as the reference's single in-order DeviceContext does.
+ *   - No entry point allocates, frees or synchronises device memory.  The
+ *     ones that need scratch (split-K partials, the in-place linear_bwd_dx
+ *     copy, the embedding scatter's sort and chunk sums, reduction partials,
+ *     Muon temporaries, the bf16 operand copies of the attention _bf16
+ *     variants) take it from the workspace the caller bound to `stream`
+ *     (ar_workspace_*, below); with none bound, or one too small, they return
+ *     AR_ENOMEM and ar_last_error() names the bytes needed.
+ *   - Thread safety: entry points may be called from several host threads.
+ *     Calls that share a workspace must not overlap in time (bind one
+ *     workspace per stream, and keep each stream's calls in order, as the
+ *     reference's single in-order DeviceContext does).
  */
 #ifndef AR_OPS_H
 #define AR_OPS_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -53,6 +61,23 @@ enum ar_precision { AR_PREC_FP32 = 0, AR_PREC_BF16 = 1 };
 
 const char* ar_last_error(void);
 int32_t ar_version(void);
+
+/* ---------------- workspaces ----------------
+ * Device scratch created by the caller, the counterpart of the DeviceBuffers
+ * the reference's host code allocates for its kernels (model.mojo:263-335,
+ * optimizer.mojo:86-101, 242-253): the library's entry points choose their own
+ * launch geometry and scratch layout, so the scratch is one caller-owned
+ * buffer instead of per-kernel buffers. */
+typedef struct ar_workspace ar_workspace;
+/* hipMalloc of `bytes` on the current device (the only allocation the per-op
+ * entry points depend on).  Create it before a stream capture, not during. */
+int32_t ar_workspace_create(ar_workspace** out, size_t bytes);
+/* Per-op calls on `stream` (on the current device) use `ws` from now on; NULL
+ * unbinds.  One workspace may serve several streams whose calls never overlap. */
+int32_t ar_workspace_bind(ar_stream_t stream, ar_workspace* ws);
+/* Unbinds it everywhere, waits for the streams it was bound to, frees it. */
+int32_t ar_workspace_destroy(ar_workspace* ws);
+size_t ar_workspace_bytes(const ar_workspace* ws);
 
 /* ---------------- kernels/ops.mojo ---------------- */
 
@@ -149,6 +174,22 @@ int32_t ar_linear_bwd_dw_bf16(ar_stream_t stream, float* grad_weight, const floa
  * cores with fp32 accumulation.  accumulate: C += result. */
 int32_t ar_gemm_mixed(ar_stream_t stream, int32_t layout, void* C, int32_t c_bf16, const void* X, int32_t x_bf16,
                       const void* W, int32_t w_bf16, int64_t M, int64_t N, int64_t K, int32_t accumulate);
+/* The bf16 step's fused LM-head loss.  The reference runs it as five
+ * launches: linear_fwd (ops.mojo:110-203) of the final normed x by lm_head,
+ * softcap_fwd (ops.mojo:500-510), cross_entropy_fwd (ops.mojo:672-740) in the
+ * forward (model.mojo:745-764) and cross_entropy_softcap_bwd (ops.mojo:
+ * 778-864) in the backward (model.mojo:845-850).  Here: one GEMM whose
+ * epilogue applies cap * tanh(z / cap) and stores the logits as bf16, then one
+ * pass per row that writes the per-token loss (lse - logit[target]; 0 for a
+ * target outside [0, vocab_size)) and grad_logits = (softmax - onehot) *
+ * loss_scale as bf16 (no softcap derivative, as the reference).
+ * input: bf16 [num_tokens, embd_dim]; weight: bf16 [vocab_size, embd_dim];
+ * logits, grad_logits: bf16 [num_tokens, vocab_size]; loss_out: fp32
+ * [num_tokens] (may be NULL).  Sizes multiples of 8, pointers 16-byte aligned. */
+int32_t ar_lm_head_softcap_ce_bf16(ar_stream_t stream, float* loss_out, void* grad_logits, void* logits,
+                                   const void* input, const void* weight, const int64_t* targets,
+                                   int64_t num_tokens, int64_t vocab_size, int64_t embd_dim, float cap,
+                                   float loss_scale);
 /* ops.mojo:1039-1085  dx = (dy - x <dy,x> / (dim rms^2)) / rms; grad_input may alias grad_output */
 int32_t ar_rmsnorm_bwd(ar_stream_t stream, float* grad_input, const float* grad_output, const float* input,
                        const float* rms_saved, int64_t num_rows, int64_t dim);
@@ -274,8 +315,8 @@ int32_t ar_gpt_train_step(ar_gpt* model, const int64_t* inputs, const int64_t* t
  * whole step" of the training driver; no counterpart in the reference, whose
  * step is ~1,700 separate launches).  Same results as ar_gpt_train_step,
  * bit for bit.  The graph records inputs / targets: pass the same device
- * buffers every call (new pointers re-record it).  The token-id sort of the
- * embedding backward runs eagerly before each replay.  The model's stream
+ * buffers every call (new pointers re-record it); the token-id sort of the
+ * embedding backward is part of the graph.  The model's stream
  * must not be the null stream, and profiling (ar_gpt_profile) must be off.
  * loss_host as in ar_gpt_train_step. */
 int32_t ar_gpt_train_step_graph(ar_gpt* model, const int64_t* inputs, const int64_t* targets, double progress,

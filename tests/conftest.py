@@ -21,6 +21,20 @@ def has_gpu() -> bool:
         return False
 
 
+@pytest.fixture(scope="session", autouse=True)
+def per_op_workspace():
+    """The host-created scratch the per-op entry points draw from (the
+    reference's host owns its kernels' buffers the same way), bound to the
+    default stream the per-op tests launch on."""
+    if not has_gpu():
+        yield None
+        return
+    from autoresearch_amd import ops
+    ws = ops.Workspace(3 << 30).bind()
+    yield ws
+    ws.close()
+
+
 def pytest_collection_modifyitems(config, items):
     if has_gpu():
         return

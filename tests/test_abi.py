@@ -51,7 +51,7 @@ def test_every_reference_kernel_has_an_entry_point():
 
 def test_load_sets_signatures():
     lib = _lib.load()
-    assert lib.ar_version() == 1
+    assert lib.ar_version() == 2  # 2: caller-created workspaces (ar_workspace_*)
     assert lib.ar_gpt_create.restype is ct.c_int32
     assert lib.ar_gpt_params.restype is ct.c_void_p
 
@@ -64,6 +64,10 @@ def test_error_path_without_gpu():
     assert b"null" in lib.ar_last_error()
     st = lib.ar_flash_attn_fwd(None, 16, 16, 16, 16, 16, 1, 8, 1, 256, 0)
     assert st in (-1, -2)
+    st = lib.ar_workspace_create(None, 1 << 20)
+    assert st == -1 and b"null" in lib.ar_last_error()
+    assert lib.ar_workspace_bytes(None) == 0
+    assert lib.ar_workspace_destroy(None) == 0
 
 
 def test_gpt_config_default():

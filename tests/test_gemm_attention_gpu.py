@@ -50,6 +50,47 @@ def test_gemm_layouts_vs_oracle(env, M, N, K, bf16):
     assert rel_err(gu.host(dw), ref) <= tol
 
 
+@pytest.mark.parametrize("M,N,K", [(13, 24, 40), (1, 1, 1), (37, 129, 3), (300, 77, 515)])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_gemm_any_shape_vs_oracle(env, M, N, K, bf16):
+    """Any M, N, K (and operands only 4-byte aligned): the tail path pads into
+    the workspace, as the reference's tiles bound-check every element
+    (ops.mojo:150-168); dX in place (model.mojo:906) included."""
+    ops, orc, gu = env
+    import torch
+    r = gu.rng(M * 7 + N * 3 + K)
+    tol = TOL_BF16 if bf16 else TOL_FP32
+    X, W, dY = gu.randn(r, M, K), gu.randn(r, N, K, scale=0.05), gu.randn(r, M, N)
+
+    def unaligned(a):
+        # a view starting 4 bytes into a fresh buffer: not 16-byte aligned
+        buf = torch.empty(a.size + 1, dtype=torch.float32, device="cuda")
+        v = buf[1:]
+        v.copy_(torch.from_numpy(a.ravel()).cuda())
+        return v
+
+    ref = np.zeros((M, N), np.float32)
+    orc.call("linear_fwd", ref, X, W, M, N, K)
+    out = unaligned(np.full((M, N), np.nan, np.float32))
+    ops.linear_fwd(out, unaligned(X), gu.dev(W), M, N, K, bf16=bf16)
+    assert rel_err(gu.host(out).reshape(M, N), ref) <= tol
+    ref = np.zeros((M, K), np.float32)
+    orc.call("linear_bwd_dx", ref, dY, W, M, N, K)
+    dx = gu.empty(M, K)
+    ops.linear_bwd_dx(dx, gu.dev(dY), unaligned(W), M, N, K, bf16=bf16)
+    assert rel_err(gu.host(dx), ref) <= tol
+    if N == K:
+        buf = gu.dev(dY)
+        ops.linear_bwd_dx(buf, buf, gu.dev(W), M, N, K, bf16=bf16)
+        assert rel_err(gu.host(buf), ref) <= tol
+    dw0 = gu.randn(r, N, K)
+    ref = dw0.copy()
+    orc.call("linear_bwd_dw", ref, dY, X, M, N, K)
+    dw = unaligned(dw0)
+    ops.linear_bwd_dw(dw, gu.dev(dY), gu.dev(X), M, N, K, bf16=bf16)
+    assert rel_err(gu.host(dw).reshape(N, K), ref) <= tol
+
+
 def test_linear_bwd_dx_in_place(env):
     """model.mojo:906 calls linear_bwd_dx with grad_input == grad_output."""
     ops, orc, gu = env
@@ -135,6 +176,82 @@ def test_gemm_bf16_storage_persistent(env, layout, M, N, K):
     check(L.ar_gemm_mixed(s0, layout, C2.data_ptr(), 0, X.data_ptr(), 1, W.data_ptr(), 1, M, N, K, 1))
     torch.cuda.synchronize()
     assert torch.equal(C, C2)
+
+
+# The dW shapes of BASELINE configs 4 and 5 at their real token counts:
+# (M, N, K) of linear_bwd_dw for the fused q|k|v, c_proj, c_fc, mlp_proj and
+# lm_head products.  The persistent kernel's reduction split count depends on
+# all three, so these are exactly the split counts the benchmark runs.
+DW_SHAPES = [(65536, 1536, 512), (65536, 512, 512), (65536, 2048, 512), (65536, 512, 2048), (65536, 8192, 512),
+             (131072, 2304, 768), (131072, 768, 768), (131072, 3072, 768), (131072, 768, 3072),
+             (131072, 8192, 768)]
+
+
+@pytest.mark.parametrize("M,N,K", DW_SHAPES)
+def test_dw_benchmark_shapes(env, M, N, K):
+    """linear_bwd_dw (accumulate) with bf16 operands at the benchmark's shapes
+    against torch fp64 of the same bf16 values: products of bf16 values are
+    exact in fp32, so the bound is the fp32 accumulation order's (1e-5)."""
+    ops, orc, gu = env
+    import torch
+    from autoresearch_amd._lib import check, load
+    L = load()
+    g = torch.Generator(device="cuda").manual_seed(M + N + K)
+    s0 = torch.cuda.current_stream().cuda_stream
+    dY = torch.randn(M, N, device="cuda", generator=g).bfloat16()
+    X = torch.randn(M, K, device="cuda", generator=g).bfloat16()
+    C0 = torch.randn(N, K, device="cuda", generator=g)
+    C = C0.clone()
+    check(L.ar_gemm_mixed(s0, 2, C.data_ptr(), 0, dY.data_ptr(), 1, X.data_ptr(), 1, M, N, K, 1))
+    ref = C0.double() + dY.double().T @ X.double()
+    assert rel_err(gu.host(C), gu.host(ref)) <= 1e-5
+    del dY, X, ref
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("M", [32768, 200])
+def test_lm_head_softcap_ce_config3(env, M):
+    """BASELINE config 3's fused LM head: x [M, 512] ~ N(0, 1), lm_head
+    [8192, 512] ~ N(0, 0.02^2) as bf16, softcap 15, cross-entropy against
+    uniform targets (a few ignored), through ar_lm_head_softcap_ce_bf16 (the
+    bf16 step's two launches).  Reference: torch fp64 on the same bf16
+    values.  The logits, the loss and the gradient are each one bf16 rounding
+    (2^-9 relative) away from it: bounds 4e-3 (logits, gradient, norm-wise)
+    and 2e-3 relative on each token's loss, inside the north-star 2e-2."""
+    ops, orc, gu = env
+    import torch
+    from autoresearch_amd._lib import check, load
+    L = load()
+    V, C, cap, scale = 8192, 512, 15.0, 0.5
+    g = torch.Generator(device="cuda").manual_seed(M)
+    s0 = torch.cuda.current_stream().cuda_stream
+    x = torch.randn(M, C, device="cuda", generator=g).bfloat16()
+    w = (torch.randn(V, C, device="cuda", generator=g) * 0.02).bfloat16()
+    tg = torch.randint(0, V, (M,), device="cuda", generator=g)
+    tg[::97] = -1  # ignored rows
+    loss = torch.full((M,), float("nan"), device="cuda")
+    logits = torch.empty(M, V, device="cuda", dtype=torch.bfloat16)
+    grad = torch.empty(M, V, device="cuda", dtype=torch.bfloat16)
+    check(L.ar_lm_head_softcap_ce_bf16(s0, loss.data_ptr(), grad.data_ptr(), logits.data_ptr(), x.data_ptr(),
+                                       w.data_ptr(), tg.data_ptr(), M, V, C, cap, scale))
+    torch.cuda.synchronize()
+    z = x.double() @ w.double().T
+    zc = cap * torch.tanh(z / cap)
+    live = tg >= 0
+    t = tg.clamp(min=0)
+    ref_loss = torch.where(live, torch.logsumexp(zc, -1) - zc.gather(1, t[:, None])[:, 0], torch.zeros_like(zc[:, 0]))
+    p = torch.softmax(zc, -1)
+    p[torch.arange(M, device="cuda"), t] -= 1.0
+    ref_grad = torch.where(live[:, None], p * scale, torch.zeros_like(p))
+    assert rel_err(gu.host(logits.float()), gu.host(zc)) <= 4e-3
+    lg, lr_ = gu.host(loss).astype(np.float64), gu.host(ref_loss)
+    assert np.all(np.abs(lg - lr_) <= 2e-3 * np.abs(lr_)), np.abs(lg - lr_).max()
+    assert np.all(lg[::97] == 0.0)
+    assert rel_err(gu.host(grad.float()), gu.host(ref_grad)) <= 4e-3
+    assert torch.all(grad[::97] == 0)
+    # the per-row gradient sums to 0 (softmax sums to 1) up to the bf16 rounding
+    rs = grad.float().sum(-1)
+    assert float(rs.abs().max()) <= 4e-3 * scale  # the -1 entry alone rounds by up to 2^-10
 
 
 def _attn_inputs(gu, r, B, T, H, hd):

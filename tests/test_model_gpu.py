@@ -24,9 +24,25 @@ WIDE = dict(sequence_len=256, vocab_size=1024, n_layer=4, n_head=2, n_kv_head=2,
             kv_dim=256)
 
 
+# BASELINE configs 4 and 5: GPTConfig.default(8192, depth) (config.mojo:27-43)
+CONFIG4 = dict(sequence_len=2048, vocab_size=8192, n_layer=8, n_head=4, n_kv_head=4, n_embd=512, head_dim=128,
+               kv_dim=512)
+CONFIG5 = dict(sequence_len=2048, vocab_size=8192, n_layer=12, n_head=6, n_kv_head=6, n_embd=768, head_dim=128,
+               kv_dim=768)
+
+
 def _tokens(seed, B, T, V):
     r = np.random.default_rng(seed)
     stream = r.integers(0, V, (B, T + 1)).astype(np.int64)
+    return np.ascontiguousarray(stream[:, :-1]).ravel(), np.ascontiguousarray(stream[:, 1:]).ravel()
+
+
+def _zipf_tokens(seed, B, T, V, s=1.1):
+    """BASELINE configs 4 / 5: p_k ~ (k+1)^-s, k < V, by inverse CDF."""
+    p = 1.0 / np.arange(1, V + 1, dtype=np.float64) ** s
+    cdf = np.cumsum(p / p.sum())
+    u = np.random.default_rng(seed).random(B * (T + 1))
+    stream = np.minimum(np.searchsorted(cdf, u, side="right"), V - 1).astype(np.int64).reshape(B, T + 1)
     return np.ascontiguousarray(stream[:, :-1]).ravel(), np.ascontiguousarray(stream[:, 1:]).ravel()
 
 
@@ -41,7 +57,7 @@ def _copy_into(dst_flat, dst_tensors, src_flat, src_tensors):
         dst_flat[o:o + s] = src_flat[so:so + ss]
 
 
-def _run(cfg, B, T, precision, rope_period, seed0, steps, tok_seed=0):
+def _run(cfg, B, T, precision, rope_period, seed0, steps, tok_seed=0, tokens=_tokens):
     """Each stage is compared on identical inputs: forward/backward from the
     same weights, then the optimizer from the same gradients (the GPU's are
     copied into the oracle), then weights are re-synchronised.  AdamW's first
@@ -63,7 +79,7 @@ def _run(cfg, B, T, precision, rope_period, seed0, steps, tok_seed=0):
     for step in range(steps):
         # forward / backward start from identical weights
         _copy_into(om.params(), ot, gu.host(gm.params()), gt)
-        x, y = _tokens(tok_seed + step, B, T, cfg["vocab_size"])
+        x, y = tokens(tok_seed + step, B, T, cfg["vocab_size"])
         xd, yd = gu.dev(x), gu.dev(y)
         om.zero_grads()
         lo = om.forward(x, y)
@@ -81,7 +97,8 @@ def _run(cfg, B, T, precision, rope_period, seed0, steps, tok_seed=0):
         om.optimizer_step(0.0)
         gm.optimizer_step(0.0)
         po, pg = _by_name(om.params().copy(), ot), _by_name(gu.host(gm.params()), gt)
-        results.append(dict(loss=(lo, lg), tok=(tl_o, tl_g), grads=(go, gg), params=(po, pg), l1=l1, pre=pre))
+        results.append(dict(loss=(lo, lg), tok=(tl_o, tl_g), grads=(go, gg), params=(po, pg), l1=l1, pre=pre,
+                            shape=cfg))
     gm.close()
     return init_o, init_g, results
 
@@ -116,9 +133,34 @@ def _check(init_o, init_g, results, tol, grad_tol, upd_tol):
         po, pg = r["params"]
         for n in po:
             w_old = r["pre"][n].astype(np.float64)
+            diff = pg[n].astype(np.float64) - po[n]
+            dec = _cautious_decay(n, w_old, r["shape"])
+            if dec is not None:
+                # Muon's cautious update decays p only where X p >= 0
+                # (optimizer.mojo:197-210).  Where X is within rounding of 0
+                # two implementations may take different branches; such an
+                # entry differs by exactly the decay lr wd |p|.  Those are set
+                # aside and the rest meet the bound.  |X| is within the
+                # update's relative noise upd_tol of 0 on about 0.8 upd_tol of
+                # the entries (X is roughly Gaussian), hence the cap 2 upd_tol.
+                flip = (dec > 0) & (np.abs(np.abs(diff) - dec) <= 0.05 * dec)
+                assert flip.sum() <= 2 * upd_tol * diff.size, (s, n, int(flip.sum()))
+                diff = np.where(flip, 0.0, diff)
             bound = tol * np.linalg.norm(po[n]) + upd_tol * np.linalg.norm(po[n] - w_old)
-            d = np.linalg.norm(pg[n].astype(np.float64) - po[n])
+            d = np.linalg.norm(diff)
             assert d <= bound, (s, n, d, bound)
+
+
+def _cautious_decay(name, w_old, shape):
+    """lr wd |p| of the Muon matrices at progress 0 (lr multiplier 1, weight
+    decay 0.2, lr 0.04 sqrt(max(1, rows / cols)): train.mojo:272,
+    optimizer.mojo:265-267); None for the AdamW tensors."""
+    part = name.split(".")[-1]
+    aspect = {"c_q": 1.0, "c_k": 1.0, "c_v": 1.0, "c_proj": 1.0, "c_fc": 4.0, "mlp_proj": 0.25}.get(part)
+    if aspect is None or not name.startswith("h"):
+        return None
+    lr = np.float32(0.04 * np.sqrt(max(1.0, aspect)))
+    return float(lr) * float(np.float32(0.2)) * np.abs(w_old)
 
 
 @pytest.mark.parametrize("seed0", [0, 42])
@@ -139,6 +181,62 @@ def test_wide_model(precision):
         _check(init_o, init_g, res, TOL_FP32, GRAD_FP32, UPD_FP32)
     else:
         _check(init_o, init_g, res, TOL_BF16, TOL_BF16, UPD_BF16)
+
+
+@pytest.mark.parametrize("precision", [0, 1])
+def test_config4_dims_two_steps(precision):
+    """BASELINE config 4 at its real dimensions (depth 8, d512, 4 x 128 heads,
+    V 8192, T 2048, windows 1024 x 3 + 2048, Zipf(1.1) tokens) with B = 1, so
+    the oracle finishes in seconds: loss, per-token loss, every gradient and
+    the post-step weights over two steps.  This runs the kernel instances the
+    benchmark runs at C = 512 (two-chunk row kernels, the V = 8192 loss rows,
+    the attention at hd 128 with both window sizes)."""
+    init_o, init_g, res = _run(CONFIG4, 1, 2048, precision, 2048, 42, steps=2, tokens=_zipf_tokens)
+    if precision == 0:
+        _check(init_o, init_g, res, TOL_FP32, GRAD_FP32, UPD_FP32)
+    else:
+        _check(init_o, init_g, res, TOL_BF16, TOL_BF16, UPD_BF16)
+
+
+@pytest.mark.parametrize("precision", [0, 1])
+def test_config5_dims_two_steps(precision):
+    """BASELINE config 5 at its real dimensions (depth 12, d768, 6 heads) with
+    B = 1: C = 768 is not a multiple of 256, so the row kernels run their
+    partial last chunk."""
+    init_o, init_g, res = _run(CONFIG5, 1, 2048, precision, 2048, 42, steps=2, tokens=_zipf_tokens)
+    if precision == 0:
+        _check(init_o, init_g, res, TOL_FP32, GRAD_FP32, UPD_FP32)
+    else:
+        _check(init_o, init_g, res, TOL_BF16, TOL_BF16, UPD_BF16)
+
+
+@pytest.mark.parametrize("cfg,B", [(CONFIG4, 32), (CONFIG5, 64)], ids=["config4", "config5"])
+def test_full_size_step_properties(cfg, B):
+    """The benchmarked workloads at full size (bf16, B = 32 / 64, T 2048),
+    where the oracle would take minutes, through size-independent properties:
+    the first loss is ln V to within 0.01 (lm_head ~ N(0, 0.001) makes the
+    logits nearly uniform, test_forward.mojo:114-120), the step is bit-identical
+    on a fresh model, and the loss stays finite and falls over five steps on a
+    fixed batch (test_training.mojo:148-158)."""
+    import gpu_util as gu
+    from autoresearch_amd.model import GPT, GPTConfig
+    T, V = cfg["sequence_len"], cfg["vocab_size"]
+    x, y = _zipf_tokens(0, B, T, V)
+    xd, yd = gu.dev(x), gu.dev(y)
+    runs = []
+    for _ in range(2):
+        gm = GPT(GPTConfig(**cfg), B, T, precision=1, rope_period=T)
+        gm.init_weights(42)
+        losses = [gm.train_step(xd, yd, 0.0) for _ in range(5)]
+        p = gu.host(gm.params())
+        runs.append((losses, p[:1 << 22].copy(), float(np.abs(p).sum())))
+        gm.close()
+    losses = runs[0][0]
+    assert abs(losses[0] - np.log(V)) < 0.01, losses
+    assert all(np.isfinite(losses)) and losses[-1] < losses[0] - 0.1, losses
+    assert runs[0][0] == runs[1][0]
+    np.testing.assert_array_equal(runs[0][1], runs[1][1])
+    assert runs[0][2] == runs[1][2]
 
 
 def test_step_is_deterministic():

@@ -365,5 +365,130 @@ def test_errors(env):
     with pytest.raises(ArError):
         ops.flash_attn_fwd(q, torch.zeros(32, device="cuda"), q, q, q, 2, 16, 1, 256, 0)  # hd > 128 (ops.mojo:267)
     a = torch.zeros(24, device="cuda")
-    with pytest.raises(ArError):
-        ops.linear_fwd(a, a, a, 3, 4, 2)  # not a multiple of 8
+    with pytest.raises(ArError, match="overlaps"):
+        ops.linear_fwd(a, a, a, 3, 4, 2)  # the output aliases an input
+    with pytest.raises(ArError, match="negative"):
+        ops.linear_fwd(torch.zeros(24, device="cuda"), a, a, -3, 4, 2)
+
+
+def _sort_fn():
+    """ar_embedding_sort (the embedding scatter's stable token sort; declared
+    for the library's own callers, not in the public header)."""
+    import ctypes as ct
+    from autoresearch_amd._lib import load
+    fn = load().ar_embedding_sort
+    fn.restype = ct.c_int32
+    fn.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_int64, ct.c_int32, ct.c_void_p,
+                   ct.c_size_t, ct.POINTER(ct.c_size_t)]
+    return fn
+
+
+@pytest.mark.parametrize("n,end_bit,dist", [(1, 13, "u"), (63, 13, "u"), (64, 7, "u"), (2049, 13, "zipf"),
+                                            (65536, 13, "zipf"), (131072, 13, "zipf"), (100003, 32, "u"),
+                                            (4096, 32, "same")])
+def test_embedding_sort_stable(env, n, end_bit, dist):
+    """The hand-written counting sort: ids ascending, equal ids in token order
+    (exactly numpy's stable argsort), for one to three digit passes, partial
+    tiles and rounds, Zipf-hot ids, and all-equal ids."""
+    ops, orc, gu = env
+    import ctypes as ct
+    import torch
+    from autoresearch_amd._lib import check
+    r = gu.rng(n + end_bit)
+    hi = min(1 << end_bit, 1 << 31)
+    if dist == "zipf":
+        V = min(hi, 8192)
+        p = 1.0 / np.arange(1, V + 1) ** 1.1
+        idx = r.choice(V, size=n, p=p / p.sum()).astype(np.int64)
+    elif dist == "same":
+        idx = np.full(n, 77, np.int64)
+    else:
+        idx = r.integers(0, hi, n).astype(np.int64)
+    fn = _sort_fn()
+    need = ct.c_size_t()
+    check(fn(None, None, None, None, n, end_bit, None, 0, ct.byref(need)), "embedding_sort")
+    scratch = torch.empty(need.value, dtype=torch.uint8, device="cuda")
+    sid = torch.empty(n, dtype=torch.int32, device="cuda")
+    stok = torch.empty(n, dtype=torch.int32, device="cuda")
+    d_idx = gu.dev(idx)
+    s0 = torch.cuda.current_stream().cuda_stream
+    check(fn(s0, sid.data_ptr(), stok.data_ptr(), d_idx.data_ptr(), n, end_bit, scratch.data_ptr(), need.value, None),
+          "embedding_sort")
+    order = np.argsort(idx, kind="stable")
+    np.testing.assert_array_equal(gu.host(stok), order.astype(np.int32))
+    np.testing.assert_array_equal(gu.host(sid).view(np.uint32), idx[order].astype(np.uint32))
+
+
+def test_workspace_binding_errors(env):
+    """A per-op call that needs scratch fails (AR_ENOMEM, naming the bytes)
+    on a stream with no workspace or too small a one, and allocates nothing."""
+    ops, orc, gu = env
+    import torch
+    from autoresearch_amd._lib import ArError
+    M, N, K = 4096, 512, 512
+    dY, X = torch.randn(M, N, device="cuda"), torch.randn(M, K, device="cuda")
+    dw = torch.zeros(N, K, device="cuda")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with pytest.raises(ArError, match="no workspace bound"):
+            ops.linear_bwd_dw(dw, dY, X, M, N, K)
+        small = ops.Workspace(4096).bind()
+        with pytest.raises(ArError, match="needs"):
+            ops.linear_bwd_dw(dw, dY, X, M, N, K)
+        big = ops.Workspace(64 << 20).bind()  # rebinding replaces the small one
+        ops.linear_bwd_dw(dw, dY, X, M, N, K)
+        s.synchronize()
+        small.close()
+        big.close()
+        with pytest.raises(ArError, match="no workspace bound"):
+            ops.linear_bwd_dw(dw, dY, X, M, N, K)
+    ref = dY.double().T @ X.double()
+    assert rel_err(gu.host(dw), gu.host(ref)) <= TOL_FP32
+
+
+def test_per_op_calls_under_stream_capture(env):
+    """Per-op entry points that use scratch (split-K dW partials + reduce, the
+    embedding sort + chunk sums, a multi-block mean) record into a graph: no
+    allocation or synchronisation happens inside them.  The graph is replayed
+    five times with eager work in between, each replay checked bit for bit
+    against the eager result."""
+    ops, orc, gu = env
+    import torch
+    r = gu.rng(11)
+    M, N, K, V = 8192, 512, 512, 1000
+    dY, X = gu.dev(gu.randn(r, M, N)), gu.dev(gu.randn(r, M, K))
+    idx = gu.dev(r.integers(0, V, M).astype(np.int64))
+    dw0, gw0 = gu.dev(gu.randn(r, N, K)), gu.dev(gu.randn(r, V, N))
+    loss = gu.dev(gu.randn(r, M))
+    s = torch.cuda.Stream()
+    ws = ops.Workspace(256 << 20).bind(s)
+    dw, gw, mean = dw0.clone(), gw0.clone(), torch.zeros(1, device="cuda")
+
+    def body():
+        ops.linear_bwd_dw(dw, dY, X, M, N, K)
+        ops.embedding_bwd(gw, dY, idx, M, N)
+        ops.mean_reduce(mean, loss, M)
+
+    with torch.cuda.stream(s):
+        body()
+    s.synchronize()
+    want = (gu.host(dw).copy(), gu.host(gw).copy(), gu.host(mean).copy())
+    g = torch.cuda.CUDAGraph()
+    dw.copy_(dw0)
+    gw.copy_(gw0)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        body()
+    for rep in range(5):
+        dw.copy_(dw0)
+        gw.copy_(gw0)
+        mean.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(gu.host(dw), want[0], err_msg=f"replay {rep}")
+        np.testing.assert_array_equal(gu.host(gw), want[1], err_msg=f"replay {rep}")
+        np.testing.assert_array_equal(gu.host(mean), want[2], err_msg=f"replay {rep}")
+        _ = (dY * 2).sum()  # eager work between replays
+    del g
+    ws.close()
