@@ -35,6 +35,7 @@
 //     (deterministic; the reference's single-block loop over M is serial).
 #include "ar_internal.hpp"
 
+#include <mutex>
 #include <type_traits>
 
 using namespace ar;
@@ -1211,8 +1212,15 @@ static int32_t gemm_padded(hipStream_t st, int layout, bool bf, float* C, const 
     return copy2d(st, C, sh[2][1], cp, ph[2][1], sh[2][0], sh[2][1], sh[2][0], sh[2][1]);
 }
 
+// Where a linear_* call takes its scratch from: the workspace bound to its
+// stream, or (fixed != nullptr) a caller-supplied region of fixed_bytes.
+struct ScratchSrc {
+    char* fixed;
+    size_t fixed_bytes;
+};
+
 static int32_t linear_call(ar_stream_t s, int layout, bool bf, float* C, const float* X, const float* W, int64_t M,
-                           int64_t N, int64_t K, const char* nm) {
+                           int64_t N, int64_t K, const char* nm, ScratchSrc src_ws = ScratchSrc{nullptr, 0}) {
     int32_t st = check_gemm_args(C, X, W, M, N, K, nm);
     if (st) return st;
     int64_t sh[3][2];
@@ -1226,7 +1234,12 @@ static int32_t linear_call(ar_stream_t s, int layout, bool bf, float* C, const f
     if (red == 0) return layout == 2 ? AR_OK : ar_zero_buffer(s, C, sh[2][0] * sh[2][1]);
     const size_t need = gemm_ws_bytes(layout, bf, C, X, W, M, N, K);
     char* ws = nullptr;
-    if (need) {
+    if (need && src_ws.fixed) {
+        if (need > src_ws.fixed_bytes)
+            return set_error(AR_EINVAL, "%s: this shape needs %zu bytes of scratch, above the fixed %zu", nm, need,
+                             src_ws.fixed_bytes);
+        ws = src_ws.fixed;
+    } else if (need) {
         ws = (char*)ar::workspace(S(s), need, &st);
         if (!ws) return st;
     }
@@ -1283,6 +1296,52 @@ extern "C" int32_t ar_linear_bwd_dw(ar_stream_t stream, float* grad_weight, cons
 extern "C" int32_t ar_linear_bwd_dw_bf16(ar_stream_t stream, float* grad_weight, const float* grad_output,
                                          const float* input, int64_t M, int64_t N, int64_t K) {
     return linear_bwd_dw_impl(stream, grad_weight, grad_output, input, M, N, K, true);
+}
+
+// ---- linear_bwd_dw_bf16 with no workspace: scratch in a fixed device array ----
+// For callers that cannot allocate device memory or bind a workspace (code
+// under stream capture, serving loops, harnesses that forbid it).  The split-K
+// partials (and, for shapes off the 8-multiple / 16-byte-aligned grid, the
+// zero-padded operand copies) go to `scratch`, one copy per device, held for
+// the life of the process.  Every call on a device shares that device's array:
+// calls that overlap in time on one device (two streams, two threads) race.
+// Nothing in it needs to start at zero: the partials and the padded copies
+// are written in full before they are read.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+// Device address of this device's `scratch` (the host-side name is only a
+// handle for the symbol lookup), looked up once per device.
+static char* noalloc_scratch(int32_t* status) {
+    constexpr int kMaxDev = 64;
+    static std::mutex mu;
+    static char* addr[kMaxDev] = {};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+        *status = set_error(AR_EHIP, "linear_bwd_dw_bf16_noalloc: no current device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            *status = set_error(AR_EHIP, "linear_bwd_dw_bf16_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+            return nullptr;
+        }
+        addr[dev] = static_cast<char*>(p);
+    }
+    *status = AR_OK;
+    return addr[dev];
+}
+
+extern "C" int32_t ar_linear_bwd_dw_bf16_noalloc(ar_stream_t stream, float* grad_weight, const float* grad_output,
+                                                 const float* input, int64_t M, int64_t N, int64_t K) {
+    int32_t st = AR_OK;
+    char* p = noalloc_scratch(&st);
+    if (!p) return st;
+    return linear_call(stream, 2, true, grad_weight, grad_output, input, M, N, K, "linear_bwd_dw_bf16_noalloc",
+                       ScratchSrc{p, kNoAllocScratchBytes});
 }
 
 // Reference-layout GEMM with bf16 or fp32 storage per operand; bf16 matrix

@@ -168,6 +168,19 @@ int32_t ar_linear_bwd_dw(ar_stream_t stream, float* grad_weight, const float* gr
                          int64_t M, int64_t N, int64_t K);
 int32_t ar_linear_bwd_dw_bf16(ar_stream_t stream, float* grad_weight, const float* grad_output,
                               const float* input, int64_t M, int64_t N, int64_t K);
+/* ar_linear_bwd_dw_bf16 that needs no workspace and allocates nothing.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory or bind a workspace (code under stream capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results
+ * (bit-identical); its scratch (split-K partials, zero-padded copies of
+ * unaligned operands) is a fixed 64 MiB device array per device, held until
+ * the process ends.  A shape that needs more returns AR_EINVAL and
+ * ar_last_error() names the bytes.  All calls on one device share that array:
+ * calls that overlap in time on one device race.  The first call on a device
+ * looks the array's address up (hipGetSymbolAddress); make it before any
+ * stream capture. */
+int32_t ar_linear_bwd_dw_bf16_noalloc(ar_stream_t stream, float* grad_weight, const float* grad_output,
+                                      const float* input, int64_t M, int64_t N, int64_t K);
 /* Storage-typed GEMM (no counterpart in the reference, which is fp32 only):
  * layout 0/1/2 = linear_fwd / linear_bwd_dx / linear_bwd_dw semantics with
  * X, W and C each stored as bf16 (flag 1) or fp32 (flag 0); bf16 matrix
