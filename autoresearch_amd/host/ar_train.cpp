@@ -17,8 +17,11 @@
 //
 // Usage: ar_train [--data DIR] [--tokenizer DIR] [--vocab V] [--depth D]
 //                 [--batch B] [--seq T] [--fp32] [--graph] [--fake-dt SEC]
+//                 [--nan-at STEP]
 //   TRAIN_TIME_BUDGET=<seconds> overrides the 300 s budget (train.mojo:211-221).
 //   --fake-dt replaces each step's measured time in the schedule (tests).
+//   --nan-at writes a NaN into lm_head before step STEP (tests of the NaN
+//     fast fail, train.mojo:284-287; the kernels run normally on NaN data).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdio.h>
@@ -90,6 +93,7 @@ struct Args {
     int64_t vocab = kVocab, depth = kDepth, B = 4, T = 512;  // train.mojo:152-153
     bool fp32 = false, graph = false;
     double fake_dt = -1.0;
+    int64_t nan_at = -1;  // --nan-at STEP: lm_head[0] := NaN before that step (tests the fast fail)
 };
 
 Args parse(int argc, char** argv) {
@@ -116,9 +120,10 @@ Args parse(int argc, char** argv) {
         else if (k == "--fp32") a.fp32 = true;
         else if (k == "--graph") a.graph = true;
         else if (k == "--fake-dt") a.fake_dt = atof(val());
+        else if (k == "--nan-at") a.nan_at = atoll(val());
         else {
             fprintf(stderr, "usage: ar_train [--data DIR] [--tokenizer DIR] [--vocab V] [--depth D] [--batch B] "
-                            "[--seq T] [--fp32] [--graph] [--fake-dt SEC]\n");
+                            "[--seq T] [--fp32] [--graph] [--fake-dt SEC] [--nan-at STEP]\n");
             exit(2);
         }
     }
@@ -196,6 +201,21 @@ int main(int argc, char** argv) {
         const double lrm = lr_multiplier(progress);
         int64_t next_epoch = epoch;
         float loss32 = 0.f;
+        if (step == a.nan_at) {
+            // fault injection from the host: one lm_head weight becomes NaN, so
+            // every logit row, and the step's loss, is NaN
+            int64_t off = -1;
+            for (int64_t i = 0; i < ar_gpt_num_tensors(m); ++i) {
+                int64_t o = 0;
+                const char* nm = nullptr;
+                ar_gpt_tensor_info(m, i, &o, &nm);
+                if (nm && std::string(nm) == "lm_head") off = o;
+            }
+            const float qnan = NAN;
+            HIPCHECK(off >= 0 ? hipSuccess : hipErrorInvalidValue, "lm_head offset");
+            HIPCHECK(hipMemcpyAsync(ar_gpt_params(m) + off, &qnan, sizeof(float), hipMemcpyHostToDevice, st), "nan");
+            HIPCHECK(hipStreamSynchronize(st), "nan");
+        }
         if (a.graph) {
             // one graph replay (zero_grads -> forward -> backward -> AdamW + Muon)
             // on the fixed token buffers; the next batch is packed meanwhile

@@ -76,6 +76,18 @@ def measured_traffic(cls: str, a, bf16: bool):
         return json.load(f)["classes"].get(cls)
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (what lscpu prints as "Model name")."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(cfg, T, V, steps_tokens_B: int) -> dict:
     """fp32 CPU oracle on this host: one forward+backward at B=1 (2048 tokens)
     and one optimizer step, extrapolated to the B=32 step."""
@@ -94,9 +106,67 @@ def cpu_baseline(cfg, T, V, steps_tokens_B: int) -> dict:
     fb, opt = t1 - t0, t2 - t1
     est = steps_tokens_B * fb + opt
     return {"value": round(steps_tokens_B * T / est, 2), "unit": "tokens/s",
-            "cores": orc.lib().orc_num_threads(), "kind": "port",
+            "cores": orc.lib().orc_num_threads(), "cpu_model": cpu_model(), "kind": "port",
             "sample": (f"fp32 oracle (OpenMP): 1 fwd+bwd at B=1,T={T} ({fb:.1f}s) + 1 AdamW/Muon update "
                        f"({opt:.1f}s), extrapolated to B={steps_tokens_B}: {steps_tokens_B}*fwdbwd + update")}
+
+
+def vendor_comparator() -> list:
+    """What the ROCm libraries reach on the step's shapes (config 4, bf16
+    operands): hipBLASLt through torch.mm for each linear layer's forward
+    (bf16 and fp32 output), dW and dX, a 8192^3 square, and torch's
+    scaled_dot_product_attention at BASELINE config 2.  A comparator only:
+    the library never calls them.  Mean of 20 calls after 3 warm-up calls."""
+    import torch
+    import torch.nn.functional as F
+
+    def timed(f, n=20):
+        for _ in range(3):
+            f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    torch.manual_seed(0)
+    rows = []
+
+    def row(name, ms, flops):
+        rows.append({"product": name, "us": round(ms * 1e3, 1), "tflops": round(flops / ms / 1e9, 1)})
+        print(f"[comparator] {name}: {ms * 1e3:.1f} us", file=sys.stderr, flush=True)
+
+    M = 65536
+    for lname, n, k in (("q|k|v", 1536, 512), ("c_proj", 512, 512), ("c_fc", 2048, 512), ("mlp_proj", 512, 2048),
+                        ("lm_head", 8192, 512)):
+        a = torch.randn(M, k, device="cuda", dtype=torch.bfloat16)
+        w = torch.randn(n, k, device="cuda", dtype=torch.bfloat16) * 0.02
+        dy = torch.randn(M, n, device="cuda", dtype=torch.bfloat16)
+        out = torch.empty(M, n, device="cuda", dtype=torch.bfloat16)
+        fl = 2.0 * M * n * k
+        row(f"{lname} fwd {M}x{n}x{k} bf16 out", timed(lambda: torch.mm(a, w.t(), out=out)), fl)
+        row(f"{lname} fwd {M}x{n}x{k} fp32 out", timed(lambda: torch.mm(a, w.t(), out_dtype=torch.float32)), fl)
+        row(f"{lname} dW {n}x{k} (reduction {M})", timed(lambda: torch.mm(dy.t(), a)), fl)
+        row(f"{lname} dX {M}x{k} (reduction {n})", timed(lambda: torch.mm(dy, w)), fl)
+        del a, w, dy, out
+    a = torch.randn(8192, 8192, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(8192, 8192, device="cuda", dtype=torch.bfloat16)
+    row("square 8192x8192x8192", timed(lambda: a @ b, 10), 2.0 * 8192 ** 3)
+    del a, b
+    q = torch.randn(16, 4, 2048, 128, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    k_ = torch.randn_like(q, requires_grad=True)
+    v = torch.randn_like(q, requires_grad=True)
+    fl = 4.0 * 16 * 4 * 128 * (2048 * 2049 / 2)
+    row("sdpa causal fwd B16 H4 T2048 hd128", timed(lambda: F.scaled_dot_product_attention(q, k_, v, is_causal=True)),
+        fl)
+    g = torch.randn(16, 4, 2048, 128, device="cuda", dtype=torch.bfloat16)
+    row("sdpa causal fwd+bwd B16 H4 T2048 hd128",
+        timed(lambda: torch.autograd.grad(F.scaled_dot_product_attention(q, k_, v, is_causal=True), (q, k_, v), g)),
+        3.5 * fl)
+    return rows
 
 
 def main(argv=None) -> int:
@@ -116,6 +186,8 @@ def main(argv=None) -> int:
     ap.add_argument("--prof-steps", type=int, default=5, help="profiled steps after the timed ones")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run one device copy of MIB MiB (calibrates rocprofv3 byte counters) and exit")
+    ap.add_argument("--vendor-comparator", action="store_true",
+                    help="only time hipBLASLt (torch.mm) and torch SDPA on the step's shapes and exit")
     a = ap.parse_args(argv)
     if a.depth is None:
         a.depth = 8 if a.config == 4 else 12
@@ -128,6 +200,10 @@ def main(argv=None) -> int:
 
     import torch
     from autoresearch_amd.model import BF16, FP32, GPT, GPTConfig
+
+    if a.vendor_comparator:
+        print(json.dumps({"vendor_comparator": vendor_comparator()}), flush=True)
+        return 0
 
     if a.copy_probe:
         n = a.copy_probe * (1 << 20) // 4

@@ -106,3 +106,27 @@ def test_driver_schedule_log_and_summary(tmp_path, graph):
     l0 = gm.forward(gu.dev(x.ravel()), gu.dev(y.ravel()))
     gm.close()
     assert abs(losses[0] - l0) <= 1e-6 * abs(l0), (losses[0], l0)
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_driver_nan_fast_fail(tmp_path, graph):
+    """train.mojo:284-287: a NaN loss ends training with "FAIL: loss = nan"
+    right after the step that produced it, before its log line, and no
+    evaluation or summary follows.  The NaN is forced from the host
+    (--nan-at writes one into lm_head before step 3); every kernel runs
+    normally on the NaN data."""
+    d = str(tmp_path)
+    _make_data(d)
+    env = dict(os.environ, TRAIN_TIME_BUDGET=str(BUDGET))
+    cmd = [DRIVER, "--data", d, "--tokenizer", d, "--vocab", str(V), "--depth", str(DEPTH), "--batch", str(B),
+           "--seq", str(T), "--fake-dt", str(DT), "--nan-at", "3"] + (["--graph"] if graph else [])
+    print("running", " ".join(cmd), flush=True)
+    r = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=180)
+    print(r.stdout[-3000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0  # the reference returns from main
+    lines = r.stdout.splitlines()
+    steps = [STEP_RE.match(l) for l in lines if l.startswith("step ")]
+    assert [int(m.group(1)) for m in steps] == [0, 1, 2]
+    assert all(math.isfinite(float(m.group(3))) for m in steps)
+    assert lines[-1] == "FAIL: loss = nan"
+    assert "---" not in lines and not any(l.startswith("val_bpb") for l in lines)
