@@ -169,6 +169,64 @@ def vendor_comparator() -> list:
     return rows
 
 
+def gemm_sweep() -> list:
+    """The persistent GEMM (ar_gemm_mixed, bf16 operands) on the step's
+    product shapes at several reduction lengths: time(K) = fixed + K-loop,
+    so the intercept is the per-tile cost that does not scale with K (the
+    epilogue, pipeline fill) and the slope the k-loop's rate.  Mean of 20
+    calls after 3 warm-up calls, timed with torch events."""
+    import ctypes as ct
+    import torch
+    from autoresearch_amd import _lib, ops
+
+    lib = _lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    ws = ops.Workspace(1 << 30).bind()
+
+    def timed(f, n=20):
+        for _ in range(3):
+            f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    rows = []
+    M = 65536
+    for layout, N, Ks, cb in ((0, 2048, (256, 512, 1024, 2048, 4096), 1), (0, 512, (512, 2048, 4096), 0),
+                              (2, 2048, (16384, 32768, 65536, 131072), 0)):
+        for K in Ks:
+            if layout == 0:  # C[M, N] = X[M, K] W[N, K]^T
+                X = torch.randn(M, K, device="cuda").to(torch.bfloat16)
+                W = (torch.randn(N, K, device="cuda") * 0.02).to(torch.bfloat16)
+                C = torch.empty(M, N, device="cuda", dtype=torch.bfloat16 if cb else torch.float32)
+                m, n, k = M, N, K
+            else:  # dW[N, 512] += dY[K, N]^T X[K, 512]: K is the reduction (tokens)
+                X = torch.randn(K, N, device="cuda").to(torch.bfloat16)
+                W = torch.randn(K, 512, device="cuda").to(torch.bfloat16)
+                C = torch.zeros(N, 512, device="cuda")
+                m, n, k = K, N, 512
+
+            def f():
+                r = lib.ar_gemm_mixed(ct.c_void_p(st), layout, ct.c_void_p(C.data_ptr()), cb, ct.c_void_p(X.data_ptr()),
+                                      1, ct.c_void_p(W.data_ptr()), 1, m, n, k, 1 if layout == 2 else 0)
+                if r != 0:
+                    raise RuntimeError(lib.ar_last_error().decode())
+            ms = timed(f)
+            fl = 2.0 * M * N * K if layout == 0 else 2.0 * K * N * 512
+            name = (f"NT {M}x{N}x{K} {'bf16' if cb else 'fp32'} out" if layout == 0
+                    else f"TN dW {N}x512, reduction {K}")
+            rows.append({"product": name, "us": round(ms * 1e3, 1), "tflops": round(fl / ms / 1e9, 1)})
+            print(f"[gemm-sweep] {name}: {ms * 1e3:.1f} us", file=sys.stderr, flush=True)
+            del X, W, C
+    ws.close()
+    return rows
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -188,6 +246,8 @@ def main(argv=None) -> int:
                     help="only run one device copy of MIB MiB (calibrates rocprofv3 byte counters) and exit")
     ap.add_argument("--vendor-comparator", action="store_true",
                     help="only time hipBLASLt (torch.mm) and torch SDPA on the step's shapes and exit")
+    ap.add_argument("--gemm-sweep", action="store_true",
+                    help="only time the persistent GEMM over several reduction lengths and exit")
     a = ap.parse_args(argv)
     if a.depth is None:
         a.depth = 8 if a.config == 4 else 12
@@ -203,6 +263,9 @@ def main(argv=None) -> int:
 
     if a.vendor_comparator:
         print(json.dumps({"vendor_comparator": vendor_comparator()}), flush=True)
+        return 0
+    if a.gemm_sweep:
+        print(json.dumps({"gemm_sweep": gemm_sweep()}), flush=True)
         return 0
 
     if a.copy_probe:
