@@ -207,6 +207,48 @@ __global__ void adamw_dev_k(float* p, const float* g, float* m, float* v, const 
     }
 }
 
+// adamw_dev_k over several tensors of one set of arenas (p, g, m, v at the
+// same element offsets) in one launch: block b updates 1024 elements of the
+// tensor whose block range holds b, with that tensor's lr, bias correction
+// and beta1.  Per element the arithmetic is adamw_dev_k's.
+__global__ __launch_bounds__(256) void adamw_multi_k(AdamTable t, float* p, const float* g, float* m, float* v,
+                                                     const float* sc, int bc2_i, float b2, float eps, float wd) {
+    const int64_t bid = blockIdx.x;
+    int j = 0;
+    while (j + 1 < t.n && bid >= t.blk0[j + 1]) ++j;
+    const float lr = sc[t.lr_i[j]], bc1 = sc[t.bc1_i[j]], bc2 = sc[bc2_i], b1 = t.b1[j];
+    const int64_t off = t.off[j], size = t.size[j];
+    const int64_t i0 = (bid - t.blk0[j]) * 1024 + threadIdx.x * 4;
+    auto one = [&](float& pv, float gv, float& mm, float& vv) {
+        pv = pv * (1.0f - lr * wd);
+        mm = b1 * mm + (1.0f - b1) * gv;
+        vv = b2 * vv + (1.0f - b2) * gv * gv;
+        pv = pv - lr * (mm / bc1) / (sqrtf(vv / bc2) + eps);
+    };
+    if (i0 + 4 <= size && (off & 3) == 0) {
+        float4* const p4 = reinterpret_cast<float4*>(p + off + i0);
+        float4* const m4 = reinterpret_cast<float4*>(m + off + i0);
+        float4* const v4 = reinterpret_cast<float4*>(v + off + i0);
+        float4 pv = *p4, mm = *m4, vv = *v4;
+        const float4 gv = *reinterpret_cast<const float4*>(g + off + i0);
+        one(pv.x, gv.x, mm.x, vv.x);
+        one(pv.y, gv.y, mm.y, vv.y);
+        one(pv.z, gv.z, mm.z, vv.z);
+        one(pv.w, gv.w, mm.w, vv.w);
+        *m4 = mm;
+        *v4 = vv;
+        *p4 = pv;
+    } else {
+        for (int64_t i = i0; i < i0 + 4 && i < size; ++i) {
+            float pv = p[off + i], mm = m[off + i], vv = v[off + i];
+            one(pv, g[off + i], mm, vv);
+            m[off + i] = mm;
+            v[off + i] = vv;
+            p[off + i] = pv;
+        }
+    }
+}
+
 // ---------------- K31 Nesterov (optimizer.mojo:132-146) ----------------
 __global__ void nesterov_k(float* out, const float* g, float* buf, float mu, int64_t n) {
     AR_GRID_LOOP(i, n) {
@@ -497,6 +539,31 @@ extern "C" int32_t ar_precompute_rope(ar_stream_t stream, float* cos_buf, float*
     free(hs);
     if (e1 != hipSuccess || e2 != hipSuccess || e3 != hipSuccess)
         return set_error(AR_EHIP, "precompute_rope: copy failed");
+    return AR_OK;
+}
+
+int32_t ar::adamw_multi(hipStream_t st, float* p, const float* g, float* m, float* v, const AdamEntry* e, int n,
+                        const float* sc, int bc2_i, float b2, float eps, float wd) {
+    for (int j0 = 0; j0 < n; j0 += kAdamMaxTensors) {
+        AdamTable t{};
+        int64_t blocks = 0;
+        t.n = n - j0 < kAdamMaxTensors ? n - j0 : kAdamMaxTensors;
+        for (int j = 0; j < t.n; ++j) {
+            const AdamEntry& x = e[j0 + j];
+            t.off[j] = x.offset;
+            t.size[j] = x.size;
+            t.blk0[j] = blocks;
+            t.lr_i[j] = x.lr_i;
+            t.bc1_i[j] = x.bc1_i;
+            t.b1[j] = x.b1;
+            blocks += (x.size + 1023) / 1024;
+        }
+        if (blocks == 0) continue;
+        if (blocks > INT32_MAX) return set_error(AR_EINVAL, "adamw: %lld blocks", (long long)blocks);
+        adamw_multi_k<<<(unsigned)blocks, 256, 0, st>>>(t, p, g, m, v, sc, bc2_i, b2, eps, wd);
+        const int32_t r = AR_LAUNCH_CHECK("adamw_multi");
+        if (r) return r;
+    }
     return AR_OK;
 }
 

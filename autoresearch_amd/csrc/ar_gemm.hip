@@ -332,9 +332,12 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
     const int64_t splits = (K + k_per_split - 1) / k_per_split;
     int64_t bt, tm, tn, z;
     tile_coords(tiles_n, tiles_mn, splits, tiles_mn * splits * batch, bt, tm, tn, z);
+    // STORE / AXPBY may run without C when only the bf16 copy aux_out is
+    // wanted (the batched Muon products whose fp32 result nothing reads)
+    const bool has_c = C != nullptr;
     A += bt * sA;
     B += bt * sB;
-    C += bt * sC;
+    if (has_c) C += bt * sC;
     if constexpr (EPI == EPI_PARTIAL) partial += bt * splits * M * N;
     const int64_t m0 = tm * BM, n0 = tn * BN;
     const int64_t kbeg = z * k_per_split;
@@ -441,7 +444,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
             if constexpr (EPI == EPI_PARTIAL) {
                 *reinterpret_cast<float4*>(partial + (z * M + row) * N + col) = x;
             } else if constexpr (EPI == EPI_STORE) {
-                st4(C + o, x);
+                if (has_c) st4(C + o, x);
                 if (aux_out) st4(static_cast<bf16*>(aux_out) + bt * sC + o, x);  // bf16 copy (batched Muon)
             } else if constexpr (EPI == EPI_ACCUM || EPI == EPI_ADD) {
                 st4(C + o, add4(pre[PRE ? t : 0], x));
@@ -458,7 +461,7 @@ __global__ __launch_bounds__(TL::THREADS) void gemm_k(TC* C, const TA* A, const 
                 const float4 y = pre[PRE ? t : 0];
                 const float4 r = make_float4(cap * x.x + beta * y.x, cap * x.y + beta * y.y, cap * x.z + beta * y.z,
                                              cap * x.w + beta * y.w);
-                st4(C + o, r);
+                if (has_c) st4(C + o, r);
                 if (aux_out) st4(static_cast<bf16*>(aux_out) + bt * sC + o, r);  // bf16 copy (batched Muon)
             }
         }
@@ -658,21 +661,30 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
         const int64_t cbase = row0 * ldc + col0;
         const int clo = lrow * (int)ldc + lcol;
         constexpr bool PRE = EPI == EPI_ACCUM || EPI == EPI_ADD || EPI == EPI_RELU2_BWD;
+        // The operand the epilogue combines with (C, the residual or the
+        // pre-activation) is loaded one half strip ahead, into a two-slot
+        // register ring, so its latency hides behind the previous strip.
+        float4 pre[2][PRE ? 4 : 1];
+        auto load_pre = [&](int s, float4 (&dst)[PRE ? 4 : 1]) {
+            if constexpr (PRE) {
+                const int64_t rb = cbase + (int64_t)(s * 16) * ldc;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int64_t o = rb + (int64_t)(t * 4) * ldc + clo;
+                    if constexpr (EPI == EPI_ACCUM) dst[t] = ld4(C + o);
+                    else if constexpr (EPI == EPI_ADD) dst[t] = ld4(static_cast<const float*>(aux) + o);
+                    else dst[t] = ld4(static_cast<const TC*>(aux) + o);
+                }
+            }
+        };
+        load_pre(0, pre[0]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const int64_t rb = cbase + (int64_t)(i * 32 + h * 16) * ldc;
-                float4 pre[PRE ? 4 : 1];
-                if constexpr (PRE) {
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const int64_t o = rb + (int64_t)(t * 4) * ldc + clo;
-                        if constexpr (EPI == EPI_ACCUM) pre[t] = ld4(C + o);
-                        else if constexpr (EPI == EPI_ADD) pre[t] = ld4(static_cast<const float*>(aux) + o);
-                        else pre[t] = ld4(static_cast<const TC*>(aux) + o);
-                    }
-                }
+                const int s = i * 2 + h;
+                const int64_t rb = cbase + (int64_t)(s * 16) * ldc;
+                if (s + 1 < 8) load_pre(s + 1, pre[(s + 1) & 1]);
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -695,14 +707,14 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
                     } else if constexpr (EPI == EPI_STORE) {
                         st4nt(C + o, x);
                     } else if constexpr (EPI == EPI_ACCUM || EPI == EPI_ADD) {
-                        st4nt(C + o, add4(pre[PRE ? t : 0], x));
+                        st4nt(C + o, add4(pre[s & 1][PRE ? t : 0], x));
                     } else if constexpr (EPI == EPI_RELU2) {
                         st4nt(C + o, make_float4(x.x > 0.f ? x.x * x.x : 0.f, x.y > 0.f ? x.y * x.y : 0.f,
                                                x.z > 0.f ? x.z * x.z : 0.f, x.w > 0.f ? x.w * x.w : 0.f));
                     } else if constexpr (EPI == EPI_SOFTCAP) {
                         st4nt(C + o, softcap4(x, cap));
                     } else if constexpr (EPI == EPI_RELU2_BWD) {
-                        const float4 a = pre[PRE ? t : 0];
+                        const float4 a = pre[s & 1][PRE ? t : 0];
                         st4nt(C + o, make_float4(relu2_grad(a.x, x.x), relu2_grad(a.y, x.y), relu2_grad(a.z, x.z),
                                                relu2_grad(a.w, x.w)));
                     }

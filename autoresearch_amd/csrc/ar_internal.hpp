@@ -101,6 +101,24 @@ int32_t rope(hipStream_t st, float* out, const float* in, const float* cos_t, co
 int32_t adamw_dev(hipStream_t st, float* p, const float* g, float* m, float* v, int64_t n, const float* sc,
                   int lr_i, int bc1_i, int bc2_i, float b1, float b2, float eps, float wd);
 
+// AdamW over several tensors of the same arenas in one launch: tensor j is
+// elements [offset, offset + size) of p, g, m and v, with its own lr
+// (sc[lr_i]), bias correction 1 - b1^t (sc[bc1_i]) and beta1.
+struct AdamEntry {
+    int64_t offset, size;
+    int lr_i, bc1_i;
+    float b1;
+};
+constexpr int kAdamMaxTensors = 32;
+struct AdamTable {
+    int n;
+    int64_t off[kAdamMaxTensors], size[kAdamMaxTensors], blk0[kAdamMaxTensors];
+    int lr_i[kAdamMaxTensors], bc1_i[kAdamMaxTensors];
+    float b1[kAdamMaxTensors];
+};
+int32_t adamw_multi(hipStream_t st, float* p, const float* g, float* m, float* v, const AdamEntry* e, int n,
+                    const float* sc, int bc2_i, float b2, float eps, float wd);
+
 // ---- fused row kernels of the bf16 step (ar_fused.hip) ----
 // mode 0: x0 = rmsnorm(table[idx]), x = sa[l] x0 + sb[l] x0; 1: x = sa[l] xin +
 // sb[l] x0; 2: x = xin.  Then rms, xn = bf16(x / rms); with gate_out also

@@ -861,20 +861,23 @@ static StepScalars step_scalars(ar_gpt* m, double progress) {
 static int32_t optimizer_body(ar_gpt* m, bool fork) {
     const ar_gpt_config& c = m->c;
     const hipStream_t ast = fork ? m->side[1] : m->st;
-    auto adam = [&](int64_t ti, int lr_i, int bc1_i, float b1) -> int32_t {
+    // every AdamW tensor in one launch
+    std::vector<AdamEntry> adam;
+    auto add = [&](int64_t ti, int lr_i, int bc1_i, float b1) {
         const Tensor& t = m->t[ti];
-        return adamw_dev(ast, m->params + t.offset, m->grads + t.offset, m->adam_m + t.offset,
-                         m->adam_v + t.offset, t.size, m->dsc, lr_i, bc1_i, kScBc2, b1, 0.95f, 1e-10f, 0.0f);
+        adam.push_back(AdamEntry{t.offset, t.size, lr_i, bc1_i, b1});
     };
-    AR_TRY(adam(m->i_lm, kScLrLm, kScBc1Default, 0.8f));
-    AR_TRY(adam(m->i_wte, kScLrWte, kScBc1Default, 0.8f));
-    AR_TRY(adam(m->i_res, kScLrRes, kScBc1Default, 0.8f));
-    AR_TRY(adam(m->i_x0, kScLrX0, kScBc1X0, 0.96f));
+    add(m->i_lm, kScLrLm, kScBc1Default, 0.8f);
+    add(m->i_wte, kScLrWte, kScBc1Default, 0.8f);
+    add(m->i_res, kScLrRes, kScBc1Default, 0.8f);
+    add(m->i_x0, kScLrX0, kScBc1X0, 0.96f);
     for (int64_t i = 0; i < c.n_layer; ++i)
         if (has_ve(c, i)) {
-            AR_TRY(adam(m->i_ve[i], kScLrVe, kScBc1Default, 0.8f));
-            AR_TRY(adam(m->i_gate[i], kScLrGate, kScBc1Default, 0.8f));
+            add(m->i_ve[i], kScLrVe, kScBc1Default, 0.8f);
+            add(m->i_gate[i], kScLrGate, kScBc1Default, 0.8f);
         }
+    AR_TRY(adamw_multi(ast, m->params, m->grads, m->adam_m, m->adam_v, adam.data(), (int)adam.size(), m->dsc,
+                       kScBc2, 0.95f, 1e-10f, 0.0f));
     // Muon on every 2-D matrix, grouped by shape and run as batched GEMMs.
     std::vector<int64_t> sq, fc, mp;
     for (int64_t i = 0; i < c.n_layer; ++i) {

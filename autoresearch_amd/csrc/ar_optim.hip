@@ -36,8 +36,16 @@ struct GroupTable {
 
 inline int64_t align64(int64_t n) { return (n + 63) & ~int64_t(63); }
 
+// The element-wise kernels run a float4 path (VEC) when every matrix of the
+// group is 16-byte aligned and its size a multiple of 4 (all model shapes);
+// the element order of each thread's sums is then 4 consecutive elements per
+// step, still fixed for a given shape.
+__device__ __forceinline__ float4 ld4v(const float* p, int64_t i4) { return reinterpret_cast<const float4*>(p)[i4]; }
+__device__ __forceinline__ void st4v(float* p, int64_t i4, float4 v) { reinterpret_cast<float4*>(p)[i4] = v; }
+
 // X_j = (1-mu) g + mu * (mu buf + (1-mu) g); buf updated (optimizer.mojo:132-146);
 // partial[j][b] = this block's sum of X^2.
+template <bool VEC>
 __global__ void nesterov_multi_k(GroupTable t, float* X, int64_t size, float mu, const float* dmu, float* partial) {
     __shared__ float red[4];
     if (dmu) mu = *dmu;
@@ -46,40 +54,79 @@ __global__ void nesterov_multi_k(GroupTable t, float* X, int64_t size, float mu,
     float* buf = t.m[j];
     float* x = X + (int64_t)j * size;
     float ss = 0.f;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size; i += (int64_t)gridDim.x * blockDim.x) {
-        const float gv = g[i];
-        const float mm = mu * buf[i] + (1.0f - mu) * gv;
-        buf[i] = mm;
-        const float o = (1.0f - mu) * gv + mu * mm;
-        x[i] = o;
+    auto one = [&](float gv, float bv, float& mm, float& o) {
+        mm = mu * bv + (1.0f - mu) * gv;
+        o = (1.0f - mu) * gv + mu * mm;
         ss += o * o;
+    };
+    if constexpr (VEC) {
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size / 4;
+             i += (int64_t)gridDim.x * blockDim.x) {
+            const float4 gv = ld4v(g, i), bv = ld4v(buf, i);
+            float4 mm, o;
+            one(gv.x, bv.x, mm.x, o.x);
+            one(gv.y, bv.y, mm.y, o.y);
+            one(gv.z, bv.z, mm.z, o.z);
+            one(gv.w, bv.w, mm.w, o.w);
+            st4v(buf, i, mm);
+            st4v(x, i, o);
+        }
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size;
+             i += (int64_t)gridDim.x * blockDim.x) {
+            float mm, o;
+            one(g[i], buf[i], mm, o);
+            buf[i] = mm;
+            x[i] = o;
+        }
     }
     ss = block_sum(ss, red);
     if (threadIdx.x == 0) partial[j * kNormBlocks + blockIdx.x] = ss;
 }
 
-// scale[j] = 1 / (||X_j||_F * 1.02 + 1e-6)  (optimizer.mojo:178)
-__global__ void norm_finish_k(float* scale, const float* partial) {
-    const int j = threadIdx.x;
-    float s = 0.f;
-    for (int b = 0; b < kNormBlocks; ++b) s += partial[j * kNormBlocks + b];
-    scale[j] = 1.0f / (sqrtf(s) * 1.02f + 1e-6f);
-}
-
-// X_j *= scale_j, and Xb (if set) = bf16(X)
-__global__ void scale_multi_k(float* X, bf16* Xb, int64_t size, const float* scale) {
+// X_j *= s_j with s_j = 1 / (||X_j||_F * 1.02 + 1e-6) (optimizer.mojo:178),
+// the norm summed from the kNormBlocks (= one wave's lanes) partials of
+// nesterov_multi_k in the same fixed order by every wave; Xb (if set) =
+// bf16(X).
+template <bool VEC>
+__global__ void scale_multi_k(float* X, bf16* Xb, int64_t size, const float* partial) {
+    static_assert(kNormBlocks == kWave, "one partial per lane");
     const int j = blockIdx.y;
-    const float sc = scale[j];
+    const float ss = wave_sum(partial[j * kNormBlocks + threadIdx.x % kWave]);
+    const float sc = 1.0f / (sqrtf(ss) * 1.02f + 1e-6f);
     float* x = X + (int64_t)j * size;
     bf16* xb = Xb ? Xb + (int64_t)j * size : nullptr;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size; i += (int64_t)gridDim.x * blockDim.x) {
-        const float v = x[i] * sc;
-        x[i] = v;
-        if (xb) xb[i] = (bf16)v;
+    if constexpr (VEC) {
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size / 4;
+             i += (int64_t)gridDim.x * blockDim.x) {
+            float4 v = ld4v(x, i);
+            v = make_float4(v.x * sc, v.y * sc, v.z * sc, v.w * sc);
+            st4v(x, i, v);
+            if (xb) {
+                bf16x4 b;
+                b[0] = (bf16)v.x;
+                b[1] = (bf16)v.y;
+                b[2] = (bf16)v.z;
+                b[3] = (bf16)v.w;
+                reinterpret_cast<bf16x4*>(xb)[i] = b;
+            }
+        }
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size;
+             i += (int64_t)gridDim.x * blockDim.x) {
+            const float v = x[i] * sc;
+            x[i] = v;
+            if (xb) xb[i] = (bf16)v;
+        }
     }
 }
 
 // p -= lr (X + wd p [X p >= 0])  (optimizer.mojo:197-210)
+__device__ __forceinline__ float cautious(float pv, float gv, float lr, float wd) {
+    const float decay = (gv * pv) >= 0.0f ? wd * pv : 0.0f;
+    return pv - lr * (gv + decay);
+}
+template <bool VEC>
 __global__ void update_multi_k(GroupTable t, const float* X, int64_t size, float lr, float wd, const float* dlr,
                                const float* dwd) {
     if (dlr) {
@@ -89,10 +136,17 @@ __global__ void update_multi_k(GroupTable t, const float* X, int64_t size, float
     const int j = blockIdx.y;
     float* p = t.p[j];
     const float* x = X + (int64_t)j * size;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size; i += (int64_t)gridDim.x * blockDim.x) {
-        const float pv = p[i], gv = x[i];
-        const float decay = (gv * pv) >= 0.0f ? wd * pv : 0.0f;
-        p[i] = pv - lr * (gv + decay);
+    if constexpr (VEC) {
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size / 4;
+             i += (int64_t)gridDim.x * blockDim.x) {
+            const float4 pv = ld4v(p, i), gv = ld4v(x, i);
+            st4v(p, i, make_float4(cautious(pv.x, gv.x, lr, wd), cautious(pv.y, gv.y, lr, wd),
+                                   cautious(pv.z, gv.z, lr, wd), cautious(pv.w, gv.w, lr, wd)));
+        }
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size;
+             i += (int64_t)gridDim.x * blockDim.x)
+            p[i] = cautious(p[i], x[i], lr, wd);
     }
 }
 
@@ -107,7 +161,7 @@ double muon_lr_factor(int64_t rows, int64_t cols) {
 int64_t muon_scratch_elems(int64_t rows, int64_t cols, bool bf16, int64_t n) {
     const int64_t size = rows * cols;
     const int64_t small = rows >= cols ? cols : rows;
-    const int64_t f32 = align64(n * kNormBlocks) + align64(n) + 2 * align64(n * size) + 2 * align64(n * small * small);
+    const int64_t f32 = align64(n * kNormBlocks) + 2 * align64(n * size) + 2 * align64(n * small * small);
     // bf16 operand copies of X, Y, A, Bm (two per float)
     return bf16 ? f32 + 2 * align64((n * size + 1) / 2) + 2 * align64((n * small * small + 1) / 2) : f32;
 }
@@ -122,8 +176,7 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
     const int64_t sm = tall ? cols : rows;
     const int64_t ss = sm * sm;
     float* partial = scratch;
-    float* scale = partial + align64(n * kNormBlocks);
-    float* X = scale + align64(n);
+    float* X = partial + align64(n * kNormBlocks);
     float* Y = X + align64(n * size);
     float* A = Y + align64(n * size);
     float* Bm = A + align64(n * ss);
@@ -136,17 +189,21 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
     ::ar::bf16* Bmb = bf16 ? Ab + 2 * align64((n * ss + 1) / 2) : nullptr;
 
     GroupTable t{};
+    bool vec = size % 4 == 0;
     for (int j = 0; j < n; ++j) {
         t.p[j] = params[j];
         t.g[j] = grads[j];
         t.m[j] = mbufs[j];
+        vec = vec && ((reinterpret_cast<uintptr_t>(params[j]) | reinterpret_cast<uintptr_t>(grads[j]) |
+                       reinterpret_cast<uintptr_t>(mbufs[j])) & 15) == 0;
     }
     const float lr = (float)(initial_lr * lrm * muon_lr_factor(rows, cols));
     const dim3 eg(kNormBlocks, n);
-    nesterov_multi_k<<<eg, 256, 0, st>>>(t, X, size, (float)momentum, dev.dsc ? dev.dsc + dev.mu_i : nullptr,
-                                         partial);
-    norm_finish_k<<<1, n, 0, st>>>(scale, partial);
-    scale_multi_k<<<eg, 256, 0, st>>>(X, Xb, size, scale);
+    const float* dmu = dev.dsc ? dev.dsc + dev.mu_i : nullptr;
+    if (vec) nesterov_multi_k<true><<<eg, 256, 0, st>>>(t, X, size, (float)momentum, dmu, partial);
+    else nesterov_multi_k<false><<<eg, 256, 0, st>>>(t, X, size, (float)momentum, dmu, partial);
+    if (vec) scale_multi_k<true><<<eg, 256, 0, st>>>(X, Xb, size, partial);
+    else scale_multi_k<false><<<eg, 256, 0, st>>>(X, Xb, size, partial);
     int32_t r = check_launch("muon: normalise");
     if (r) return r;
     ar_stream_t s = reinterpret_cast<ar_stream_t>(st);
@@ -166,14 +223,17 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
             r = gemm_batched_bf16(st, true, true, A, Ab, Xbc, Xbc, rows, rows, cols, cols, cols, rows, n, size, size,
                                   ss);
         if (r) return r;
-        if ((r = gemm_batched_bf16(st, true, false, Bm, Bmb, Ab, Ab, sm, sm, sm, sm, sm, sm, n, ss, ss, ss, A, cc,
-                                   cb)))
+        // only the bf16 copy of Bm is read (as the next product's operand),
+        // and the last iteration's X is read in fp32 only (the update)
+        if ((r = gemm_batched_bf16(st, true, false, nullptr, Bmb, Ab, Ab, sm, sm, sm, sm, sm, sm, n, ss, ss, ss, A,
+                                   cc, cb)))
             return r;
+        ::ar::bf16* const Yout = it < 4 ? Ybc : nullptr;
         if (tall)
-            r = gemm_batched_bf16(st, true, false, Yc, Ybc, Xbc, Bmb, rows, cols, cols, cols, cols, cols, n, size, ss,
+            r = gemm_batched_bf16(st, true, false, Yc, Yout, Xbc, Bmb, rows, cols, cols, cols, cols, cols, n, size, ss,
                                   size, Xc, 1.0f, ca);
         else
-            r = gemm_batched_bf16(st, true, false, Yc, Ybc, Bmb, Xbc, rows, cols, rows, rows, cols, cols, n, ss, size,
+            r = gemm_batched_bf16(st, true, false, Yc, Yout, Bmb, Xbc, rows, cols, rows, rows, cols, cols, n, ss, size,
                                   size, Xc, 1.0f, ca);
         if (r) return r;
         float* tmp = Xc;
@@ -206,8 +266,10 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
         Xc = Yc;
         Yc = tmp;
     }
-    update_multi_k<<<eg, 256, 0, st>>>(t, Xc, size, lr, (float)wd, dev.dsc ? dev.dsc + dev.lr_i : nullptr,
-                                       dev.dsc ? dev.dsc + dev.wd_i : nullptr);
+    const float* dlr = dev.dsc ? dev.dsc + dev.lr_i : nullptr;
+    const float* dwd = dev.dsc ? dev.dsc + dev.wd_i : nullptr;
+    if (vec) update_multi_k<true><<<eg, 256, 0, st>>>(t, Xc, size, lr, (float)wd, dlr, dwd);
+    else update_multi_k<false><<<eg, 256, 0, st>>>(t, Xc, size, lr, (float)wd, dlr, dwd);
     return check_launch("muon: update");
 }
 
