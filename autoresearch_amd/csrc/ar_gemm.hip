@@ -545,6 +545,8 @@ __device__ __forceinline__ void pk_item(int lin, int items, int tiles_n, int til
     tn = r - tm * tiles_n;
 }
 
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
 template <bool AK, bool BKM, typename TC, int EPI>
 __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, const bf16* B, int64_t M, int64_t N,
                                                      int64_t lda, int64_t ldb, int64_t ldc, int64_t kps,
@@ -555,6 +557,11 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
     const int lane = threadIdx.x % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int wm = wave >> 2, wn = wave & 3;
+    // bf16 outputs whose epilogue is element-wise on the product alone: the
+    // MFMA operands are swapped so that each accumulator holds a transposed
+    // 32 x 32 block (lane l: row l % 32, four consecutive columns per group of
+    // four values), and the epilogue stages bf16 instead of fp32 (see below)
+    constexpr bool SW = std::is_same<TC, bf16>::value && (EPI == EPI_STORE || EPI == EPI_RELU2 || EPI == EPI_SOFTCAP);
     const int tiles_n = (int)(N / 256), tiles_mn = (int)(M / 256) * tiles_n, items = tiles_mn * (int)splits;
     const int grid = (int)gridDim.x, b = (int)blockIdx.x;
     const int nk = (int)(kps / kPkBK);
@@ -646,7 +653,8 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks & 1][i], fb[ks & 1][j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = SW ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks & 1][j], fa[ks & 1][i], acc[i][j], 0, 0, 0)
+                                   : __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks & 1][i], fb[ks & 1][j], acc[i][j], 0, 0, 0);
         }
         if (++ckt != nk) continue;
         ckt = 0;
@@ -660,6 +668,63 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
         // this wave's 128 x 64 block: element (r, c) at base + r * ld + c
         const int64_t cbase = row0 * ldc + col0;
         const int clo = lrow * (int)ldc + lcol;
+        if constexpr (SW) {
+            // Per 32-row block i: the lane's 32 values (row m = lane % 32,
+            // columns j * 32 + 8 g + 4 (lane / 32) + 0..3) go through the
+            // element-wise op in fp32, are rounded to bf16 and written as 8-byte
+            // pieces into a wave-private 32 x 64 bf16 strip; each lane then
+            // reads 16 bytes (8 columns of one row) and stores them, 8 rows of
+            // 128 bytes per store instruction.  Strip layout: row m at m * 128
+            // bytes, logical 8-byte piece c (columns 4c..4c+3) in slot
+            // ((c / 2) ^ (m % 8)) * 2 + ((c % 2) ^ (m / 8 % 2)): 16 rows of one
+            // piece land in 16 different slots, and a 16-byte pair stays
+            // adjacent (its halves swapped on rows with m / 8 odd).
+            unsigned char* const bstrip = smem_raw + 2 * kPkStage + wave * 4096;
+            const int m = lane & 31, hh = lane >> 5;
+            const int rr = lane >> 3, c16 = lane & 7;
+            TC* const lbase = C + cbase + (int64_t)rr * ldc + c16 * 8;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; ++g4) {
+                        float4 x = make_float4(acc[i][j][g4 * 4], acc[i][j][g4 * 4 + 1], acc[i][j][g4 * 4 + 2],
+                                               acc[i][j][g4 * 4 + 3]);
+                        if constexpr (EPI == EPI_RELU2)
+                            x = make_float4(x.x > 0.f ? x.x * x.x : 0.f, x.y > 0.f ? x.y * x.y : 0.f,
+                                            x.z > 0.f ? x.z * x.z : 0.f, x.w > 0.f ? x.w * x.w : 0.f);
+                        else if constexpr (EPI == EPI_SOFTCAP)
+                            x = softcap4(x, cap);
+                        bf16x4 v;
+                        v[0] = (bf16)x.x;
+                        v[1] = (bf16)x.y;
+                        v[2] = (bf16)x.z;
+                        v[3] = (bf16)x.w;
+                        const int c = j * 8 + g4 * 2 + hh;
+                        const int slot = (((c >> 1) ^ (m & 7)) << 1) + ((c & 1) ^ ((m >> 3) & 1));
+                        *reinterpret_cast<bf16x4*>(bstrip + m * 128 + slot * 8) = v;
+                    }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const int r = p * 8 + rr;
+                    u32x4 q = *reinterpret_cast<const u32x4*>(bstrip + r * 128 + ((c16 ^ (r & 7)) << 4));
+                    if (p & 1) q = __builtin_shufflevector(q, q, 2, 3, 0, 1);  // r / 8 odd
+                    __builtin_nontemporal_store(q, reinterpret_cast<u32x4*>(lbase + (int64_t)(i * 32 + p * 8) * ldc));
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+            }
+            continue;
+        }
         constexpr bool PRE = EPI == EPI_ACCUM || EPI == EPI_ADD || EPI == EPI_RELU2_BWD;
         // The operand the epilogue combines with (C, the residual or the
         // pre-activation) is loaded one half strip ahead, into a two-slot
