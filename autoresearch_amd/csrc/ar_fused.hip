@@ -27,6 +27,8 @@
 
 #include "ar_internal.hpp"
 
+#include <type_traits>
+
 namespace ar {
 namespace {
 
@@ -324,6 +326,66 @@ __global__ __launch_bounds__(kBlock) void ce_fused_k(float* loss, bf16* grad, co
     }
 }
 
+// The same for bf16 logits with V % 8 == 0: 16-byte loads and stores, 8
+// columns per thread and step (the row is NV8 x 8 registers per thread).
+template <int NV8>
+__global__ __launch_bounds__(kBlock) void ce_fused8_k(float* loss, bf16* grad, const bf16* logits,
+                                                      const int64_t* targets, int64_t V, float scale) {
+    __shared__ float red[kBlock / kWave];
+    const int64_t t = blockIdx.x;
+    const int64_t tg = targets[t];
+    const bf16* rowp = logits + t * V;
+    const int64_t V8 = V / 8;
+    float x[NV8][8];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NV8; ++j) {
+        const int64_t i = threadIdx.x + (int64_t)kBlock * j;
+        if (i < V8) {
+            const bf16x8 v = *reinterpret_cast<const bf16x8*>(rowp + 8 * i);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[j][e] = (float)v[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[j][e] = -INFINITY;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m = fmaxf(m, x[j][e]);
+    }
+    m = block_max(m, red);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV8; ++j) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[j][e] = __expf(x[j][e] - m);
+        s += (x[j][0] + x[j][1]) + (x[j][2] + x[j][3]);
+        s += (x[j][4] + x[j][5]) + (x[j][6] + x[j][7]);
+    }
+    s = block_sum(s, red);
+    const bool live = tg >= 0 && tg < V;  // other targets are ignored rows
+    if (loss && threadIdx.x == 0) loss[t] = live ? -(float)logits[t * V + tg] + (m + logf(s)) : 0.f;
+    bf16* g = grad + t * V;
+    const float rs = 1.0f / s;
+#pragma unroll
+    for (int j = 0; j < NV8; ++j) {
+        const int64_t i = threadIdx.x + (int64_t)kBlock * j;
+        if (i >= V8) continue;
+        bf16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float v = 0.f;
+            if (live) {
+                v = x[j][e] * rs;
+                if (tg == 8 * i + e) v -= 1.0f;
+                v *= scale;
+            }
+            o[e] = (bf16)v;
+        }
+        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), reinterpret_cast<u32x4*>(g + 8 * i));
+    }
+}
+
 // ---------------------------------------------------------------------
 // ve_bwd (ve_apply_bwd, ops.mojo:1193-1237) from a bf16 dV with row stride
 // ldv: wave per token; gve = gate * dv, ggate[h] = sum_d ve[d] dv[d]
@@ -556,6 +618,16 @@ static int32_t ce_fused_t(hipStream_t st, float* loss, bf16* grad, const TL* log
     if (rows > 0x7fffffff) return set_error(AR_EINVAL, "ce_fused: too many rows");
     const int64_t nv4 = cdiv(V, 4 * kBlock);
     const unsigned grid = (unsigned)rows;
+    if constexpr (std::is_same<TL, bf16>::value) {
+        const int64_t nv8 = cdiv(V, 8 * kBlock);
+        if (V % 8 == 0 && nv8 <= 8) {
+            if (nv8 <= 1) ce_fused8_k<1><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
+            else if (nv8 <= 2) ce_fused8_k<2><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
+            else if (nv8 <= 4) ce_fused8_k<4><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
+            else ce_fused8_k<8><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
+            return check_launch("ce_fused");
+        }
+    }
     if (nv4 <= 2) ce_fused_k<2, TL><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
     else if (nv4 <= 4) ce_fused_k<4, TL><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);
     else if (nv4 <= 8) ce_fused_k<8, TL><<<grid, kBlock, 0, st>>>(loss, grad, logits, targets, V, scale);

@@ -237,50 +237,68 @@ __global__ void ve_apply_bwd_k(float* gve, float* ggate, const float* gv, const 
 // ---------------- K27 ve_gate_bwd (ops.mojo:1240-1274), deterministic ----------------
 // Block b owns a fixed token range.  Thread (c = tid % CW, j = tid / CW),
 // CW = 32 or 64 channel lanes (gc <= CW), walks tokens t0 + j + NJ i with
-// four tokens' loads issued together: gx[t,c] += sum_h dz[t,h] W[h,c] for
-// its tokens (no conflicts), and a per-block partial of
-// gW[h,c] = sum_t dz[t,h] x[t,c], reduced over j in LDS in j order.
+// U tokens' loads issued together: gx[t,c] += sum_h dz[t,h] W[h,c] for its
+// tokens (no conflicts), and a per-block partial of
+// gW[h,c] = sum_t dz[t,h] x[t,c], reduced over j in LDS in j order.  The
+// gate factors dz[t,h] = ggate g (1 - g/2) of kGateTok tokens at a time are
+// staged in LDS by one coalesced pass, so a token step waits for one round
+// of loads (x and gx together), not one per head.
+constexpr int kGateTok = 256;
 template <int CW, typename TG>
-__global__ __launch_bounds__(256) void ve_gate_bwd_partial_k(TG* gx, float* partial, const float* ggate,
-                                                             const float* gate, const float* xn, const float* w,
-                                                             int64_t nt, int64_t nkv, int64_t gc, int64_t C,
-                                                             int64_t ldx) {
-    constexpr int NJ = 256 / CW, U = 4;
+__global__ __launch_bounds__(256) void ve_gate_bwd_partial_k(TG* __restrict__ gx, float* __restrict__ partial,
+                                                             const float* __restrict__ ggate,
+                                                             const float* __restrict__ gate,
+                                                             const float* __restrict__ xn,
+                                                             const float* __restrict__ w, int64_t nt, int64_t nkv,
+                                                             int64_t gc, int64_t C, int64_t ldx) {
+    constexpr int NJ = 256 / CW, U = 8;
     __shared__ float acc_s[NJ][kGateMaxH][CW];
+    __shared__ float dz_s[kGateTok * kGateMaxH];
     const int c = threadIdx.x % CW, j = threadIdx.x / CW;
     const int64_t per = (nt + gridDim.x - 1) / gridDim.x;
     const int64_t t0 = (int64_t)blockIdx.x * per;
     const int64_t t1 = t0 + per < nt ? t0 + per : nt;
-    float accw[kGateMaxH];
+    float accw[kGateMaxH], wv[kGateMaxH];
 #pragma unroll
-    for (int h = 0; h < kGateMaxH; ++h) accw[h] = 0.f;
-    if (c < gc) {
-        for (int64_t t = t0 + j; t < t1; t += U * NJ) {
-            float x[U], ax[U];
+    for (int h = 0; h < kGateMaxH; ++h) {
+        accw[h] = 0.f;
+        wv[h] = (h < nkv && c < gc) ? w[h * gc + c] : 0.f;
+    }
+    for (int64_t base = t0; base < t1; base += kGateTok) {
+        const int64_t end = base + kGateTok < t1 ? base + kGateTok : t1;
+        __syncthreads();  // the previous tokens' factors are no longer read
+        for (int64_t i = threadIdx.x; i < (end - base) * nkv; i += 256) {
+            const float g = gate[base * nkv + i];
+            dz_s[i] = ggate[base * nkv + i] * g * (1.0f - g / 2.0f);
+        }
+        __syncthreads();
+        if (c >= gc) continue;
+        for (int64_t t = base + j; t < end; t += U * NJ) {
+            float x[U], gv[U], ax[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int64_t tt = t + u * NJ;
-                x[u] = tt < t1 ? xn[tt * ldx + c] : 0.f;
+                const bool ok = tt < end;
+                x[u] = ok ? xn[tt * ldx + c] : 0.f;
+                gv[u] = ok ? (float)gx[tt * C + c] : 0.f;
                 ax[u] = 0.f;
             }
 #pragma unroll
             for (int h = 0; h < kGateMaxH; ++h) {
                 if (h >= nkv) break;
-                const float wv = w[h * gc + c];
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const int64_t tt = t + u * NJ;
-                    if (tt >= t1) break;
-                    const float g = gate[tt * nkv + h];
-                    const float dz = ggate[tt * nkv + h] * g * (1.0f - g / 2.0f);
-                    ax[u] += dz * wv;
+                    if (tt >= end) break;
+                    const float dz = dz_s[(tt - base) * nkv + h];
+                    ax[u] += dz * wv[h];
                     accw[h] += dz * x[u];
                 }
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int64_t tt = t + u * NJ;
-                if (tt < t1) gx[tt * C + c] = (TG)((float)gx[tt * C + c] + ax[u]);
+                if (tt < end) gx[tt * C + c] = (TG)(gv[u] + ax[u]);
             }
         }
     }
