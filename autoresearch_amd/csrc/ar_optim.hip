@@ -7,7 +7,7 @@
 // fraction of the GPU).  Here every product of an iteration is one batched
 // MFMA GEMM over the whole group (e.g. all 32 512x512 attention matrices),
 // and the element-wise steps are multi-tensor kernels over the group:
-// 29 launches per group per step.  A wide matrix (rows < cols) uses the
+// 18 launches per group per step.  A wide matrix (rows < cols) uses the
 // A = X X^T / B @ X formulation directly through the GEMM operand layouts,
 // exactly as the reference's wide branch (optimizer.mojo:297-303, 327-332).
 #include <math.h>
