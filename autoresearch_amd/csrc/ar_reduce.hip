@@ -455,12 +455,37 @@ __device__ __forceinline__ int64_t emb_upper(const uint32_t* k, int64_t lo, int6
     return lo;
 }
 
+// The same for a whole wave (every lane calls it with the same arguments and
+// gets the same result): 64 probes per step, each step narrowing the range to
+// one probe interval, i.e. ceil(log64(hi - lo)) dependent loads instead of
+// log2(hi - lo).  Invariant: the answer lies in [lo, hi], keys[lo - 1] <= v.
+__device__ __forceinline__ int64_t emb_upper_wave(const uint32_t* k, int64_t lo, int64_t hi, uint32_t v, int lane) {
+    while (lo < hi) {
+        const int64_t step = (hi - lo + kWave - 1) / kWave;
+        const int64_t q = lo + (int64_t)lane * step;
+        const bool past = q >= hi || k[q] > v;
+        const uint64_t m = __builtin_amdgcn_ballot_w64(past);
+        const int f = m ? __builtin_ctzll(m) : kWave;  // first probe past the run of v
+        if (f == 0) return lo;
+        const int64_t a = lo + (int64_t)(f - 1) * step + 1;  // probe f - 1 is inside the run
+        const int64_t b = lo + (int64_t)f * step;
+        lo = a;
+        hi = b < hi ? b : hi;
+    }
+    return lo;
+}
+
 // Chunk sums, one workgroup per 64-position window of the sorted ids (every
 // chunk lies inside one window): the window's rows are walked in order, 8
 // rows' loads issued ahead, and each chunk's sum (started from its first row,
 // then += the next rows in token order) is written to partial[chunk start].
 // Threads own float2 columns t + 256 j (dim % 2 == 0).
 constexpr int kUnroll = 8;
+// The window walk's loads are branch-free (clamped row and column, the
+// clamped values never added or stored) so that kWinAhead rows' gathers are
+// in flight together; a bound-checked load in a branch makes the compiler
+// wait for each one before issuing the next.
+constexpr int kWinAhead = 8;
 
 template <int NJ>
 __global__ __launch_bounds__(256) void emb_chunk_sum_win_k(float* partial, const uint32_t* keys, const int32_t* tok,
@@ -477,20 +502,20 @@ __global__ __launch_bounds__(256) void emb_chunk_sum_win_k(float* partial, const
     const int64_t d2 = dim / 2;
     float2 acc[NJ];
     int start = 0;
-    for (int r0 = 0; r0 < len; r0 += kUnroll) {
-        float2 x[kUnroll][NJ];
+    int64_t cj[NJ];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const int r = r0 + u < len ? r0 + u : 0;
+    for (int j = 0; j < NJ; ++j) cj[j] = threadIdx.x + 256 * j < d2 ? threadIdx.x + 256 * j : 0;
+    for (int r0 = 0; r0 < len; r0 += kWinAhead) {
+        float2 x[kWinAhead][NJ];
+#pragma unroll
+        for (int u = 0; u < kWinAhead; ++u) {
+            const int r = r0 + u < len ? r0 + u : len - 1;
             const float2* row = reinterpret_cast<const float2*>(dy + (int64_t)s_tok[r] * dim);
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const int64_t c = threadIdx.x + 256 * j;
-                x[u][j] = (r0 + u < len && c < d2) ? row[c] : make_float2(0.f, 0.f);
-            }
+            for (int j = 0; j < NJ; ++j) x[u][j] = row[cj[j]];
         }
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < kWinAhead; ++u) {
             const int r = r0 + u;
             if (r >= len) break;
             if (r == 0 || s_key[r] != s_key[r - 1]) {
@@ -549,7 +574,7 @@ __global__ __launch_bounds__(256) void emb_segment_apply_v_k(float* gw, const fl
     const int64_t p = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
     if (p >= n || !(p == 0 || keys[p] != keys[p - 1])) return;
     const uint32_t v = keys[p];
-    const int64_t end = emb_upper(keys, p + 1, n, v);
+    const int64_t end = emb_upper_wave(keys, p + 1, n, v, lane);
     const int64_t d4 = dim / 4;
     float4* row = reinterpret_cast<float4*>(gw + (int64_t)v * dim);
     float4 acc[NC];
