@@ -42,6 +42,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
@@ -152,39 +153,39 @@ __device__ __forceinline__ bf16x8 accfrag(const f32x16& a, int s) {
 // (id % NCH) ^ swz(row) of row id / NCH; a wave's 64 slots are one 1 KB
 // global_load_lds).  Rows past T repeat row T - 1: callers mask every score
 // of such a row to probability 0.
-template <int HD, int ROWS>
-struct TileU {  // 16-byte chunks per thread of a ROWS-row tile
-    static constexpr int N = (ROWS * Geo<HD>::NCH + kThreads - 1) / kThreads;
+template <int HD, int ROWS, int NTH = kThreads>
+struct TileU {  // 16-byte chunks per thread of a ROWS-row tile (NTH threads per workgroup)
+    static constexpr int N = (ROWS * Geo<HD>::NCH + NTH - 1) / NTH;
 };
 
 // This thread's chunk byte offsets from a tile's first row (row stride rs
 // elements), fixed for the kernel: a whole tile's DMA is then a wave-uniform
 // base address plus these offsets (no per-copy address arithmetic).
-template <int HD, int ROWS = kTile, int N>
+template <int HD, int ROWS = kTile, int N, int NTH = kThreads>
 __device__ __forceinline__ void tile_offsets(unsigned (&off)[N], int64_t rs) {
     using G = Geo<HD>;
-    static_assert(N == TileU<HD, ROWS>::N, "offset count");
+    static_assert(N == TileU<HD, ROWS, NTH>::N, "offset count");
 #pragma unroll
-    for (int i = 0; i < TileU<HD, ROWS>::N; ++i) {
-        const int id = i * kThreads + threadIdx.x;
+    for (int i = 0; i < N; ++i) {
+        const int id = i * NTH + threadIdx.x;
         const int r = id / G::NCH, c = (id % G::NCH) ^ G::swz(r);
         off[i] = (unsigned)(r * (int)rs + c * 8) * 2u;
     }
 }
 
-template <int HD, int ROWS = kTile, int N>
+template <int HD, int ROWS = kTile, int N, int NTH = kThreads>
 __device__ __forceinline__ void dma_tile(bf16* dst, const bf16* base, int64_t rs, int row0, int T,
                                          const unsigned (&off)[N]) {
     using G = Geo<HD>;
-    static_assert(N == TileU<HD, ROWS>::N, "offset count");
+    static_assert(N == TileU<HD, ROWS, NTH>::N, "offset count");
     constexpr int UNITS = ROWS * G::NCH;  // a multiple of 64: the guards below are wave-uniform
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     if (row0 + ROWS <= T) {
         const bf16* tb = base + (int64_t)row0 * rs;
 #pragma unroll
-        for (int i = 0; i < TileU<HD, ROWS>::N; ++i) {
-            if (UNITS % kThreads != 0 && i * kThreads + wave * kWave >= UNITS) break;
-            dma16s(tb, off[i], lds_addr(dst + (i * kThreads + wave * kWave) * 8));
+        for (int i = 0; i < N; ++i) {
+            if (UNITS % NTH != 0 && i * NTH + wave * kWave >= UNITS) break;
+            dma16s(tb, off[i], lds_addr(dst + (i * NTH + wave * kWave) * 8));
         }
         return;
     }
@@ -194,12 +195,12 @@ __device__ __forceinline__ void dma_tile(bf16* dst, const bf16* base, int64_t rs
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
 #pragma unroll
-    for (int i = 0; i < TileU<HD, ROWS>::N; ++i) {
-        const int id = i * kThreads + tid;
-        if (UNITS % kThreads != 0 && i * kThreads + wave * kWave >= UNITS) break;
+    for (int i = 0; i < N; ++i) {
+        const int id = i * NTH + tid;
+        if (UNITS % NTH != 0 && i * NTH + wave * kWave >= UNITS) break;
         const int r = id / G::NCH, c = (id % G::NCH) ^ G::swz(r);
         const int row = row0 + r < T ? row0 + r : T - 1;
-        dma16(base + (int64_t)row * rs + c * 8, lds_addr(dst + (i * kThreads + wave * kWave) * 8));
+        dma16(base + (int64_t)row * rs + c * 8, lds_addr(dst + (i * NTH + wave * kWave) * 8));
     }
 }
 
@@ -641,23 +642,62 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
 // in registers; the own V rows live in LDS (read as row fragments for dP), so
 // two workgroups still share a CU without spills.  Q / dO stream in 32-row
 // tiles (double-buffered, direct-to-LDS).
+//
+// With WDS the bf16 dS that feeds the dK product is also stored, for the dQ
+// product to read instead of recomputing S and dP (fa2_dq_ds_k), in the
+// layout that product's B operand takes: per (b, h), 32-query block q32 and
+// 32-key block k32, 1024 bf16 at ds + ((bh * n32 + q32) * n32 + k32) * 1024
+// (n32 = ceil(T / 32)), fragment s (keys 16 s..16 s+15) at s * 512, lane l
+// (query l % 32) at 8 l: keys 16 s + 4 (l / 32) + {0..3, 8..11}.  A wave turns
+// its 32 x 32 dS^T block (lane = key) around through 2.3 KB of wave-private
+// LDS and stores the two fragments as two 1 KB rows of 16-byte pieces.  Only
+// blocks that block_hidden keeps are written (masked scores as zeros), and
+// only those are used by the dQ product.
 constexpr int kDkvTile = 32;
+constexpr int kDsBlock = 32 * 32;  // bf16 elements per stored dS block
+constexpr int kStgLd = 36;         // staging row stride (bf16): 8-byte writes and transposed reads conflict-free
 
-template <int HD>
+// The 32 x 32 score block of keys kb0..kb0+31 and queries q0..q0+31 (both
+// 32-aligned) holds no visible score: the dK / dV kernel skips it and writes
+// no dS for it, and the dQ-from-dS kernel skips it too.
+__device__ __forceinline__ bool block_hidden(int kb0, int q0, int T, int window) {
+    return q0 + 31 < kb0 || (window > 0 && q0 > kb0 + 31 + window) || kb0 >= T || q0 >= T;
+}
+
+// s_waitcnt vmcnt(N) (lgkmcnt / expcnt left open).
+template <int N>
+__device__ __forceinline__ void wait_vmem_n() {
+    static_assert(N >= 0 && N < 16, "vmcnt");
+    __builtin_amdgcn_s_waitcnt(N | 0x0F70);
+}
+
+// Transposed fragment of an unswizzled 32-row tile with row stride ld (bf16):
+// lane l gets column l % 32, rows 16 s + 4 (l / 32) + {0..3, 8..11}.
+__device__ __forceinline__ bf16x8 trfrag_plain(const bf16* t, int ld, int s, int lane) {
+    const int g = lane >> 4, src = lane & 15;
+    const int row = 16 * s + 4 * (g >> 1) + (src >> 2), col = 16 * (g & 1) + 4 * (src & 3);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + row * ld + col));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + (row + 8) * ld + col));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+template <int HD, bool WDS>
 constexpr size_t dkv_fused_lds() {
     const size_t tiles = 4 * (size_t)kDkvTile * HD * sizeof(bf16);  // Q, dO x 2 stages
     const size_t own_v = (size_t)kOwn * HD * sizeof(bf16);
     const size_t ld = 4 * kDkvTile * sizeof(float);                 // LSE, D x 2 stages
-    const size_t loop = tiles + own_v + ld;
+    const size_t stg = WDS ? 4 * 32 * kStgLd * sizeof(bf16) : 0;   // dS transpose staging, per wave
+    const size_t loop = tiles + own_v + ld + stg;
     const size_t stage = 4 * 32 * 68 * sizeof(float);               // store_rows staging
     return loop > stage ? loop : stage;
 }
 
-template <int HD>
+template <int HD, bool WDS>
 __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, RowOut out_v, const bf16* q,
                                                                const bf16* k, const bf16* v, const bf16* dout,
-                                                               const float* lse, const float* dbuf, int B, int T,
-                                                               int H, int window, float scale_log2, float scale) {
+                                                               const float* lse, const float* dbuf, bf16* ds_out,
+                                                               int B, int T, int H, int window, float scale_log2,
+                                                               float scale) {
     using G = Geo<HD>;
     constexpr int KT = kDkvTile, TT = KT * HD;  // rows, bf16 elements per streamed tile
     extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -665,6 +705,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
     bf16* const sV = lds + 4 * TT;                        // the workgroup's own 128 V rows
     float* const sLD = reinterpret_cast<float*>(sV + kOwn * HD);
     const int lane = threadIdx.x % kWave, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    bf16* const stg = reinterpret_cast<bf16*>(sLD + 4 * KT) + wave * 32 * kStgLd;
     const int nkb = (T + kOwn - 1) / kOwn;
     int bh, kblk;
     block_coords(nkb, B * H, false, bh, kblk);
@@ -724,8 +765,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
         const bf16* sD = lds + (2 * cur + 1) * TT;
         const float* sL = sLD + cur * 2 * KT;
         const float* sDl = sL + KT;
-        const bool skip = qt0 + KT - 1 < kw || (window > 0 && qt0 > kw + 31 + window) || kw >= T;
-        if (!skip) {
+        if (!block_hidden(kw, qt0, T, window)) {
             const int lane = opaque_lane(threadIdx.x % kWave);
             const unsigned rb = rowbase<HD>(lane);
             unsigned tb0, tb1;
@@ -765,6 +805,28 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
                 ds(std::false_type{});
             else
                 ds(std::true_type{});
+            if constexpr (WDS) {
+                // dS^T block (lane = key; queries 16 st + 4 g + {0..3, 8..11}, g =
+                // lane / 32) into the staging rows, read back transposed (lane =
+                // query) and stored as the block's two B fragments
+                const int g = lane >> 5;
+                bf16* const srow = stg + (lane & 31) * kStgLd + 4 * g;
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    const bf16x8 f = accfrag(dp, st);
+                    *reinterpret_cast<bf16x4*>(srow + 16 * st) = __builtin_shufflevector(f, f, 0, 1, 2, 3);
+                    *reinterpret_cast<bf16x4*>(srow + 16 * st + 8) = __builtin_shufflevector(f, f, 4, 5, 6, 7);
+                }
+                const int n32 = (T + 31) / 32;
+                bf16* const blk = ds_out + (((int64_t)bh * n32 + qt0 / 32) * n32 + kw / 32) * kDsBlock + lane * 8;
+                // nontemporal: 1 KB of whole lines per store, streamed past L2
+                // (allocated there, they evicted the Q / dO tiles the other
+                // workgroups of the head still read)
+#pragma unroll
+                for (int st = 0; st < 2; ++st)
+                    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, trfrag_plain(stg, kStgLd, st, lane)),
+                                                reinterpret_cast<u32x4*>(blk + st * 512));
+            }
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
                 const bf16x8 fp = accfrag(s, st), fs = accfrag(dp, st);
@@ -775,12 +837,165 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dkv_fused_k(RowOut out_k, Row
                 }
             }
         }
-        wait_vmem();  // this thread's part of the next Q / dO tile (and its LSE / D) has landed
+        // this thread's part of the next Q / dO tile (and its LSE / D) has
+        // landed; the tile's two dS stores, issued after those loads, may
+        // still be in flight (vmcnt counts in issue order)
+        if (WDS && !block_hidden(kw, qt0, T, window))
+            wait_vmem_n<2>();
+        else
+            wait_vmem();
         __syncthreads();
     }
     float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 68;
     store_rows<HD>(at_head(out_v, b, h, T, HD), kw, T, adv, 1.0f, scratch, lane);
     store_rows<HD>(at_head(out_k, b, h, T, HD), kw, T, adk, scale, scratch, lane);
+}
+
+// ============================ backward: dQ from stored dS ============================
+// dQ^T += K^T dS^T over the key tiles of the query block, from the dS blocks
+// the dK / dV kernel stored (the same bf16 values the dQ kernel above forms
+// for its product, so this is that kernel's result without the S / dP
+// recompute).  One 512-thread workgroup per CU owns 256 queries (8 waves x
+// 32) and streams 64-key tiles through three LDS stages, loads two tiles
+// ahead: the K rows (natural, swizzled; K^T read transposed as in fa2_dq_k)
+// and each wave's four dS fragments of the tile (4 KB contiguous in global
+// memory and in LDS, read back as 16 bytes per lane).  Every load is a
+// direct-to-LDS copy, so all vector-memory waits are the explicit ones below.
+constexpr int kDqThreads = 512, kDqOwn = 256, kDqStages = 3;
+
+template <int HD>
+constexpr size_t dq_ds_lds() {
+    const size_t stage = ((size_t)Geo<HD>::TILE + (kDqThreads / kWave) * 2 * kDsBlock) * sizeof(bf16);
+    const size_t tiles = kDqStages * stage;
+    const size_t out = (kDqThreads / kWave) * 32 * 68 * sizeof(float);  // store_rows staging
+    return tiles > out ? tiles : out;
+}
+
+template <int HD>
+__global__ __launch_bounds__(kDqThreads) void fa2_dq_ds_k(RowOut dq, const bf16* k, const bf16* ds, int B, int T,
+                                                         int H, int window, float scale) {
+    using G = Geo<HD>;
+    constexpr int NK = TileU<HD, kTile, kDqThreads>::N;
+    constexpr bool K_ALL = kTile * G::NCH % kDqThreads == 0;  // every wave copies part of each K tile
+    constexpr int SDS = 2 * kDsBlock;              // bf16 elements of one wave's dS fragments per tile (4 KB)
+    constexpr int STG = G::TILE + (kDqThreads / kWave) * SDS;  // bf16 elements per stage
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    bf16* const lds = reinterpret_cast<bf16*>(smem_raw);
+    const int lane = threadIdx.x % kWave, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int nqb = (T + kDqOwn - 1) / kDqOwn, n32 = (T + 31) / 32;
+    int bh, qb;
+    block_coords(nqb, B * H, true, bh, qb);
+    const int b = bh / H, h = bh % H;
+    const int q0 = qb * kDqOwn, qw = q0 + wave * 32;
+    const int64_t rs = (int64_t)H * HD;
+    const int64_t boff = (int64_t)b * T * rs + (int64_t)h * HD;
+    // this wave's row of dS blocks (a wave past T reads row n32 - 1, unused)
+    const bf16* const dsw = ds + ((int64_t)bh * n32 + (qw / 32 < n32 ? qw / 32 : n32 - 1)) * n32 * kDsBlock;
+
+    f32x16 acc[G::DT];
+#pragma unroll
+    for (int dt = 0; dt < G::DT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[dt][e] = 0.f;
+
+    int kstart = 0;
+    if (window > 0) kstart = q0 - window > 0 ? q0 - window : 0;
+    kstart = (kstart / kTile) * kTile;
+    const int kend = (q0 + kDqOwn < T) ? q0 + kDqOwn : T;
+    const int ntiles = kend > kstart ? (kend - kstart + kTile - 1) / kTile : 0;
+
+    unsigned toff[NK];
+    tile_offsets<HD, kTile, NK, kDqThreads>(toff, rs);
+    const unsigned lds0 = lds_addr(smem_raw);
+    // tile t into stage t % 3: K rows, then this wave's 4 KB of dS fragments
+    // (blocks k32, k32 + 1 of its row).  A block hidden from this wave is
+    // never written and never read back: its copy is pointed at the row's
+    // block kstart / 32 (already fetched by the first tile, so an L2 hit)
+    // instead, which keeps the per-tile copy count the same for every wave.
+    const int kdummy = kstart / 32;
+    auto load = [&](int t) {
+        const int kv0 = kstart + t * kTile, stage = t % kDqStages;
+        dma_tile<HD, kTile, NK, kDqThreads>(lds + stage * STG, k + boff, rs, kv0, T, toff);
+        const unsigned dl = lds0 + (unsigned)(stage * STG + G::TILE + wave * SDS) * 2u;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const int blk = block_hidden(kv0 + 32 * kb, qw, T, window) ? kdummy : kv0 / 32 + kb;
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+                dma16s(dsw + (int64_t)blk * kDsBlock, (unsigned)(s * 1024 + lane * 16), dl + (2 * kb + s) * 1024);
+        }
+    };
+    // wait for the older of two tiles in flight: a wave's vector-memory
+    // instructions per tile are its K copies (NK, or none for the waves that
+    // a small K tile leaves out) and its 4 dS copies
+    auto wait_older = [&]() {
+        if (K_ALL || wave * kWave < kTile * G::NCH)
+            wait_vmem_n<NK + 4>();
+        else
+            wait_vmem_n<4>();
+    };
+    if (ntiles > 0) load(0);
+    if (ntiles > 1) load(1);
+    if (ntiles > 1)
+        wait_older();
+    else
+        wait_vmem();
+    __syncthreads();
+    for (int it = 0; it < ntiles; ++it) {
+        const int kv0 = kstart + it * kTile;
+        if (it + 2 < ntiles) load(it + 2);  // into the stage tile it - 1 used (retired by the last barrier)
+        const bf16* sK = lds + (it % kDqStages) * STG;
+        const bf16* sS = sK + G::TILE + wave * SDS;
+        const int lane = opaque_lane(threadIdx.x % kWave);
+        unsigned tb0, tb1;
+        trbase<HD>(lane, tb0, tb1);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            if (block_hidden(kv0 + 32 * kb, qw, T, window)) continue;  // wave-uniform
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const bf16x8 db = *reinterpret_cast<const bf16x8*>(sS + (2 * kb + st) * 512 + lane * 8);
+#pragma unroll
+                for (int dt = 0; dt < G::DT; ++dt) acc[dt] = mma(trfrag_x<HD>(sK, tb0, tb1, kb, st, dt), db, acc[dt]);
+            }
+        }
+        // tile it + 1 has landed (this thread's part); tile it + 2's loads may
+        // still be in flight
+        if (it + 2 < ntiles)
+            wait_older();
+        else
+            wait_vmem();
+        __syncthreads();
+    }
+    float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 68;
+    store_rows<HD>(at_head(dq, b, h, T, HD), qw, T, acc, scale, scratch, lane);
+}
+
+// D = rowsum(dO * O) (ops.mojo:329-346) per (token, head) row: bf16 dO (the
+// values the dP products read) against fp32 O, HD / 16 lanes per row, each
+// 16 columns (all six 16-byte loads issued before the arithmetic), then a
+// butterfly over those lanes.
+template <int HD>
+__global__ __launch_bounds__(kThreads) void fa2_d_k(float* d, const float* o, const bf16* dout, int64_t rows) {
+    constexpr int LPR = HD / 16;
+    const int64_t gid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t r = gid / LPR;
+    const int c = (int)(gid % LPR);
+    float sum = 0.f;
+    if (r < rows) {
+        const bf16* gp = dout + r * HD + c * 16;
+        const float* op = o + r * HD + c * 16;
+        const bf16x8 g0 = *reinterpret_cast<const bf16x8*>(gp), g1 = *reinterpret_cast<const bf16x8*>(gp + 8);
+        const float4 a0 = *reinterpret_cast<const float4*>(op), a1 = *reinterpret_cast<const float4*>(op + 4);
+        const float4 a2 = *reinterpret_cast<const float4*>(op + 8), a3 = *reinterpret_cast<const float4*>(op + 12);
+        sum = a0.x * (float)g0[0] + a0.y * (float)g0[1] + a0.z * (float)g0[2] + a0.w * (float)g0[3] +
+              a1.x * (float)g0[4] + a1.y * (float)g0[5] + a1.z * (float)g0[6] + a1.w * (float)g0[7];
+        sum += a2.x * (float)g1[0] + a2.y * (float)g1[1] + a2.z * (float)g1[2] + a2.w * (float)g1[3] +
+               a3.x * (float)g1[4] + a3.y * (float)g1[5] + a3.z * (float)g1[6] + a3.w * (float)g1[7];
+    }
+#pragma unroll
+    for (int m = LPR / 2; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, kWave);
+    if (r < rows && c == 0) d[r] = sum;
 }
 
 template <int HD>
@@ -812,12 +1027,61 @@ int32_t flash_hd(hipStream_t st, AttnOp op, float* o1, float* o2, const FlashOut
     }
     const RowOut ov{o2, fo.b2, rs, brs, nullptr, nullptr, 0, 1};
     const RowOut ok{o1, fo.b1, rs, brs, fo.cos_t, fo.sin_t, 0, period};
-    fa2_dkv_fused_k<HD><<<grid, kThreads, dkv_fused_lds<HD>(), st>>>(ok, ov, q, k, v, dout, lse, dbuf, B, T, H,
-                                                                    window, scale_log2, scale);
+    if (fo.ds)
+        fa2_dkv_fused_k<HD, true><<<grid, kThreads, dkv_fused_lds<HD, true>(), st>>>(ok, ov, q, k, v, dout, lse, dbuf, fo.ds,
+                                                                          B, T, H, window, scale_log2, scale);
+    else
+        fa2_dkv_fused_k<HD, false><<<grid, kThreads, dkv_fused_lds<HD, false>(), st>>>(ok, ov, q, k, v, dout, lse, dbuf,
+                                                                           nullptr, B, T, H, window, scale_log2, scale);
     return check_launch("flash_attn_bwd_dkv (bf16 operands)");
 }
 
+template <int HD>
+int32_t flash_dq_ds_hd(hipStream_t st, const FlashOut& fo, const bf16* k, const bf16* ds, int B, int T, int H,
+                       int window) {
+    const float scale = 1.0f / sqrtf((float)HD);
+    const unsigned grid = (unsigned)(((T + kDqOwn - 1) / kDqOwn) * B * H);
+    const int64_t rs = (int64_t)H * HD, brs = fo.brs > 0 ? fo.brs : rs;
+    const int64_t period = fo.period > 0 ? fo.period : (int64_t)B * T;
+    const RowOut out{nullptr, fo.b1, rs, brs, fo.cos_t, fo.sin_t, 0, period};
+    fa2_dq_ds_k<HD><<<grid, kDqThreads, dq_ds_lds<HD>(), st>>>(out, k, ds, B, T, H, window, scale);
+    return check_launch("flash_attn_bwd_dq from dS (bf16 operands)");
+}
+
 }  // namespace
+
+int64_t flash_ds_elems(int64_t B, int64_t T, int64_t H) {
+    return B * H * ((T + 31) / 32) * ((T + 31) / 32) * kDsBlock;
+}
+
+int32_t flash_d_bf16(hipStream_t st, float* d, const float* o, const bf16* dout, int64_t B, int64_t T, int64_t H,
+                     int64_t HD) {
+    const int64_t rows = B * T * H;
+    if (rows <= 0) return AR_OK;
+    if (HD != 32 && HD != 64 && HD != 128)
+        return set_error(AR_EUNSUPPORTED, "flash attention D: head_dim %lld not in {32, 64, 128}", (long long)HD);
+    const int64_t threads = rows * (HD / 16);
+    const unsigned grid = (unsigned)((threads + kThreads - 1) / kThreads);
+    if (HD == 128) fa2_d_k<128><<<grid, kThreads, 0, st>>>(d, o, dout, rows);
+    else if (HD == 64) fa2_d_k<64><<<grid, kThreads, 0, st>>>(d, o, dout, rows);
+    else fa2_d_k<32><<<grid, kThreads, 0, st>>>(d, o, dout, rows);
+    return check_launch("flash attention D (bf16 dO)");
+}
+
+int32_t flash_dq_ds_bf16(hipStream_t st, const FlashOut& fo, const bf16* k, const bf16* ds, int64_t B, int64_t T,
+                         int64_t H, int64_t HD, int64_t window) {
+    if (B <= 0 || T <= 0 || H <= 0) return B == 0 || T == 0 ? AR_OK : set_error(AR_EINVAL, "flash attention: bad shape");
+    if (((T + kOwn - 1) / kOwn) * B * H > 0x7fffffff || T > (1 << 30))
+        return set_error(AR_EINVAL, "flash attention: shape too large");
+    if (!fo.b1 || !ds) return set_error(AR_EINVAL, "flash attention dQ from dS: null output / dS");
+    const int w = window > T ? (int)T : (int)window;
+    switch (HD) {
+        case 32: return flash_dq_ds_hd<32>(st, fo, k, ds, (int)B, (int)T, (int)H, w);
+        case 64: return flash_dq_ds_hd<64>(st, fo, k, ds, (int)B, (int)T, (int)H, w);
+        case 128: return flash_dq_ds_hd<128>(st, fo, k, ds, (int)B, (int)T, (int)H, w);
+        default: return set_error(AR_EUNSUPPORTED, "flash attention: head_dim %lld not in {32, 64, 128}", (long long)HD);
+    }
+}
 
 int32_t flash_attn_bf16(hipStream_t st, AttnOp op, float* o1, float* o2, const FlashOut& fo, const bf16* q,
                         const bf16* k, const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int64_t B,

@@ -88,10 +88,22 @@ struct FlashOut {
     // the dK / dV kernel, instead of being read from dbuf.
     const float* o_for_d = nullptr;
     float* d_out = nullptr;
+    // DKV only: when set, the bf16 dS tiles are stored here for flash_dq_ds_bf16
+    // (flash_ds_elems(B, T, H) bf16 elements).
+    bf16* ds = nullptr;
 };
 int32_t flash_attn_bf16(hipStream_t st, AttnOp op, float* o1, float* o2, const FlashOut& fo, const bf16* q,
                         const bf16* k, const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int64_t B,
                         int64_t T, int64_t H, int64_t HD, int64_t window);
+// dS workspace size (bf16 elements) of a DKV launch with FlashOut::ds.
+int64_t flash_ds_elems(int64_t B, int64_t T, int64_t H);
+// D = rowsum(dO * O) per (token, head) from bf16 dO [B, T, H, hd] and fp32 O.
+int32_t flash_d_bf16(hipStream_t st, float* d, const float* o, const bf16* dout, int64_t B, int64_t T, int64_t H,
+                     int64_t HD);
+// dQ = scale * dS K from the dS tiles a DKV launch stored (same window): bf16
+// to fo.b1 (row stride fo.brs), inverse-rope rotated with fo.cos_t / sin_t.
+int32_t flash_dq_ds_bf16(hipStream_t st, const FlashOut& fo, const bf16* k, const bf16* ds, int64_t B, int64_t T,
+                         int64_t H, int64_t HD, int64_t window);
 
 // ---- element-wise (ar_elementwise.hip) ----
 int32_t rope(hipStream_t st, float* out, const float* in, const float* cos_t, const float* sin_t, int64_t nt,

@@ -86,6 +86,9 @@ struct ar_gpt {
     ar::bf16* qkv = nullptr;  // [BT, 3C] q | k | v GEMM output
     ar::bf16 *x_final_b = nullptr, *grad_logits_b = nullptr, *grad_xb = nullptr, *grad_x_norm_b = nullptr,
              *grad_h = nullptr, *grad_attn_out_b = nullptr, *grad_qkv = nullptr;
+    // bf16 dS tiles of one layer's attention backward (written by the dK / dV
+    // kernel, read by the dQ product)
+    ar::bf16* ds_buf = nullptr;
     float grad_logits_scale = 0.f;  // loss_scale baked into grad_logits_b
     bool grad_logits_valid = false;
     // step-dependent optimizer scalars in device memory (StepScalars)
@@ -233,6 +236,14 @@ int32_t attention_b(ar_gpt* m, AttnOp op, float* o1, float* o2, const FlashOut& 
     attn_prof_end(m, e, op, ws);
     return r;
 }
+// dQ from the dS tiles of the preceding DKV launch (profiling class
+// flash_attn_bwd_dq, one product: 2 B H hd keys flops).
+int32_t attention_dq_ds(ar_gpt* m, const FlashOut& fo, const bf16* k, int64_t ws) {
+    const int e = prof_begin(m);
+    const int32_t r = flash_dq_ds_bf16(m->st, fo, k, m->ds_buf, m->B, m->T, m->c.n_head, m->c.head_dim, ws);
+    prof_end(m, e, 4, 2.0 * m->B * m->c.n_head * m->c.head_dim * attn_keys(m, ws));
+    return r;
+}
 // bf16-step GEMMs (operand storage per flag; profiling class cls).
 int32_t gemm_b(ar_gpt* m, int cls, int layout, void* C, bool cb, const void* X, bool xb, const void* W, bool wb,
                int64_t M, int64_t N, int64_t K, bool accumulate) {
@@ -367,6 +378,7 @@ static int32_t gpt_build(ar_gpt* m) {
         AR_TRY(balloc(&m->grad_h, BT * F));
         AR_TRY(balloc(&m->grad_attn_out_b, BT * C));
         AR_TRY(balloc(&m->grad_qkv, BT * 3 * C));
+        AR_TRY(balloc(&m->ds_buf, flash_ds_elems(m->B, m->T, H)));
     } else {
         FALLOC(m->rms_qk, BT * H);
         FALLOC(m->proj_out, BT * C);
@@ -617,23 +629,22 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
         const int64_t ws = window_size(c, i);
         // dQ | dK | dV straight into the packed bf16 [BT, 3C] buffer, dQ / dK
         // rotated back by the inverse rope (rope_bwd; Q6: q/k norm backward skipped).
-        // The dQ kernel also forms D = rowsum(dO * O) (precompute_d) into d_buf for dK / dV.
+        // D = rowsum(dO * O) (precompute_d) first; the dK / dV kernel stores its
+        // bf16 dS tiles and dQ = dS K is formed from them (no S / dP recompute).
         FlashOut fo;
         fo.brs = 3 * C;
         fo.cos_t = m->rope_cos;
         fo.sin_t = m->rope_sin;
         fo.period = m->period;
-        fo.b1 = m->grad_qkv;
-        fo.o_for_d = b.attn_out;
-        fo.d_out = m->d_buf;
-        AR_TRY(attention_b(m, AttnOp::DQ, nullptr, nullptr, fo, b.q, b.k, b.v, m->grad_attn_out_b, b.lse, m->d_buf,
-                           ws));
-        fo.o_for_d = nullptr;
-        fo.d_out = nullptr;
         fo.b1 = m->grad_qkv + C;
         fo.b2 = m->grad_qkv + 2 * C;
+        fo.ds = m->ds_buf;
+        AR_TRY(flash_d_bf16(st, m->d_buf, b.attn_out, m->grad_attn_out_b, m->B, m->T, H, hd));
         AR_TRY(attention_b(m, AttnOp::DKV, nullptr, nullptr, fo, b.q, b.k, b.v, m->grad_attn_out_b, b.lse, m->d_buf,
                            ws));
+        fo.b1 = m->grad_qkv;
+        fo.b2 = nullptr;
+        AR_TRY(attention_dq_ds(m, fo, b.k, ws));
         // ve_apply_bwd from the bf16 dV
         if (ve)
             AR_TRY(ve_bwd(st, m->grad_ve, m->grad_gate, m->grad_qkv + 2 * C, 3 * C, b.gate, P(m, m->i_ve[i]), inputs,
