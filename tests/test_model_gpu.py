@@ -183,6 +183,23 @@ def test_wide_model(precision):
         _check(init_o, init_g, res, TOL_BF16, TOL_BF16, UPD_BF16)
 
 
+ODD = dict(sequence_len=100, vocab_size=512, n_layer=4, n_head=4, n_kv_head=4, n_embd=128, head_dim=32,
+           kv_dim=128)
+
+
+@pytest.mark.parametrize("precision", [0, 1])
+def test_odd_length_small_heads(precision):
+    """T = 100 (not a multiple of the 32-, 64- or 128-row attention blocks),
+    head_dim 32 and windows of 50 (three layers) and 100: the attention
+    kernels' partial last blocks, rows past T and windows shorter than a tile,
+    in the whole step against the oracle."""
+    init_o, init_g, res = _run(ODD, 2, 100, precision, 100, 5, steps=2)
+    if precision == 0:
+        _check(init_o, init_g, res, TOL_FP32, GRAD_FP32, UPD_FP32)
+    else:
+        _check(init_o, init_g, res, TOL_BF16, TOL_BF16, UPD_BF16)
+
+
 @pytest.mark.parametrize("precision", [0, 1])
 def test_config4_dims_two_steps(precision):
     """BASELINE config 4 at its real dimensions (depth 8, d512, 4 x 128 heads,
