@@ -516,8 +516,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_fwd_k(RowOut out, float* lse,
 template <int HD>
 __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q, const bf16* k, const bf16* v,
                                                      const bf16* dout, const float* lse, const float* dbuf,
-                                                     const float* o_for_d, float* d_out, int B, int T, int H,
-                                                     int window, float scale_log2, float scale) {
+                                                     int B, int T, int H, int window, float scale_log2,
+                                                     float scale) {
     using G = Geo<HD>;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     bf16* const lds = reinterpret_cast<bf16*>(smem_raw);  // stage s: K at 2 s TILE, V at (2 s + 1) TILE
@@ -535,27 +535,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa2_dq_k(RowOut dq, const bf16* q
     own_frags<HD>(df, dout + boff, rs, my_q, T, lane);
     const int64_t bth = ((int64_t)b * T + (my_q < T ? my_q : 0)) * H + h;
     const float my_lse2 = lse[bth] * kLog2e;
-    float my_D;
-    if (o_for_d) {
-        // D = rowsum(dO * O): this lane's half row (d = 16 ks + 8 (lane / 32) + 0..7) of the bf16 dO
-        // fragments against fp32 O, then the partner lane's half
-        float dsum = 0.f;
-        if (my_q < T) {
-            const float* orow = o_for_d + boff + (int64_t)my_q * rs + (lane >> 5) * 8;
-#pragma unroll
-            for (int ks = 0; ks < G::KSTEPS; ++ks) {
-                const float4 o0 = *reinterpret_cast<const float4*>(orow + ks * 16);
-                const float4 o1 = *reinterpret_cast<const float4*>(orow + ks * 16 + 4);
-                dsum += o0.x * (float)df[ks][0] + o0.y * (float)df[ks][1] + o0.z * (float)df[ks][2] +
-                        o0.w * (float)df[ks][3] + o1.x * (float)df[ks][4] + o1.y * (float)df[ks][5] +
-                        o1.z * (float)df[ks][6] + o1.w * (float)df[ks][7];
-            }
-        }
-        my_D = dsum + __shfl_xor(dsum, 32, kWave);
-        if (lane < 32 && my_q < T) d_out[bth] = my_D;
-    } else {
-        my_D = dbuf[bth];
-    }
+    const float my_D = dbuf[bth];
 
     f32x16 acc[G::DT];
 #pragma unroll
@@ -1021,8 +1001,8 @@ int32_t flash_hd(hipStream_t st, AttnOp op, float* o1, float* o2, const FlashOut
     const int64_t period = fo.period > 0 ? fo.period : (int64_t)B * T;
     if (op == AttnOp::DQ) {
         const RowOut out{o1, fo.b1, rs, brs, fo.cos_t, fo.sin_t, 0, period};
-        fa2_dq_k<HD><<<grid, kThreads, fa2_lds<HD>(false), st>>>(out, q, k, v, dout, lse, dbuf, fo.o_for_d, fo.d_out,
-                                                                 B, T, H, window, scale_log2, scale);
+        fa2_dq_k<HD><<<grid, kThreads, fa2_lds<HD>(false), st>>>(out, q, k, v, dout, lse, dbuf, B, T, H, window,
+                                                                 scale_log2, scale);
         return check_launch("flash_attn_bwd_dq (bf16 operands)");
     }
     const RowOut ov{o2, fo.b2, rs, brs, nullptr, nullptr, 0, 1};

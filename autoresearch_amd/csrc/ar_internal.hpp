@@ -83,11 +83,6 @@ struct FlashOut {
     const float* cos_t = nullptr;
     const float* sin_t = nullptr;
     int64_t period = 0;
-    // DQ only: when set, D = rowsum(dO * O) is formed in the dQ kernel from O
-    // (fp32, [B, T, H, hd]) and the lane's own dO row, written to d_out for
-    // the dK / dV kernel, instead of being read from dbuf.
-    const float* o_for_d = nullptr;
-    float* d_out = nullptr;
     // DKV only: when set, the bf16 dS tiles are stored here for flash_dq_ds_bf16
     // (flash_ds_elems(B, T, H) bf16 elements).
     bf16* ds = nullptr;
