@@ -223,8 +223,13 @@ constexpr int lds_tile_elems() {
 }
 
 // ============================ forward ============================
+// Occupancy: two workgroups per CU (<= 256 registers; the tiles take 67.6 KB
+// of LDS at hd 128).  Unbounded, the compiler took 264 registers at hd 128 and
+// the kernel ran one wave per SIMD, with every tile load exposed.  The
+// backward kernels get the same bound up to hd 64; at hd 128 their own-row
+// fragments alone (2 x 64 registers) leave no room for it without spills.
 template <bool BF16, int HD, typename TIN>
-__global__ __launch_bounds__(kThreads) void fa_fwd_k(float* out, float* lse, const TIN* q, const TIN* k, const TIN* v,
+__global__ __launch_bounds__(kThreads, 2) void fa_fwd_k(float* out, float* lse, const TIN* q, const TIN* k, const TIN* v,
                                                      int B, int T, int H, int window, float scale_log2) {
     using A = AT<BF16>;
     using LT = typename A::LT;
@@ -336,7 +341,7 @@ __global__ __launch_bounds__(kThreads) void fa_fwd_k(float* out, float* lse, con
 
 // ============================ backward: dQ ============================
 template <bool BF16, int HD, typename TIN>
-__global__ __launch_bounds__(kThreads) void fa_bwd_dq_k(float* dq, const TIN* q, const TIN* k, const TIN* v,
+__global__ __launch_bounds__(kThreads, HD <= 64 ? 2 : 1) void fa_bwd_dq_k(float* dq, const TIN* q, const TIN* k, const TIN* v,
                                                         const TIN* dout, const float* lse, const float* dbuf, int B,
                                                         int T, int H, int window, float scale_log2, float scale) {
     using A = AT<BF16>;
@@ -417,7 +422,7 @@ __global__ __launch_bounds__(kThreads) void fa_bwd_dq_k(float* dq, const TIN* q,
 
 // ============================ backward: dK, dV ============================
 template <bool BF16, int HD, typename TIN>
-__global__ __launch_bounds__(kThreads) void fa_bwd_dkv_k(float* dk, float* dv, const TIN* q, const TIN* k,
+__global__ __launch_bounds__(kThreads, HD <= 64 ? 2 : 1) void fa_bwd_dkv_k(float* dk, float* dv, const TIN* q, const TIN* k,
                                                          const TIN* v, const TIN* dout, const float* lse,
                                                          const float* dbuf, int B, int T, int H, int window,
                                                          float scale_log2, float scale) {
