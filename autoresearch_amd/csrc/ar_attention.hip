@@ -341,7 +341,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa_fwd_k(float* out, float* lse, 
 
 // ============================ backward: dQ ============================
 template <bool BF16, int HD, typename TIN>
-__global__ __launch_bounds__(kThreads, HD <= 64 ? 2 : 1) void fa_bwd_dq_k(float* dq, const TIN* q, const TIN* k, const TIN* v,
+__global__ __launch_bounds__(kThreads, 2) void fa_bwd_dq_k(float* dq, const TIN* q, const TIN* k, const TIN* v,
                                                         const TIN* dout, const float* lse, const float* dbuf, int B,
                                                         int T, int H, int window, float scale_log2, float scale) {
     using A = AT<BF16>;
@@ -380,39 +380,38 @@ __global__ __launch_bounds__(kThreads, HD <= 64 ? 2 : 1) void fa_bwd_dq_k(float*
         __syncthreads();
         const bool skip = kv0 > qw + 31 || (window > 0 && kv0 + kTile - 1 < qw - window) || qw >= T;
         if (!skip) {
-            f32x16 s[2], dp[2];
+            // one 32-key half at a time: only one S / dP pair is live, which
+            // keeps the hd-128 kernel within 256 registers beside the own-row
+            // Q and dO fragments and the dQ accumulators
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
+                f32x16 s, dp;
 #pragma unroll
-                for (int e = 0; e < 16; ++e) s[kb][e] = dp[kb][e] = 0.f;
+                for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.f;
                 const LT* krow = sK + (kb * 32 + (lane & 31)) * LDN;
                 const LT* vrow = sV + (kb * 32 + (lane & 31)) * LDN;
 #pragma unroll
                 for (int ks = 0; ks < HD / A::KS; ++ks) {
-                    s[kb] = A::mma(A::rowfrag(krow, ks, lane), qf[ks], s[kb]);
-                    dp[kb] = A::mma(A::rowfrag(vrow, ks, lane), df[ks], dp[kb]);
+                    s = A::mma(A::rowfrag(krow, ks, lane), qf[ks], s);
+                    dp = A::mma(A::rowfrag(vrow, ks, lane), df[ks], dp);
                 }
-            }
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int key = kv0 + kb * 32 + acc_row(e, lane);
                     const bool ok = key <= my_q && key < T && my_q < T && (window <= 0 || key >= my_q - window);
-                    const float p = ok ? exp2f(s[kb][e] * scale_log2 - my_lse2) : 0.f;
-                    s[kb][e] = p * (dp[kb][e] - my_D);
+                    const float p = ok ? exp2f(s[e] * scale_log2 - my_lse2) : 0.f;
+                    s[e] = p * (dp[e] - my_D);
                 }
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
                 for (int st = 0; st < A::STEPS32; ++st) {
-                    const typename A::Frag db = A::accfrag(s[kb], st);
+                    const typename A::Frag db = A::accfrag(s, st);
 #pragma unroll
                     for (int dt = 0; dt < HD / 32; ++dt) {
                         const int d = dt * 32 + (lane & 31);
                         acc[dt] = A::mma(A::permfrag(sK, LDN, sKT, d, kb, st, lane), db, acc[dt]);
                     }
                 }
+            }
         }
         __syncthreads();
     }
