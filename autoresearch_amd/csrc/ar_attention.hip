@@ -420,8 +420,12 @@ __global__ __launch_bounds__(kThreads, 2) void fa_bwd_dq_k(float* dq, const TIN*
 }
 
 // ============================ backward: dK, dV ============================
-template <bool BF16, int HD, typename TIN>
-__global__ __launch_bounds__(kThreads, HD <= 64 ? 2 : 1) void fa_bwd_dkv_k(float* dk, float* dv, const TIN* q, const TIN* k,
+// MODE 0 forms dK and dV in one pass.  At hd 128 the own K and V fragments and
+// both accumulator sets (4 x 64 registers) leave no room for two workgroups
+// per CU, so dV (MODE 1: S, P, dV) and dK (MODE 2: S, dP, dS, dK) run as two
+// launches that each recompute S, and each fits 256 registers.
+template <bool BF16, int HD, typename TIN, int MODE>
+__global__ __launch_bounds__(kThreads, (HD <= 64 || MODE != 0) ? 2 : 1) void fa_bwd_dkv_k(float* dk, float* dv, const TIN* q, const TIN* k,
                                                          const TIN* v, const TIN* dout, const float* lse,
                                                          const float* dbuf, int B, int T, int H, int window,
                                                          float scale_log2, float scale) {
@@ -442,9 +446,10 @@ __global__ __launch_bounds__(kThreads, HD <= 64 ? 2 : 1) void fa_bwd_dkv_k(float
     const int64_t rs = (int64_t)H * HD;
     const int64_t boff = (int64_t)b * T * rs + (int64_t)h * HD;
 
-    typename A::Frag kf[HD / A::KS], vf[HD / A::KS];
+    constexpr bool DOV = MODE != 2, DOK = MODE != 1;
+    typename A::Frag kf[HD / A::KS], vf[DOK ? HD / A::KS : 1];
     load_bfrags<BF16, HD>(kf, k + boff, rs, my_k, T, lane);
-    load_bfrags<BF16, HD>(vf, v + boff, rs, my_k, T, lane);
+    if constexpr (DOK) load_bfrags<BF16, HD>(vf, v + boff, rs, my_k, T, lane);
 
     f32x16 dka[HD / 32], dva[HD / 32];
 #pragma unroll
@@ -467,7 +472,9 @@ __global__ __launch_bounds__(kThreads, HD <= 64 ? 2 : 1) void fa_bwd_dkv_k(float
         __syncthreads();
         const bool skip = qt0 + kTile - 1 < kw || (window > 0 && qt0 > kw + 31 + window) || kw >= T;
         if (!skip) {
-#pragma unroll
+            // the two 32-query halves one after the other (not unrolled: at
+            // hd 128 the dK launch has no registers for two halves in flight)
+#pragma unroll 1
             for (int qb = 0; qb < 2; ++qb) {
                 f32x16 s, dp;
 #pragma unroll
@@ -477,9 +484,11 @@ __global__ __launch_bounds__(kThreads, HD <= 64 ? 2 : 1) void fa_bwd_dkv_k(float
 #pragma unroll
                 for (int ks = 0; ks < HD / A::KS; ++ks) {
                     s = A::mma(A::rowfrag(qrow, ks, lane), kf[ks], s);
-                    dp = A::mma(A::rowfrag(drow, ks, lane), vf[ks], dp);
+                    if constexpr (DOK) dp = A::mma(A::rowfrag(drow, ks, lane), vf[ks], dp);
                 }
-                // s, dp: lane holds key my_k, queries qt0 + 32qb + acc_row(e)
+                // s, dp: lane holds key my_k, queries qt0 + 32qb + acc_row(e).
+                // MODE 0 keeps P and dS; the split launches each need one of
+                // them and form it in place in s.
                 f32x16 p, ds;
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
@@ -487,18 +496,24 @@ __global__ __launch_bounds__(kThreads, HD <= 64 ? 2 : 1) void fa_bwd_dkv_k(float
                     const int qq = qt0 + qr;
                     const bool ok = my_k <= qq && qq < T && my_k < T && (window <= 0 || my_k >= qq - window);
                     const float pv = ok ? exp2f(s[e] * scale_log2 - sL[qr]) : 0.f;
-                    p[e] = pv;
-                    ds[e] = pv * (dp[e] - sDl[qr]);
+                    if constexpr (MODE == 0) {
+                        p[e] = pv;
+                        ds[e] = pv * (dp[e] - sDl[qr]);
+                    } else if constexpr (MODE == 1) {
+                        s[e] = pv;
+                    } else {
+                        s[e] = pv * (dp[e] - sDl[qr]);
+                    }
                 }
 #pragma unroll
                 for (int st = 0; st < A::STEPS32; ++st) {
-                    const typename A::Frag pb = A::accfrag(p, st);
-                    const typename A::Frag db = A::accfrag(ds, st);
+                    const typename A::Frag pb = A::accfrag(MODE == 0 ? p : s, st);
+                    const typename A::Frag db = A::accfrag(MODE == 0 ? ds : s, st);
 #pragma unroll
                     for (int dt = 0; dt < HD / 32; ++dt) {
                         const int d = dt * 32 + (lane & 31);
-                        dva[dt] = A::mma(A::permfrag(sD, LDN, sDT, d, qb, st, lane), pb, dva[dt]);
-                        dka[dt] = A::mma(A::permfrag(sQ, LDN, sQT, d, qb, st, lane), db, dka[dt]);
+                        if constexpr (DOV) dva[dt] = A::mma(A::permfrag(sD, LDN, sDT, d, qb, st, lane), pb, dva[dt]);
+                        if constexpr (DOK) dka[dt] = A::mma(A::permfrag(sQ, LDN, sQT, d, qb, st, lane), db, dka[dt]);
                     }
                 }
             }
@@ -506,8 +521,8 @@ __global__ __launch_bounds__(kThreads, HD <= 64 ? 2 : 1) void fa_bwd_dkv_k(float
         __syncthreads();
     }
     float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 36;
-    store_rows_T<HD>(dk + boff, rs, kw, T, dka, scale, scratch, lane);
-    store_rows_T<HD>(dv + boff, rs, kw, T, dva, 1.0f, scratch, lane);
+    if constexpr (DOK) store_rows_T<HD>(dk + boff, rs, kw, T, dka, scale, scratch, lane);
+    if constexpr (DOV) store_rows_T<HD>(dv + boff, rs, kw, T, dva, 1.0f, scratch, lane);
 }
 
 template <bool BF16, int HD>
@@ -555,8 +570,15 @@ static int32_t attn_dispatch_hd(hipStream_t st, AttnOp op, float* o1, float* o2,
         return check_launch("flash_attn_bwd_dq");
     }
     const size_t lds = dkv_lds<BF16, HD>();
-    fa_bwd_dkv_k<BF16, HD, TIN><<<grid, kThreads, lds, st>>>(o1, o2, q, k, v, dout, lse, dbuf, B, T, H, window,
-                                                             scale_log2, scale);
+    if (HD == 128) {
+        fa_bwd_dkv_k<BF16, HD, TIN, 1><<<grid, kThreads, lds, st>>>(o1, o2, q, k, v, dout, lse, dbuf, B, T, H,
+                                                                    window, scale_log2, scale);
+        fa_bwd_dkv_k<BF16, HD, TIN, 2><<<grid, kThreads, lds, st>>>(o1, o2, q, k, v, dout, lse, dbuf, B, T, H,
+                                                                    window, scale_log2, scale);
+    } else {
+        fa_bwd_dkv_k<BF16, HD, TIN, 0><<<grid, kThreads, lds, st>>>(o1, o2, q, k, v, dout, lse, dbuf, B, T, H,
+                                                                    window, scale_log2, scale);
+    }
     return check_launch("flash_attn_bwd_dkv");
 }
 
