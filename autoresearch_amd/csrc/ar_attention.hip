@@ -40,6 +40,12 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 __device__ __forceinline__ int acc_row(int v, int lane) { return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); }
 
+// 2^x with the hardware's v_exp_f32 (1 ulp): results below 2^-126
+// (probabilities that change no fp32 sum they enter) flush to zero, and
+// 2^-inf = 0.  The library exp2f spends several instructions and registers per
+// element on denormal results.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 template <bool BF16> struct AT;
 
 template <> struct AT<true> {
@@ -287,13 +293,13 @@ __global__ __launch_bounds__(kThreads, 2) void fa_fwd_k(float* out, float* lse, 
             mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
             const float m_new = fmaxf(m, mt);
             const float m_use = m_new == -INFINITY ? 0.f : m_new;
-            const float alpha = exp2f(m - m_use);
+            const float alpha = exp2_hw(m - m_use);
             float rsum = 0.f;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const float p = exp2f(s[kb][e] - m_use);
+                    const float p = exp2_hw(s[kb][e] - m_use);
                     s[kb][e] = p;
                     rsum += p;
                 }
@@ -380,10 +386,10 @@ __global__ __launch_bounds__(kThreads, 2) void fa_bwd_dq_k(float* dq, const TIN*
         __syncthreads();
         const bool skip = kv0 > qw + 31 || (window > 0 && kv0 + kTile - 1 < qw - window) || qw >= T;
         if (!skip) {
-            // one 32-key half at a time: only one S / dP pair is live, which
-            // keeps the hd-128 kernel within 256 registers beside the own-row
-            // Q and dO fragments and the dQ accumulators
-#pragma unroll
+            // one 32-key half at a time (not unrolled): only one S / dP pair is
+            // live, which keeps the hd-128 kernel within 256 registers beside
+            // the own-row Q and dO fragments and the dQ accumulators
+#pragma unroll 1
             for (int kb = 0; kb < 2; ++kb) {
                 f32x16 s, dp;
 #pragma unroll
@@ -399,7 +405,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa_bwd_dq_k(float* dq, const TIN*
                 for (int e = 0; e < 16; ++e) {
                     const int key = kv0 + kb * 32 + acc_row(e, lane);
                     const bool ok = key <= my_q && key < T && my_q < T && (window <= 0 || key >= my_q - window);
-                    const float p = ok ? exp2f(s[e] * scale_log2 - my_lse2) : 0.f;
+                    const float p = ok ? exp2_hw(s[e] * scale_log2 - my_lse2) : 0.f;
                     s[e] = p * (dp[e] - my_D);
                 }
 #pragma unroll
@@ -495,7 +501,7 @@ __global__ __launch_bounds__(kThreads, (HD <= 64 || MODE != 0) ? 2 : 1) void fa_
                     const int qr = qb * 32 + acc_row(e, lane);
                     const int qq = qt0 + qr;
                     const bool ok = my_k <= qq && qq < T && my_k < T && (window <= 0 || my_k >= qq - window);
-                    const float pv = ok ? exp2f(s[e] * scale_log2 - sL[qr]) : 0.f;
+                    const float pv = ok ? exp2_hw(s[e] * scale_log2 - sL[qr]) : 0.f;
                     if constexpr (MODE == 0) {
                         p[e] = pv;
                         ds[e] = pv * (dp[e] - sDl[qr]);
