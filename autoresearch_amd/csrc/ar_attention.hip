@@ -163,6 +163,53 @@ __device__ __forceinline__ void load_tile(typename AT<BF16>::LT* nat, typename A
     }
 }
 
+// load_tile split in two, so that a tile's global loads can be issued before
+// the MFMAs of the previous tile and written to LDS after them: TileVals holds
+// this thread's items of one tile (fp32 compute: 2 x 4 rows x 4 columns).
+// Rows at or beyond T load row T - 1 and are zeroed by a select, so no load
+// sits in a branch.
+template <bool BF16, int HD, typename TIN>
+struct TileVals {
+    using A = AT<BF16>;
+    using LT = typename A::LT;
+    static constexpr int CW = A::CW, ITEMS = (kTile / 4) * (HD / CW), NIT = (ITEMS + kThreads - 1) / kThreads;
+    static_assert(!BF16 && sizeof(TIN) == 4, "fp32 operands, fp32 compute");
+    static_assert(ITEMS % kWave == 0, "whole waves per item pass");
+    LT v[NIT][4][CW];
+    __device__ __forceinline__ void load(const TIN* base, int64_t rs, int row0, int T) {
+#pragma unroll
+        for (int n = 0; n < NIT; ++n) {
+            const int it = n * kThreads + threadIdx.x;
+            if (ITEMS % kThreads != 0 && it >= ITEMS) break;  // whole waves (ITEMS is a multiple of 64)
+            const int r4 = it % (kTile / 4), dc = (it / (kTile / 4)) * CW;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = row0 + r4 * 4 + i;
+                const TIN* src = base + (int64_t)(row < T ? row : T - 1) * rs + dc;
+#pragma unroll
+                for (int j = 0; j < CW; j += 4) *reinterpret_cast<float4*>(&v[n][i][j]) =
+                    *reinterpret_cast<const float4*>(src + j);
+            }
+        }
+    }
+    __device__ __forceinline__ void write(LT* nat, int row0, int T) const {
+        constexpr int LDN = HD + A::PADN;
+#pragma unroll
+        for (int n = 0; n < NIT; ++n) {
+            const int it = n * kThreads + threadIdx.x;
+            if (ITEMS % kThreads != 0 && it >= ITEMS) break;
+            const int r4 = it % (kTile / 4), dc = (it / (kTile / 4)) * CW;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool in = row0 + r4 * 4 + i < T;
+                float4 x = *reinterpret_cast<const float4*>(&v[n][i][0]);
+                if (!in) x = make_float4(0.f, 0.f, 0.f, 0.f);
+                *reinterpret_cast<float4*>(nat + (r4 * 4 + i) * LDN + dc) = x;
+            }
+        }
+    }
+};
+
 // Load the 32 rows [r0, r0+32) of an operand as B fragments (lane row r0 + l%32).
 template <bool BF16, int HD, typename TIN>
 __device__ __forceinline__ void load_bfrags(typename AT<BF16>::Frag (&f)[HD / AT<BF16>::KS], const TIN* base,
@@ -264,10 +311,21 @@ __global__ __launch_bounds__(kThreads, 2) void fa_fwd_k(float* out, float* lse, 
     if (window > 0) kstart = q0 - window > 0 ? q0 - window : 0;
     kstart = (kstart / kTile) * kTile;
     const int kend = (q0 + kOwn < T) ? q0 + kOwn : T;
+    // the next tile's K / V rows are loaded into registers while this tile's
+    // MFMAs run, and written to LDS after the barrier that ends them
+    TileVals<BF16, HD, TIN> nk, nv;
+    if (kstart < kend) {
+        nk.load(k + boff, rs, kstart, T);
+        nv.load(v + boff, rs, kstart, T);
+    }
     for (int kv0 = kstart; kv0 < kend; kv0 += kTile) {
-        load_tile<BF16, HD>(sK, nullptr, k + boff, rs, kv0, T, false);
-        load_tile<BF16, HD>(A::TRANS ? nullptr : sV, A::TRANS ? sVT : nullptr, v + boff, rs, kv0, T, true);
+        nk.write(sK, kv0, T);
+        nv.write(sV, kv0, T);
         __syncthreads();
+        if (kv0 + kTile < kend) {
+            nk.load(k + boff, rs, kv0 + kTile, T);
+            nv.load(v + boff, rs, kv0 + kTile, T);
+        }
         const bool skip = kv0 > qw + 31 || (window > 0 && kv0 + kTile - 1 < qw - window) || qw >= T;
         if (!skip) {
             f32x16 s[2];
