@@ -524,16 +524,49 @@ __global__ __launch_bounds__(kThreads, (HD <= 64 || MODE != 0) ? 2 : 1) void fa_
     const int qstart = (k0 / kTile) * kTile;
     int qend = T;
     if (window > 0 && k0 + kOwn - 1 + window + 1 < T) qend = k0 + kOwn - 1 + window + 1;
-    for (int qt0 = qstart; qt0 < qend; qt0 += kTile) {
-        load_tile<BF16, HD>(sQ, sQT, q + boff, rs, qt0, T, true);
-        load_tile<BF16, HD>(sD, sDT, dout + boff, rs, qt0, T, true);
+    // Launches with registers to spare (the dV launch at hd 128, every one
+    // below) load the next Q / dO tile and its LSE / D values into registers
+    // while this tile's MFMAs run; the hd-128 dK launch has none and loads each
+    // tile when it starts.
+    constexpr bool PF = MODE == 1 || HD <= 64;
+    TileVals<BF16, HD, TIN> nq, nd;
+    float nl = 0.f, ndl = 0.f;
+    auto ld_load = [&](int qt0) {  // LSE / D of query qt0 + tid (row 0 past T: masked)
         if (threadIdx.x < kTile) {
             const int qq = qt0 + threadIdx.x;
             const int64_t bth = ((int64_t)b * T + (qq < T ? qq : 0)) * H + h;
-            sL[threadIdx.x] = lse[bth] * kLog2e;
-            sDl[threadIdx.x] = dbuf[bth];
+            nl = lse[bth];
+            ndl = dbuf[bth];
+        }
+    };
+    if constexpr (PF) {
+        if (qstart < qend) {
+            nq.load(q + boff, rs, qstart, T);
+            nd.load(dout + boff, rs, qstart, T);
+            ld_load(qstart);
+        }
+    }
+    for (int qt0 = qstart; qt0 < qend; qt0 += kTile) {
+        if constexpr (PF) {
+            nq.write(sQ, qt0, T);
+            nd.write(sD, qt0, T);
+        } else {
+            load_tile<BF16, HD>(sQ, sQT, q + boff, rs, qt0, T, true);
+            load_tile<BF16, HD>(sD, sDT, dout + boff, rs, qt0, T, true);
+            ld_load(qt0);
+        }
+        if (threadIdx.x < kTile) {
+            sL[threadIdx.x] = nl * kLog2e;
+            sDl[threadIdx.x] = ndl;
         }
         __syncthreads();
+        if constexpr (PF) {
+            if (qt0 + kTile < qend) {
+                nq.load(q + boff, rs, qt0 + kTile, T);
+                nd.load(dout + boff, rs, qt0 + kTile, T);
+                ld_load(qt0 + kTile);
+            }
+        }
         const bool skip = qt0 + kTile - 1 < kw || (window > 0 && qt0 > kw + 31 + window) || kw >= T;
         if (!skip) {
             // the two 32-query halves one after the other (not unrolled: at
