@@ -23,6 +23,7 @@
 // and quirks are kept; only where each bf16 rounding happens moves (to the
 // producer instead of each consumer).
 #include <math.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -124,6 +125,10 @@ struct ar_gpt {
 };
 
 namespace {
+
+// Largest attention-backward dS workspace the bf16 step allocates (4 GiB:
+// BASELINE config 5 takes 3.2 GB).
+constexpr int64_t kDsMaxBytes = int64_t(4) << 30;
 
 bool has_ve(const ar_gpt_config& c, int64_t i) { return (i % 2) == ((c.n_layer - 1) % 2); }  // config.mojo:45-47
 int64_t window_size(const ar_gpt_config& c, int64_t i) {                                      // config.mojo:49-55
@@ -378,7 +383,13 @@ static int32_t gpt_build(ar_gpt* m) {
         AR_TRY(balloc(&m->grad_h, BT * F));
         AR_TRY(balloc(&m->grad_attn_out_b, BT * C));
         AR_TRY(balloc(&m->grad_qkv, BT * 3 * C));
-        AR_TRY(balloc(&m->ds_buf, flash_ds_elems(m->B, m->T, H)));
+        // The dS workspace grows with T^2; past kDsMaxBytes (or the
+        // AR_ATTN_DS_MAX_BYTES override) the step keeps the dQ kernel that
+        // recomputes S and dP instead.
+        int64_t ds_max = kDsMaxBytes;
+        if (const char* e = getenv("AR_ATTN_DS_MAX_BYTES")) ds_max = strtoll(e, nullptr, 10);
+        const int64_t ds_elems = flash_ds_elems(m->B, m->T, H);
+        if (ds_elems * (int64_t)sizeof(bf16) <= ds_max) AR_TRY(balloc(&m->ds_buf, ds_elems));
     } else {
         FALLOC(m->rms_qk, BT * H);
         FALLOC(m->proj_out, BT * C);
@@ -631,6 +642,8 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
         // rotated back by the inverse rope (rope_bwd; Q6: q/k norm backward skipped).
         // D = rowsum(dO * O) (precompute_d) first; the dK / dV kernel stores its
         // bf16 dS tiles and dQ = dS K is formed from them (no S / dP recompute).
+        // Without the dS workspace (long sequences) the dQ kernel recomputes S
+        // and dP.
         FlashOut fo;
         fo.brs = 3 * C;
         fo.cos_t = m->rope_cos;
@@ -644,7 +657,12 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
                            ws));
         fo.b1 = m->grad_qkv;
         fo.b2 = nullptr;
-        AR_TRY(attention_dq_ds(m, fo, b.k, ws));
+        fo.ds = nullptr;
+        if (m->ds_buf)
+            AR_TRY(attention_dq_ds(m, fo, b.k, ws));
+        else
+            AR_TRY(attention_b(m, AttnOp::DQ, nullptr, nullptr, fo, b.q, b.k, b.v, m->grad_attn_out_b, b.lse,
+                               m->d_buf, ws));
         // ve_apply_bwd from the bf16 dV
         if (ve)
             AR_TRY(ve_bwd(st, m->grad_ve, m->grad_gate, m->grad_qkv + 2 * C, 3 * C, b.gate, P(m, m->i_ve[i]), inputs,

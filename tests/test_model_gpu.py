@@ -200,6 +200,16 @@ def test_odd_length_small_heads(precision):
         _check(init_o, init_g, res, TOL_BF16, TOL_BF16, UPD_BF16)
 
 
+@pytest.mark.parametrize("cfg,T", [(WIDE, 256), (ODD, 100)], ids=["wide", "odd"])
+def test_bf16_attention_backward_without_ds_workspace(cfg, T, monkeypatch):
+    """The bf16 step's fallback for long sequences: with the dS workspace cap
+    at 0 bytes the model keeps the dQ kernel that recomputes S and dP (and D
+    from its own kernel); the whole step must still match the oracle."""
+    monkeypatch.setenv("AR_ATTN_DS_MAX_BYTES", "0")
+    init_o, init_g, res = _run(cfg, 2, T, 1, T, 3, steps=2)
+    _check(init_o, init_g, res, TOL_BF16, TOL_BF16, UPD_BF16)
+
+
 @pytest.mark.parametrize("precision", [0, 1])
 def test_config4_dims_two_steps(precision):
     """BASELINE config 4 at its real dimensions (depth 8, d512, 4 x 128 heads,
