@@ -1153,6 +1153,16 @@ int32_t gemm_epilogue(hipStream_t st, int layout, int epi, void* C, int c_bf16, 
 #undef AR_GE
 }
 
+int32_t gemm_f32_add(hipStream_t st, bool bf, float* C, const float* X, const float* W, const float* R, int64_t M,
+                     int64_t N, int64_t K) {
+    if (bf)
+        return gemm_launch<float, float, float, true, true, true>(st, C, X, W, M, N, K, K, K, N, false, 1, nullptr,
+                                                                  "linear_fwd_add", 1, 0, 0, 0, EPI_ADD, R, nullptr,
+                                                                  0.f);
+    return gemm_launch<float, float, float, true, true, false>(st, C, X, W, M, N, K, K, K, N, false, 1, nullptr,
+                                                               "linear_fwd_add", 1, 0, 0, 0, EPI_ADD, R, nullptr, 0.f);
+}
+
 int32_t gemm_f32(hipStream_t st, int layout, bool bf, float* C, const float* X, const float* W, int64_t M, int64_t N,
                  int64_t K, bool accumulate, int64_t splits, float* partial) {
     if (layout == 0) {

@@ -21,6 +21,10 @@ int64_t gemm_auto_splits(int layout, bool bf16, bool bf16_operands, int64_t M, i
 int64_t gemm_partial_elems(int layout, int64_t M, int64_t N, int64_t K, int64_t splits);
 int32_t gemm_f32(hipStream_t st, int layout, bool bf16, float* C, const float* X, const float* W, int64_t M,
                  int64_t N, int64_t K, bool accumulate, int64_t splits, float* partial);
+// Y = X W^T (layout 0 of gemm_f32) added to R in the epilogue: C = R + Y,
+// the add in fp32 exactly as a separate residual add does it (R may alias C).
+int32_t gemm_f32_add(hipStream_t st, bool bf16, float* C, const float* X, const float* W, const float* R, int64_t M,
+                     int64_t N, int64_t K);
 // Same, with each operand stored as bf16 (flag set) or fp32; bf16 compute.
 int32_t gemm_bf16io(hipStream_t st, int layout, void* C, int c_bf16, const void* X, int x_bf16, const void* W,
                     int w_bf16, int64_t M, int64_t N, int64_t K, bool accumulate, int64_t splits, float* partial);

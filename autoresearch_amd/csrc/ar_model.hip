@@ -70,7 +70,7 @@ struct ar_gpt {
     float *rope_cos = nullptr, *rope_sin = nullptr;
     int64_t rope_rows = 0;
     // activations
-    float *x0, *x, *rms_qk, *proj_out, *mlp_out, *logits, *loss, *mean_loss, *x_final, *rms_final, *d_buf;
+    float *x0, *x, *rms_qk, *logits, *loss, *mean_loss, *x_final, *rms_final, *d_buf;
     std::vector<LayerBufs> L;
     // gradients of activations
     float *grad_x, *grad_x0, *grad_logits, *grad_attn_out, *grad_q, *grad_k, *grad_v, *grad_x_norm, *grad_tmp,
@@ -194,6 +194,14 @@ int32_t linear(ar_gpt* m, float* out, const float* in, const float* w, int64_t M
     const int32_t r = gemm_f32(m->st, 0, m->bf16, out, in, w, M, N, K, false, 1, nullptr);
     prof_end(m, e, 0, 2.0 * M * N * K);
     return r;
+}
+// out = r + in @ w^T (r may alias out): the residual add in the product's epilogue, the same fp32 add
+int32_t linear_add(ar_gpt* m, float* out, const float* in, const float* w, const float* r, int64_t M, int64_t N,
+                   int64_t K) {
+    const int e = prof_begin(m);
+    const int32_t rc = gemm_f32_add(m->st, m->bf16, out, in, w, r, M, N, K);
+    prof_end(m, e, 0, 2.0 * M * N * K);
+    return rc;
 }
 int32_t linear_dx(ar_gpt* m, float* dx, const float* dy, const float* w, int64_t M, int64_t N, int64_t K) {
     const int e = prof_begin(m);
@@ -392,8 +400,6 @@ static int32_t gpt_build(ar_gpt* m) {
         if (ds_elems * (int64_t)sizeof(bf16) <= ds_max) AR_TRY(balloc(&m->ds_buf, ds_elems));
     } else {
         FALLOC(m->rms_qk, BT * H);
-        FALLOC(m->proj_out, BT * C);
-        FALLOC(m->mlp_out, BT * C);
         FALLOC(m->x_final, BT * C);
         m->L.resize(Lr);
         for (int64_t i = 0; i < Lr; ++i) {
@@ -712,13 +718,12 @@ static int32_t forward_fp32(ar_gpt* m, const int64_t* inputs, const int64_t* tar
         AR_TRY(ar_rmsnorm_fwd(st, b.k, m->rms_qk, b.k, BT * H, hd));
         AR_TRY(attention(m, AttnOp::FWD, b.attn_out, b.lse, b.q, b.k, b.v, nullptr, nullptr, nullptr,
                          window_size(c, i)));
-        AR_TRY(linear(m, m->proj_out, b.attn_out, P(m, m->i_proj[i]), BT, C, C));
-        AR_TRY(ar_add_residual_fwd(st, m->x, b.x, m->proj_out, BT * C));
+        // x = x_layer + attn_out @ c_proj^T (add_residual_fwd in the product's epilogue)
+        AR_TRY(linear_add(m, m->x, b.attn_out, P(m, m->i_proj[i]), b.x, BT, C, C));
         AR_TRY(ar_rmsnorm_fwd(st, b.xn_mlp, b.rms_mlp, m->x, BT, C));
         AR_TRY(linear(m, b.mlp_hidden, b.xn_mlp, P(m, m->i_fc[i]), BT, F, C));
         AR_TRY(ar_relu_squared_fwd(st, b.mlp_act, b.mlp_hidden, BT * F));
-        AR_TRY(linear(m, m->mlp_out, b.mlp_act, P(m, m->i_mlpp[i]), BT, C, F));
-        AR_TRY(ar_add_residual_fwd(st, m->x, m->x, m->mlp_out, BT * C));
+        AR_TRY(linear_add(m, m->x, b.mlp_act, P(m, m->i_mlpp[i]), m->x, BT, C, F));
     }
     // m->x is the saved pre-final x.
     AR_TRY(ar_rmsnorm_fwd(st, m->x_final, m->rms_final, m->x, BT, C));
