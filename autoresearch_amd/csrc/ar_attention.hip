@@ -651,8 +651,8 @@ namespace ar {
 template <bool BF16, int HD, typename TIN>
 static int32_t attn_dispatch_hd(hipStream_t st, AttnOp op, float* o1, float* o2, const TIN* q, const TIN* k,
                                 const TIN* v, const TIN* dout, const float* lse, const float* dbuf, int B, int T, int H,
-                                int window) {
-    const float scale = 1.0f / sqrtf((float)HD);
+                                int window, float sc) {
+    const float scale = sc > 0.f ? sc : 1.0f / sqrtf((float)HD);
     const float scale_log2 = scale * kLog2e;
     dim3 grid((unsigned)((T + kOwn - 1) / kOwn), (unsigned)(B * H));
     if (op == AttnOp::FWD) {
@@ -682,15 +682,15 @@ static int32_t attn_dispatch_hd(hipStream_t st, AttnOp op, float* o1, float* o2,
 template <bool BF16, typename TIN>
 int32_t attn_dispatch(hipStream_t st, AttnOp op, float* o1, float* o2, const TIN* q, const TIN* k, const TIN* v,
                       const TIN* dout, const float* lse, const float* dbuf, int64_t B, int64_t T, int64_t H,
-                      int64_t HD, int64_t window) {
+                      int64_t HD, int64_t window, float scale) {
     if (HD > 128) return set_error(AR_EUNSUPPORTED, "flash attention: head_dim %lld > 128", (long long)HD);
     if (B <= 0 || T <= 0 || H <= 0) return B == 0 || T == 0 ? AR_OK : set_error(AR_EINVAL, "flash attention: bad shape");
     if (B * H > 65535 || T > (1 << 30)) return set_error(AR_EINVAL, "flash attention: shape too large");
     const int w = window > (int64_t)T ? (int)T : (int)window;  // a window >= T is full causal
     switch (HD) {
-        case 32: return attn_dispatch_hd<BF16, 32, TIN>(st, op, o1, o2, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
-        case 64: return attn_dispatch_hd<BF16, 64, TIN>(st, op, o1, o2, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
-        case 128: return attn_dispatch_hd<BF16, 128, TIN>(st, op, o1, o2, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
+        case 32: return attn_dispatch_hd<BF16, 32, TIN>(st, op, o1, o2, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w, scale);
+        case 64: return attn_dispatch_hd<BF16, 64, TIN>(st, op, o1, o2, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w, scale);
+        case 128: return attn_dispatch_hd<BF16, 128, TIN>(st, op, o1, o2, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w, scale);
         default: return set_error(AR_EUNSUPPORTED, "flash attention: head_dim %lld not in {32, 64, 128}", (long long)HD);
     }
 }
@@ -706,23 +706,87 @@ static __host__ __device__ inline bool al16(const void* p) { return (reinterpret
             if (!p || !al16(p)) return ar::set_error(AR_EINVAL, "%s: null or unaligned pointer", __func__); \
     } while (0)
 
-extern "C" int32_t ar_flash_attn_fwd(ar_stream_t stream, float* output, float* lse_out, const float* q, const float* k,
-                                     const float* v, int64_t B, int64_t T, int64_t num_heads, int64_t head_dim,
-                                     int64_t window_size) {
-    AR_ATTN_PTRS(output, q, k, v);
-    AR_CHECK_ARG(lse_out != nullptr, "flash_attn_fwd: null lse");
-    return ar::attn_dispatch<false, float>(S(stream), ar::AttnOp::FWD, output, lse_out, q, k, v, nullptr, nullptr,
-                                           nullptr, B, T, num_heads, head_dim, window_size);
-}
-// bf16 compute: operands rounded to bf16 once (into the library workspace),
-// then the bf16-operand kernels of ar_flash.hip.
+// ---- any head_dim <= 128 (ops.mojo:267 accepts every head_dim up to 128) ----
+// The tiled kernels exist for head_dim 32, 64 and 128.  Another head_dim runs
+// them at the next of those sizes on copies of q, k, v (and dO) whose rows are
+// zero past head_dim, with the softmax scale of the real head_dim: the zero
+// columns add nothing to any score or to D, and the output columns past
+// head_dim (O, dQ, dK, dV) are exact zeros that the copy back drops.
 namespace {
+
+bool native_hd(int64_t hd) { return hd == 32 || hd == 64 || hd == 128; }
+int64_t padded_hd(int64_t hd) { return hd <= 32 ? 32 : (hd <= 64 ? 64 : 128); }
+size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
+
+template <typename TO>
+__global__ void pad_rows_k(TO* dst, const float* src, int64_t rows, int hd, int hdp) {
+    const int64_t n = rows * hdp;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / hdp;
+        const int d = (int)(i - r * hdp);
+        dst[i] = (TO)(d < hd ? src[r * hd + d] : 0.0f);
+    }
+}
+__global__ void unpad_rows_k(float* dst, const float* src, int64_t rows, int hd, int hdp) {
+    const int64_t n = rows * hd;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / hd;
+        dst[i] = src[r * hdp + (i - r * hd)];
+    }
+}
+
+// One attention op at a head_dim outside {32, 64, 128}: fp32 operands (bf = false)
+// or bf16-rounded copies (bf = true).  in = {q, k, v[, dO]}.
+int32_t attn_padded(ar_stream_t stream, bool bf, ar::AttnOp op, float* o1, float* o2, const float* const* in,
+                    const float* lse, const float* dbuf, int64_t B, int64_t T, int64_t H, int64_t hd,
+                    int64_t window) {
+    if (hd <= 0 || hd > 128)
+        return ar::set_error(AR_EUNSUPPORTED, "flash attention: head_dim %lld not in [1, 128]", (long long)hd);
+    if (B <= 0 || T <= 0 || H <= 0) return B == 0 || T == 0 ? AR_OK : ar::set_error(AR_EINVAL, "flash attention: bad shape");
+    const int64_t hdp = padded_hd(hd), rows = B * T * H, n = rows * hdp;
+    const int nin = op == ar::AttnOp::FWD ? 3 : 4;
+    const int nout = op == ar::AttnOp::DKV ? 2 : 1;
+    const size_t in_b = align256((size_t)n * (bf ? sizeof(ar::bf16) : sizeof(float)));
+    const size_t out_b = align256((size_t)n * sizeof(float));
+    int32_t st;
+    char* w = (char*)ar::workspace(ar::S(stream), nin * in_b + nout * out_b, &st);
+    if (!w) return st;
+    const unsigned g = ar::flat_grid(n, 256);
+    void* pin[4] = {nullptr, nullptr, nullptr, nullptr};
+    for (int i = 0; i < nin; ++i) {
+        pin[i] = w + i * in_b;
+        if (bf) pad_rows_k<ar::bf16><<<g, 256, 0, ar::S(stream)>>>((ar::bf16*)pin[i], in[i], rows, (int)hd, (int)hdp);
+        else pad_rows_k<float><<<g, 256, 0, ar::S(stream)>>>((float*)pin[i], in[i], rows, (int)hd, (int)hdp);
+    }
+    int32_t r = ar::check_launch("flash attention: pad head_dim");
+    if (r) return r;
+    float* p1 = (float*)(w + nin * in_b);
+    float* p2 = op == ar::AttnOp::DKV ? (float*)(w + nin * in_b + out_b) : o2;  // FWD: o2 = LSE, unpadded
+    const float scale = 1.0f / sqrtf((float)hd);
+    if (bf)
+        r = ar::flash_attn_bf16(ar::S(stream), op, p1, p2, ar::FlashOut{}, (const ar::bf16*)pin[0],
+                                (const ar::bf16*)pin[1], (const ar::bf16*)pin[2], (const ar::bf16*)pin[3], lse, dbuf,
+                                B, T, H, hdp, window, scale);
+    else
+        r = ar::attn_dispatch<false, float>(ar::S(stream), op, p1, p2, (const float*)pin[0], (const float*)pin[1],
+                                            (const float*)pin[2], (const float*)pin[3], lse, dbuf, B, T, H, hdp,
+                                            window, scale);
+    if (r) return r;
+    const unsigned go = ar::flat_grid(rows * hd, 256);
+    unpad_rows_k<<<go, 256, 0, ar::S(stream)>>>(o1, p1, rows, (int)hd, (int)hdp);
+    if (op == ar::AttnOp::DKV) unpad_rows_k<<<go, 256, 0, ar::S(stream)>>>(o2, p2, rows, (int)hd, (int)hdp);
+    return ar::check_launch("flash attention: unpad head_dim");
+}
+
+// bf16 compute at head_dim 32 / 64 / 128: operands rounded to bf16 once (into
+// the library workspace), then the bf16-operand kernels of ar_flash.hip.
 int32_t to_bf16_ws(ar_stream_t stream, const float* const* src, int n, int64_t elems, ar::bf16** dst) {
     int32_t st;
-    ar::bf16* w = (ar::bf16*)ar::workspace(S(stream), (size_t)n * (size_t)elems * sizeof(ar::bf16), &st);
+    const size_t each = align256((size_t)elems * sizeof(ar::bf16));
+    char* w = (char*)ar::workspace(S(stream), (size_t)n * each, &st);
     if (!w) return st;
     for (int i = 0; i < n; ++i) {
-        dst[i] = w + (int64_t)i * elems;
+        dst[i] = (ar::bf16*)(w + i * each);
         const int32_t r = ar::to_bf16(S(stream), dst[i], src[i], elems);
         if (r) return r;
     }
@@ -730,13 +794,30 @@ int32_t to_bf16_ws(ar_stream_t stream, const float* const* src, int n, int64_t e
 }
 }  // namespace
 
+extern "C" int32_t ar_flash_attn_fwd(ar_stream_t stream, float* output, float* lse_out, const float* q, const float* k,
+                                     const float* v, int64_t B, int64_t T, int64_t num_heads, int64_t head_dim,
+                                     int64_t window_size) {
+    AR_ATTN_PTRS(output, q, k, v);
+    AR_CHECK_ARG(lse_out != nullptr, "flash_attn_fwd: null lse");
+    if (!native_hd(head_dim)) {
+        const float* in[3] = {q, k, v};
+        return attn_padded(stream, false, ar::AttnOp::FWD, output, lse_out, in, nullptr, nullptr, B, T, num_heads,
+                           head_dim, window_size);
+    }
+    return ar::attn_dispatch<false, float>(S(stream), ar::AttnOp::FWD, output, lse_out, q, k, v, nullptr, nullptr,
+                                           nullptr, B, T, num_heads, head_dim, window_size);
+}
+
 extern "C" int32_t ar_flash_attn_fwd_bf16(ar_stream_t stream, float* output, float* lse_out, const float* q,
                                           const float* k, const float* v, int64_t B, int64_t T, int64_t num_heads,
                                           int64_t head_dim, int64_t window_size) {
     AR_ATTN_PTRS(output, q, k, v);
     AR_CHECK_ARG(lse_out != nullptr, "flash_attn_fwd_bf16: null lse");
-    AR_CHECK_ARG(B >= 0 && T >= 0 && num_heads >= 0 && head_dim % 32 == 0, "flash_attn_fwd_bf16: bad shape");
+    AR_CHECK_ARG(B >= 0 && T >= 0 && num_heads >= 0, "flash_attn_fwd_bf16: bad shape");
     const float* src[3] = {q, k, v};
+    if (!native_hd(head_dim))
+        return attn_padded(stream, true, ar::AttnOp::FWD, output, lse_out, src, nullptr, nullptr, B, T, num_heads,
+                           head_dim, window_size);
     ar::bf16* b[3];
     int32_t r = to_bf16_ws(stream, src, 3, B * T * num_heads * head_dim, b);
     if (r) return r;
@@ -749,6 +830,11 @@ extern "C" int32_t ar_flash_attn_bwd_dq(ar_stream_t stream, float* grad_q, const
                                         int64_t window_size) {
     AR_ATTN_PTRS(grad_q, q, k, v, grad_output);
     AR_CHECK_ARG(lse && d_buf, "flash_attn_bwd_dq: null lse / d_buf");
+    if (!native_hd(head_dim)) {
+        const float* in[4] = {q, k, v, grad_output};
+        return attn_padded(stream, false, ar::AttnOp::DQ, grad_q, nullptr, in, lse, d_buf, B, T, num_heads, head_dim,
+                           window_size);
+    }
     return ar::attn_dispatch<false, float>(S(stream), ar::AttnOp::DQ, grad_q, nullptr, q, k, v, grad_output, lse,
                                            d_buf, B, T, num_heads, head_dim, window_size);
 }
@@ -758,8 +844,11 @@ extern "C" int32_t ar_flash_attn_bwd_dq_bf16(ar_stream_t stream, float* grad_q, 
                                              int64_t head_dim, int64_t window_size) {
     AR_ATTN_PTRS(grad_q, q, k, v, grad_output);
     AR_CHECK_ARG(lse && d_buf, "flash_attn_bwd_dq_bf16: null lse / d_buf");
-    AR_CHECK_ARG(B >= 0 && T >= 0 && num_heads >= 0 && head_dim % 32 == 0, "flash_attn_bwd_dq_bf16: bad shape");
+    AR_CHECK_ARG(B >= 0 && T >= 0 && num_heads >= 0, "flash_attn_bwd_dq_bf16: bad shape");
     const float* src[4] = {q, k, v, grad_output};
+    if (!native_hd(head_dim))
+        return attn_padded(stream, true, ar::AttnOp::DQ, grad_q, nullptr, src, lse, d_buf, B, T, num_heads, head_dim,
+                           window_size);
     ar::bf16* b[4];
     int32_t r = to_bf16_ws(stream, src, 4, B * T * num_heads * head_dim, b);
     if (r) return r;
@@ -772,6 +861,11 @@ extern "C" int32_t ar_flash_attn_bwd_dkv(ar_stream_t stream, float* grad_k, floa
                                          int64_t head_dim, int64_t window_size) {
     AR_ATTN_PTRS(grad_k, grad_v, q, k, v, grad_output);
     AR_CHECK_ARG(lse && d_buf, "flash_attn_bwd_dkv: null lse / d_buf");
+    if (!native_hd(head_dim)) {
+        const float* in[4] = {q, k, v, grad_output};
+        return attn_padded(stream, false, ar::AttnOp::DKV, grad_k, grad_v, in, lse, d_buf, B, T, num_heads, head_dim,
+                           window_size);
+    }
     return ar::attn_dispatch<false, float>(S(stream), ar::AttnOp::DKV, grad_k, grad_v, q, k, v, grad_output, lse,
                                            d_buf, B, T, num_heads, head_dim, window_size);
 }
@@ -781,8 +875,11 @@ extern "C" int32_t ar_flash_attn_bwd_dkv_bf16(ar_stream_t stream, float* grad_k,
                                               int64_t num_heads, int64_t head_dim, int64_t window_size) {
     AR_ATTN_PTRS(grad_k, grad_v, q, k, v, grad_output);
     AR_CHECK_ARG(lse && d_buf, "flash_attn_bwd_dkv_bf16: null lse / d_buf");
-    AR_CHECK_ARG(B >= 0 && T >= 0 && num_heads >= 0 && head_dim % 32 == 0, "flash_attn_bwd_dkv_bf16: bad shape");
+    AR_CHECK_ARG(B >= 0 && T >= 0 && num_heads >= 0, "flash_attn_bwd_dkv_bf16: bad shape");
     const float* src[4] = {q, k, v, grad_output};
+    if (!native_hd(head_dim))
+        return attn_padded(stream, true, ar::AttnOp::DKV, grad_k, grad_v, src, lse, d_buf, B, T, num_heads, head_dim,
+                           window_size);
     ar::bf16* b[4];
     int32_t r = to_bf16_ws(stream, src, 4, B * T * num_heads * head_dim, b);
     if (r) return r;
@@ -792,4 +889,4 @@ extern "C" int32_t ar_flash_attn_bwd_dkv_bf16(ar_stream_t stream, float* grad_k,
 
 template int32_t ar::attn_dispatch<false, float>(hipStream_t, ar::AttnOp, float*, float*, const float*, const float*,
                                                  const float*, const float*, const float*, const float*, int64_t,
-                                                 int64_t, int64_t, int64_t, int64_t);
+                                                 int64_t, int64_t, int64_t, int64_t, float);

@@ -988,8 +988,8 @@ constexpr size_t fa2_lds(bool with_ld) {
 template <int HD>
 int32_t flash_hd(hipStream_t st, AttnOp op, float* o1, float* o2, const FlashOut& fo, const bf16* q, const bf16* k,
                  const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int B, int T, int H,
-                 int window) {
-    const float scale = 1.0f / sqrtf((float)HD);
+                 int window, float sc) {
+    const float scale = sc > 0.f ? sc : 1.0f / sqrtf((float)HD);
     const float scale_log2 = scale * kLog2e;
     const unsigned grid = (unsigned)(((T + kOwn - 1) / kOwn) * B * H);
     const int64_t rs = (int64_t)H * HD, brs = fo.brs > 0 ? fo.brs : rs;
@@ -1065,15 +1065,15 @@ int32_t flash_dq_ds_bf16(hipStream_t st, const FlashOut& fo, const bf16* k, cons
 
 int32_t flash_attn_bf16(hipStream_t st, AttnOp op, float* o1, float* o2, const FlashOut& fo, const bf16* q,
                         const bf16* k, const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int64_t B,
-                        int64_t T, int64_t H, int64_t HD, int64_t window) {
+                        int64_t T, int64_t H, int64_t HD, int64_t window, float scale) {
     if (B <= 0 || T <= 0 || H <= 0) return B == 0 || T == 0 ? AR_OK : set_error(AR_EINVAL, "flash attention: bad shape");
     if (((T + kOwn - 1) / kOwn) * B * H > 0x7fffffff || T > (1 << 30))
         return set_error(AR_EINVAL, "flash attention: shape too large");
     const int w = window > T ? (int)T : (int)window;  // a window >= T is full causal
     switch (HD) {
-        case 32: return flash_hd<32>(st, op, o1, o2, fo, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
-        case 64: return flash_hd<64>(st, op, o1, o2, fo, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
-        case 128: return flash_hd<128>(st, op, o1, o2, fo, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w);
+        case 32: return flash_hd<32>(st, op, o1, o2, fo, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w, scale);
+        case 64: return flash_hd<64>(st, op, o1, o2, fo, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w, scale);
+        case 128: return flash_hd<128>(st, op, o1, o2, fo, q, k, v, dout, lse, dbuf, (int)B, (int)T, (int)H, w, scale);
         default: return set_error(AR_EUNSUPPORTED, "flash attention: head_dim %lld not in {32, 64, 128}", (long long)HD);
     }
 }

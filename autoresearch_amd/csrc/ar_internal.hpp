@@ -70,10 +70,12 @@ constexpr int kGateMaxH = 16;
 
 // ---- attention (ar_attention.hip) ----
 enum class AttnOp { FWD, DQ, DKV };
+// scale: the softmax scale; 0 = 1/sqrt(HD).  A caller that zero-pads rows
+// from a smaller head_dim to HD passes 1/sqrt of the unpadded head_dim.
 template <bool BF16, typename TIN>
 int32_t attn_dispatch(hipStream_t st, AttnOp op, float* o1, float* o2, const TIN* q, const TIN* k, const TIN* v,
                       const TIN* dout, const float* lse, const float* dbuf, int64_t B, int64_t T, int64_t H,
-                      int64_t HD, int64_t window);
+                      int64_t HD, int64_t window, float scale = 0.f);
 
 // bf16-stored operands (ar_flash.hip): q, k, v, dout bf16.  fp32 outputs
 // (may be null except LSE): FWD o1 = O, o2 = LSE; DQ o1 = dQ; DKV o1 = dK,
@@ -93,7 +95,7 @@ struct FlashOut {
 };
 int32_t flash_attn_bf16(hipStream_t st, AttnOp op, float* o1, float* o2, const FlashOut& fo, const bf16* q,
                         const bf16* k, const bf16* v, const bf16* dout, const float* lse, const float* dbuf, int64_t B,
-                        int64_t T, int64_t H, int64_t HD, int64_t window);
+                        int64_t T, int64_t H, int64_t HD, int64_t window, float scale = 0.f);
 // dS workspace size (bf16 elements) of a DKV launch with FlashOut::ds.
 int64_t flash_ds_elems(int64_t B, int64_t T, int64_t H);
 // D = rowsum(dO * O) per (token, head) from bf16 dO [B, T, H, hd] and fp32 O.

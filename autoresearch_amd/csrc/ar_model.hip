@@ -394,10 +394,24 @@ static int32_t gpt_build(ar_gpt* m) {
         // The dS workspace grows with T^2; past kDsMaxBytes (or the
         // AR_ATTN_DS_MAX_BYTES override) the step keeps the dQ kernel that
         // recomputes S and dP instead.
+        // If the allocation fails the step also takes the recomputing path.
         int64_t ds_max = kDsMaxBytes;
-        if (const char* e = getenv("AR_ATTN_DS_MAX_BYTES")) ds_max = strtoll(e, nullptr, 10);
+        if (const char* e = getenv("AR_ATTN_DS_MAX_BYTES")) {
+            char* end = nullptr;
+            ds_max = strtoll(e, &end, 10);
+            if (end == e || *end != '\0' || ds_max < 0)
+                return set_error(AR_EINVAL, "gpt: AR_ATTN_DS_MAX_BYTES='%s' is not a non-negative byte count", e);
+        }
         const int64_t ds_elems = flash_ds_elems(m->B, m->T, H);
-        if (ds_elems * (int64_t)sizeof(bf16) <= ds_max) AR_TRY(balloc(&m->ds_buf, ds_elems));
+        if (ds_elems * (int64_t)sizeof(bf16) <= ds_max) {
+            void* p = nullptr;
+            if (hipMalloc(&p, (size_t)ds_elems * sizeof(bf16)) == hipSuccess) {
+                m->allocs.push_back(p);
+                m->ds_buf = (bf16*)p;
+            } else {
+                (void)hipGetLastError();  // clear the failed allocation's error; ds_buf stays null
+            }
+        }
     } else {
         FALLOC(m->rms_qk, BT * H);
         FALLOC(m->x_final, BT * C);

@@ -46,7 +46,8 @@ __device__ __forceinline__ void st4v(float* p, int64_t i4, float4 v) { reinterpr
 // X_j = (1-mu) g + mu * (mu buf + (1-mu) g); buf updated (optimizer.mojo:132-146);
 // partial[j][b] = this block's sum of X^2.
 template <bool VEC>
-__global__ void nesterov_multi_k(GroupTable t, float* X, int64_t size, float mu, const float* dmu, float* partial) {
+__global__ void nesterov_multi_k(GroupTable t, float* X, int64_t size, float mu, const float* dmu, float* partial,
+                                 int64_t rows, int64_t cols, int64_t cols_p) {
     __shared__ float red[4];
     if (dmu) mu = *dmu;
     const int j = blockIdx.y;
@@ -72,12 +73,20 @@ __global__ void nesterov_multi_k(GroupTable t, float* X, int64_t size, float mu,
             st4v(x, i, o);
         }
     } else {
+        // X may be zero-padded to [rows_p, cols_p] (size = rows_p * cols_p);
+        // g and buf are [rows, cols]
         for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size;
              i += (int64_t)gridDim.x * blockDim.x) {
-            float mm, o;
-            one(g[i], buf[i], mm, o);
-            buf[i] = mm;
-            x[i] = o;
+            const int64_t r = i / cols_p, c = i - r * cols_p;
+            if (r < rows && c < cols) {
+                const int64_t e = r * cols + c;
+                float mm, o;
+                one(g[e], buf[e], mm, o);
+                buf[e] = mm;
+                x[i] = o;
+            } else {
+                x[i] = 0.0f;
+            }
         }
     }
     ss = block_sum(ss, red);
@@ -128,14 +137,14 @@ __device__ __forceinline__ float cautious(float pv, float gv, float lr, float wd
 }
 template <bool VEC>
 __global__ void update_multi_k(GroupTable t, const float* X, int64_t size, float lr, float wd, const float* dlr,
-                               const float* dwd) {
+                               const float* dwd, int64_t cols, int64_t xsize, int64_t cols_p) {
     if (dlr) {
         lr = *dlr;
         wd = *dwd;
     }
     const int j = blockIdx.y;
     float* p = t.p[j];
-    const float* x = X + (int64_t)j * size;
+    const float* x = X + (int64_t)j * xsize;
     if constexpr (VEC) {
         for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size / 4;
              i += (int64_t)gridDim.x * blockDim.x) {
@@ -144,9 +153,12 @@ __global__ void update_multi_k(GroupTable t, const float* X, int64_t size, float
                                    cautious(pv.z, gv.z, lr, wd), cautious(pv.w, gv.w, lr, wd)));
         }
     } else {
+        // p is [rows, cols] (size = rows * cols); X may be padded to cols_p columns
         for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < size;
-             i += (int64_t)gridDim.x * blockDim.x)
-            p[i] = cautious(p[i], x[i], lr, wd);
+             i += (int64_t)gridDim.x * blockDim.x) {
+            const int64_t r = i / cols, c = i - r * cols;
+            p[i] = cautious(p[i], x[r * cols_p + c], lr, wd);
+        }
     }
 }
 
@@ -159,6 +171,8 @@ double muon_lr_factor(int64_t rows, int64_t cols) {
 }
 
 int64_t muon_scratch_elems(int64_t rows, int64_t cols, bool bf16, int64_t n) {
+    rows = (rows + 7) & ~int64_t(7);  // the products' zero-padded shape
+    cols = (cols + 7) & ~int64_t(7);
     const int64_t size = rows * cols;
     const int64_t small = rows >= cols ? cols : rows;
     const int64_t f32 = align64(n * kNormBlocks) + 2 * align64(n * size) + 2 * align64(n * small * small);
@@ -171,8 +185,18 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
                         bool bf16, float* scratch, const MuonDev& dev) {
     if (n <= 0) return AR_OK;
     if (n > kMuonMaxGroup) return set_error(AR_EINVAL, "muon: group of %d > %d matrices", n, kMuonMaxGroup);
-    const int64_t size = rows * cols;
+    // The products work on X zero-padded to multiples of 8 rows and columns
+    // (the batched GEMMs' 16-byte operand rows).  Zero rows and columns stay
+    // zero through every Polar Express iteration (A = X^T X, B = b A + c A^2
+    // and X' = a X + X B are zero wherever X is) and add nothing to the
+    // Frobenius norm; the tall / wide choice and the lr factor are the
+    // unpadded shape's (optimizer.mojo:266-268, 297-303).
+    const int64_t psize = rows * cols;
     const bool tall = rows >= cols;
+    rows = (rows + 7) & ~int64_t(7);
+    const int64_t cols_u = cols;
+    cols = (cols + 7) & ~int64_t(7);
+    const int64_t size = rows * cols;
     const int64_t sm = tall ? cols : rows;
     const int64_t ss = sm * sm;
     float* partial = scratch;
@@ -189,7 +213,7 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
     ::ar::bf16* Bmb = bf16 ? Ab + 2 * align64((n * ss + 1) / 2) : nullptr;
 
     GroupTable t{};
-    bool vec = size % 4 == 0;
+    bool vec = size == psize && size % 4 == 0;
     for (int j = 0; j < n; ++j) {
         t.p[j] = params[j];
         t.g[j] = grads[j];
@@ -197,11 +221,12 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
         vec = vec && ((reinterpret_cast<uintptr_t>(params[j]) | reinterpret_cast<uintptr_t>(grads[j]) |
                        reinterpret_cast<uintptr_t>(mbufs[j])) & 15) == 0;
     }
-    const float lr = (float)(initial_lr * lrm * muon_lr_factor(rows, cols));
+    const int64_t rows_u = psize / cols_u;
+    const float lr = (float)(initial_lr * lrm * muon_lr_factor(rows_u, cols_u));
     const dim3 eg(kNormBlocks, n);
     const float* dmu = dev.dsc ? dev.dsc + dev.mu_i : nullptr;
-    if (vec) nesterov_multi_k<true><<<eg, 256, 0, st>>>(t, X, size, (float)momentum, dmu, partial);
-    else nesterov_multi_k<false><<<eg, 256, 0, st>>>(t, X, size, (float)momentum, dmu, partial);
+    if (vec) nesterov_multi_k<true><<<eg, 256, 0, st>>>(t, X, size, (float)momentum, dmu, partial, rows, cols, cols);
+    else nesterov_multi_k<false><<<eg, 256, 0, st>>>(t, X, size, (float)momentum, dmu, partial, rows_u, cols_u, cols);
     if (vec) scale_multi_k<true><<<eg, 256, 0, st>>>(X, Xb, size, partial);
     else scale_multi_k<false><<<eg, 256, 0, st>>>(X, Xb, size, partial);
     int32_t r = check_launch("muon: normalise");
@@ -268,8 +293,8 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
     }
     const float* dlr = dev.dsc ? dev.dsc + dev.lr_i : nullptr;
     const float* dwd = dev.dsc ? dev.dsc + dev.wd_i : nullptr;
-    if (vec) update_multi_k<true><<<eg, 256, 0, st>>>(t, Xc, size, lr, (float)wd, dlr, dwd);
-    else update_multi_k<false><<<eg, 256, 0, st>>>(t, Xc, size, lr, (float)wd, dlr, dwd);
+    if (vec) update_multi_k<true><<<eg, 256, 0, st>>>(t, Xc, size, lr, (float)wd, dlr, dwd, cols, size, cols);
+    else update_multi_k<false><<<eg, 256, 0, st>>>(t, Xc, psize, lr, (float)wd, dlr, dwd, cols_u, size, cols);
     return check_launch("muon: update");
 }
 
@@ -280,7 +305,7 @@ extern "C" int32_t ar_muon_step(ar_stream_t stream, float* params, float* grads,
                                 int64_t cols, double initial_lr, double lr_multiplier, double momentum,
                                 double weight_decay, int32_t precision) {
     AR_CHECK_ARG(params && grads && momentum_buf, "muon_step: null pointer");
-    AR_CHECK_ARG(rows > 0 && cols > 0 && rows % 8 == 0 && cols % 8 == 0, "muon_step: rows, cols must be multiples of 8");
+    AR_CHECK_ARG(rows > 0 && cols > 0, "muon_step: bad shape");
     const bool bf = precision == AR_PREC_BF16;
     int32_t st;
     float* scratch = (float*)ar::workspace(ar::S(stream), (size_t)ar::muon_scratch_elems(rows, cols, bf, 1) * sizeof(float), &st);

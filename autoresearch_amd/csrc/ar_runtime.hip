@@ -116,22 +116,23 @@ extern "C" int32_t ar_workspace_bind(ar_stream_t stream, ar_workspace* ws) {
 extern "C" int32_t ar_workspace_destroy(ar_workspace* ws) {
     if (!ws) return AR_OK;
     int32_t r = AR_OK;
-    std::vector<hipStream_t> streams;
     {
         std::lock_guard<std::mutex> lk(g_mu);
         for (size_t i = 0; i < g_bind.size();) {
-            if (g_bind[i].ws == ws) {
-                streams.push_back(g_bind[i].stream);
-                g_bind.erase(g_bind.begin() + i);
-            } else {
-                ++i;
-            }
+            if (g_bind[i].ws == ws) g_bind.erase(g_bind.begin() + i);
+            else ++i;
         }
     }
-    // work queued on the streams it served may still use it
-    for (hipStream_t st : streams)
-        if (hipStreamSynchronize(st) != hipSuccess) r = set_error(AR_EHIP, "workspace_destroy: stream sync failed");
+    // Work queued on the streams it served may still use it.  Those stream
+    // handles may already be destroyed, so wait for the workspace's whole
+    // device instead of each recorded stream.
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return set_error(AR_EHIP, "workspace_destroy: hipGetDevice failed");
+    if (cur != ws->device && hipSetDevice(ws->device) != hipSuccess)
+        return set_error(AR_EHIP, "workspace_destroy: hipSetDevice(%d) failed", ws->device);
+    if (hipDeviceSynchronize() != hipSuccess) r = set_error(AR_EHIP, "workspace_destroy: device sync failed");
     if (hipFree(ws->ptr) != hipSuccess) r = set_error(AR_EHIP, "workspace_destroy: hipFree failed");
+    if (cur != ws->device) (void)hipSetDevice(cur);
     delete ws;
     return r;
 }

@@ -21,7 +21,9 @@ launch on the model's stream during P further profiled steps, which run the
 same kernels on the same stream right after the timed ones (events are kept
 out of the timed steps, where they would add ~2 % of launch overhead);
 `cpu_baseline` times the fp32 CPU oracle on this host on a bounded sample of
-the same workload.
+the same workload.  The default run (config 4, bf16) also reports, under
+`extra_workloads`, short runs (2 warm-up + 5 timed + 2 profiled steps) of
+config 4 at the reference's fp32 precision and of config 5 in bf16.
 """
 from __future__ import annotations
 
@@ -65,12 +67,12 @@ def step_flops(L, C, V, B, T, H, hd, windows, mats) -> float:
     return gemm + attn + muon
 
 
-def measured_traffic(cls: str, a, bf16: bool):
+def measured_traffic(cls: str, a, bf16: bool, depth: int, batch: int):
     """HBM bytes per launch of kernel class `cls` from the committed counter
     passes (rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled by a 1 GiB copy; see
     profiles/counters_config4_bf16.md), for the workload those passes ran."""
     path = os.path.join(ROOT, "profiles", "traffic_config4_bf16.json")
-    if not (bf16 and (a.depth, a.batch, a.seq, a.vocab) == (8, 32, 2048, 8192) and os.path.exists(path)):
+    if not (bf16 and (depth, batch, a.seq, a.vocab) == (8, 32, 2048, 8192) and os.path.exists(path)):
         return None
     with open(path) as f:
         return json.load(f)["classes"].get(cls)
@@ -240,6 +242,8 @@ def main(argv=None) -> int:
     ap.add_argument("--vocab", type=int, default=8192)
     ap.add_argument("--precision", choices=["bf16", "fp32"], default="bf16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra-legs", action="store_true",
+                    help="skip the short fp32 config-4 and bf16 config-5 runs reported beside the headline")
     ap.add_argument("--graph", action="store_true", help="replay the step from a HIP graph")
     ap.add_argument("--prof-steps", type=int, default=5, help="profiled steps after the timed ones")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -259,7 +263,6 @@ def main(argv=None) -> int:
         return 2
 
     import torch
-    from autoresearch_amd.model import BF16, FP32, GPT, GPTConfig
 
     if a.vendor_comparator:
         print(json.dumps({"vendor_comparator": vendor_comparator()}), flush=True)
@@ -278,12 +281,55 @@ def main(argv=None) -> int:
         print(json.dumps({"copy_probe_bytes_read": 4 * n, "copy_probe_bytes_written": 4 * n}), flush=True)
         return 0
 
-    cfg = GPTConfig.default(a.vocab, a.depth)
-    B, T, V = a.batch, a.seq, a.vocab
-    prec = BF16 if a.precision == "bf16" else FP32
     torch.cuda.set_device(0)
     stream = torch.cuda.Stream()  # a stream of its own (graph capture cannot use the null stream)
     torch.cuda.set_stream(stream)
+    head = run_workload(a, a.config, a.depth, a.batch, a.precision, a.steps, a.warmup, a.prof_steps, a.graph)
+    cfg, B, T, V = head.pop("_cfg"), a.batch, a.seq, a.vocab
+
+    # The other figures the driver should see beside the headline: config 4 at
+    # the reference's own fp32 precision and config 5 in bf16 (short runs of
+    # their own; the headline's timed region is unaffected).
+    extra = {}
+    if not a.no_extra_legs and (a.config, a.depth, a.batch, a.precision) == (4, 8, 32, "bf16"):
+        for key, conf, depth, batch, prec in (("config4_fp32", 4, 8, 32, "fp32"), ("config5_bf16", 5, 12, 64, "bf16")):
+            r = run_workload(a, conf, depth, batch, prec, 5, 2, 2, a.graph)
+            r.pop("_cfg")
+            extra[key] = {k: r[k] for k in ("workload", "dtype", "steps", "warmup", "ms_per_step", "value", "unit",
+                                            "mfma_util", "roofline", "kernel_classes", "loss_after")}
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        print("[bench] cpu baseline (oracle) ...", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(cfg, T, V, B)
+
+    out = {
+        "metric": METRIC, "value": head["value"], "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": a.precision, "data": "synthetic Zipf(1.1) token ids, seed 0",
+        "step_mode": "hip_graph" if a.graph else "eager",
+        "config": {"workload": head["workload"], "global_batch": B, "seq_len": T, "parallelism": "single GPU"},
+        "mfma_util": head["mfma_util"], "step_tflop": head["step_tflop"],
+        "roofline": head["roofline"], "kernel_classes": head["kernel_classes"], "cpu_baseline": cpu,
+        "loss_after": head["loss_after"],
+    }
+    if extra:
+        out["extra_workloads"] = extra
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def run_workload(a, config, depth, batch, precision, steps, warmup, prof_steps, graph) -> dict:
+    """Build the model of one BASELINE workload, run W warm-up and K timed
+    steps, then P event-profiled steps; return its figures."""
+    import ctypes as ct
+    import torch
+    from autoresearch_amd._lib import check
+    from autoresearch_amd.model import BF16, FP32, GPT, GPTConfig
+
+    cfg = GPTConfig.default(a.vocab, depth)
+    B, T, V = batch, a.seq, a.vocab
+    prec = BF16 if precision == "bf16" else FP32
     toks = zipf_tokens(B * (T + 1), V, 1.1, 0).reshape(B, T + 1)
     x = torch.from_numpy(np.ascontiguousarray(toks[:, :-1]).ravel()).cuda()
     y = torch.from_numpy(np.ascontiguousarray(toks[:, 1:]).ravel()).cuda()
@@ -291,31 +337,29 @@ def main(argv=None) -> int:
     m.init_weights(42)
     torch.cuda.synchronize()
     print(f"[bench] model ready: L={cfg.n_layer} C={cfg.n_embd} H={cfg.n_head} V={V} B={B} T={T} "
-          f"{a.precision} {'graph' if a.graph else 'eager'}", file=sys.stderr, flush=True)
-    step = m.train_step_graph if a.graph else m.train_step
-    from autoresearch_amd._lib import check
+          f"{precision} {'graph' if graph else 'eager'}", file=sys.stderr, flush=True)
+    step = m.train_step_graph if graph else m.train_step
 
-    for i in range(a.warmup):
+    for i in range(warmup):
         step(x, y, 0.0, sync_loss=False)
     torch.cuda.synchronize()
-    print(f"[bench] warmup done ({a.warmup} steps)", file=sys.stderr, flush=True)
+    print(f"[bench] warmup done ({warmup} steps)", file=sys.stderr, flush=True)
 
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(a.steps):
+    for i in range(steps):
         step(x, y, 0.0, sync_loss=False)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    ms = (t1 - t0) * 1e3 / a.steps
+    ms = (t1 - t0) * 1e3 / steps
 
     # Per-class timing: HIP events around every GEMM / attention / Muon launch
     # of P eager steps on the same stream.
-    import ctypes as ct
     check(m.lib.ar_gpt_profile(m.h, 1), "gpt_profile")
-    for i in range(a.prof_steps):
+    for i in range(prof_steps):
         m.train_step(x, y, 0.0, sync_loss=False)
     cls_stats = []
-    per = max(a.prof_steps, 1)
+    per = max(prof_steps, 1)
     for c in range(len(CLASS_NAMES)):
         t, n, f = ct.c_double(), ct.c_int64(), ct.c_double()
         check(m.lib.ar_gpt_profile_read(m.h, c, ct.byref(t), ct.byref(n), ct.byref(f)), "gpt_profile_read")
@@ -323,10 +367,12 @@ def main(argv=None) -> int:
     check(m.lib.ar_gpt_profile(m.h, 0), "gpt_profile")
     torch.cuda.synchronize()
     loss = m.forward(x, y)
-    print(f"[bench] timed {a.steps} steps: {ms:.2f} ms/step, loss after = {loss:.4f}", file=sys.stderr, flush=True)
+    print(f"[bench] timed {steps} steps: {ms:.2f} ms/step, loss after = {loss:.4f}", file=sys.stderr, flush=True)
+    m.close()
+    del x, y
+    torch.cuda.empty_cache()
 
-    tokens = B * T
-    value = tokens / (ms / 1e3)
+    value = B * T / (ms / 1e3)
     windows = [cfg.window_size(i) for i in range(cfg.n_layer)]
     mats = []
     F = 4 * cfg.n_embd
@@ -341,33 +387,19 @@ def main(argv=None) -> int:
     name, t_ms, n, f = dom
     achieved = (f / (t_ms / 1e3)) / 1e12 if t_ms > 0 else 0.0
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(achieved / peak, 4), "traffic": measured_traffic(name, a, prec == BF16), "kernel": name,
+                "frac": round(achieved / peak, 4),
+                "traffic": measured_traffic(name, a, prec == BF16, depth, batch), "kernel": name,
                 "launches_per_step": n, "avg_launch_ms": round(t_ms / max(n, 1), 4),
                 "share_of_step": round(t_ms / ms, 4)}
     breakdown = {s[0]: {"ms_per_step": round(s[1], 3),
                         "tflops": round((s[3] / (s[1] / 1e3)) / 1e12, 1) if s[1] > 0 else 0.0}
                  for s in cls_stats}
-
-    cpu = None
-    if not a.no_cpu_baseline:
-        print("[bench] cpu baseline (oracle) ...", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(cfg, T, V, B)
-
-    out = {
-        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
-        "warmup": a.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": a.precision, "data": "synthetic Zipf(1.1) token ids, seed 0",
-        "step_mode": "hip_graph" if a.graph else "eager",
-        "config": {"workload": f"config {a.config}: full training step depth{cfg.n_layer} d{cfg.n_embd} "
-                               f"H{cfg.n_head}x{cfg.head_dim} V{V} T{T} B{B} SSSL, AdamW+Muon",
-                   "global_batch": B, "seq_len": T, "parallelism": "single GPU"},
-        "mfma_util": round(mfma_util, 4), "step_tflop": round(flops / 1e12, 3),
-        "roofline": roofline, "kernel_classes": breakdown, "cpu_baseline": cpu,
-        "loss_after": round(loss, 4),
-    }
-    print(json.dumps(out), flush=True)
-    m.close()
-    return 0
+    return {"_cfg": cfg, "workload": f"config {config}: full training step depth{cfg.n_layer} d{cfg.n_embd} "
+                                     f"H{cfg.n_head}x{cfg.head_dim} V{V} T{T} B{B} SSSL, AdamW+Muon",
+            "dtype": precision, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 3),
+            "value": round(value, 1), "unit": "tokens/s", "mfma_util": round(mfma_util, 4),
+            "step_tflop": round(flops / 1e12, 3), "roofline": roofline, "kernel_classes": breakdown,
+            "loss_after": round(loss, 4)}
 
 
 if __name__ == "__main__":

@@ -73,9 +73,12 @@ typedef struct ar_workspace ar_workspace;
  * entry points depend on).  Create it before a stream capture, not during. */
 int32_t ar_workspace_create(ar_workspace** out, size_t bytes);
 /* Per-op calls on `stream` (on the current device) use `ws` from now on; NULL
- * unbinds.  One workspace may serve several streams whose calls never overlap. */
+ * unbinds.  One workspace may serve several streams whose calls never overlap.
+ * Bindings are keyed by the stream handle: unbind a stream
+ * (ar_workspace_bind(stream, NULL)) before hipStreamDestroy, or a later stream
+ * that reuses the handle inherits the binding. */
 int32_t ar_workspace_bind(ar_stream_t stream, ar_workspace* ws);
-/* Unbinds it everywhere, waits for the streams it was bound to, frees it. */
+/* Unbinds it everywhere, waits for its device to finish queued work, frees it. */
 int32_t ar_workspace_destroy(ar_workspace* ws);
 size_t ar_workspace_bytes(const ar_workspace* ws);
 
@@ -98,7 +101,11 @@ int32_t ar_rope_fwd(ar_stream_t stream, float* output, const float* input, const
 /* ops.mojo:244-323  causal / sliding-window softmax attention + LSE.
  * q,k,v,output: [B*T*num_heads, head_dim]; lse_out: [B*T*num_heads].
  * Key kp visible from qp iff kp <= qp and (window_size <= 0 or kp >= qp - window_size).
- * head_dim must be 32, 64 or 128 (AR_EUNSUPPORTED otherwise). */
+ * Any head_dim in [1, 128] (AR_EUNSUPPORTED above, where ops.mojo:267 returns
+ * silently).  head_dim 32, 64 and 128 run the tiled kernels directly; any
+ * other runs them at the next of those sizes on zero-padded copies of the rows
+ * in the workspace (softmax scale 1/sqrt(head_dim)).  The same holds for the
+ * dq and dkv entries below. */
 int32_t ar_flash_attn_fwd(ar_stream_t stream, float* output, float* lse_out, const float* q, const float* k,
                           const float* v, int64_t B, int64_t T, int64_t num_heads, int64_t head_dim,
                           int64_t window_size);
@@ -254,9 +261,11 @@ int32_t ar_scale_add(ar_stream_t stream, float* output, const float* a, const fl
                      int64_t size);
 /* optimizer.mojo:197-210  p -= lr (g + wd p [g p >= 0]) */
 int32_t ar_muon_update(ar_stream_t stream, float* params, const float* grads, float lr, float wd, int64_t size);
-/* optimizer.mojo:255-342  MuonState.step for one [rows, cols] matrix:
- * Nesterov -> Frobenius normalise -> 5 Polar Express iterations -> cautious
- * update.  `grads` is read only (the reference uses it as scratch after its
+/* optimizer.mojo:255-342  MuonState.step for one [rows, cols] matrix of any
+ * shape: Nesterov -> Frobenius normalise -> 5 Polar Express iterations ->
+ * cautious update.  The products run on the matrix zero-padded to multiples
+ * of 8 rows and columns (zero rows / columns stay zero through the
+ * iterations).  `grads` is read only (the reference uses it as scratch after its
  * last read, optimizer.mojo:317-332; its contents are not used afterwards).
  * precision selects the GEMM path (AR_PREC_FP32 / AR_PREC_BF16). */
 int32_t ar_muon_step(ar_stream_t stream, float* params, float* grads, float* momentum_buf, int64_t rows,

@@ -209,6 +209,27 @@ def test_dw_benchmark_shapes(env, M, N, K):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("M,N,K", DW_SHAPES)
+def test_dw_benchmark_shapes_fp32(env, M, N, K):
+    """linear_bwd_dw (accumulate) with fp32 operands (the fp32 step's dW,
+    ops.mojo:953-1033) at the benchmark's shapes against torch fp64 of the
+    same values: the north-star fp32 bar 1e-5."""
+    ops, orc, gu = env
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(M + N + K + 1)
+    dY = torch.randn(M, N, device="cuda", generator=g)
+    X = torch.randn(M, K, device="cuda", generator=g)
+    C0 = torch.randn(N, K, device="cuda", generator=g)
+    C = C0.clone()
+    ops.linear_bwd_dw(C, dY, X, M, N, K)
+    ref = C0.double() + dY.double().T @ X.double()
+    err = rel_err(gu.host(C), gu.host(ref))
+    print(f"MARGIN dw_fp32 M={M} N={N} K={K} rel_err={err:.3e}")
+    assert err <= TOL_FP32
+    del dY, X, ref
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("M", [32768, 200])
 def test_lm_head_softcap_ce_config3(env, M):
     """BASELINE config 3's fused LM head: x [M, 512] ~ N(0, 1), lm_head
@@ -262,8 +283,13 @@ def _attn_inputs(gu, r, B, T, H, hd):
     return q, k, v, do
 
 
+# hd 16 / 80 / 96 / 100 / 7 run the tiled kernels on zero-padded rows
+# (ops.mojo:267 accepts any head_dim <= 128); (1, 200, 2, 128, 50) runs
+# partial 32- and 64-row tiles at hd 128.
 @pytest.mark.parametrize("B,T,H,hd,window", [(1, 128, 2, 64, 0), (2, 200, 2, 64, 32), (1, 256, 4, 128, 0),
-                                              (1, 320, 1, 128, 100), (2, 64, 2, 32, 16)])
+                                              (1, 320, 1, 128, 100), (2, 64, 2, 32, 16), (1, 200, 2, 128, 50),
+                                              (2, 96, 2, 16, 0), (1, 150, 3, 80, 40), (1, 128, 2, 96, 0),
+                                              (2, 70, 1, 100, 20), (1, 33, 2, 7, 0)])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_attention_vs_oracle(env, B, T, H, hd, window, bf16):
     ops, orc, gu = env
@@ -353,7 +379,10 @@ def test_attention_config2(env, window, bf16):
     assert rel_err(gu.host(dv), gu.host(vr.grad)) <= tol
 
 
-@pytest.mark.parametrize("rows,cols", [(128, 128), (512, 128), (128, 512), (256, 1024)])
+# (30, 50), (50, 30), (13, 7), (100, 100): shapes that are not multiples of 8
+# (optimizer.mojo:255-342 takes any matrix)
+@pytest.mark.parametrize("rows,cols", [(128, 128), (512, 128), (128, 512), (256, 1024), (30, 50), (50, 30), (13, 7),
+                                       (100, 100)])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_muon_step_vs_oracle(env, rows, cols, bf16):
     ops, orc, gu = env

@@ -13,8 +13,24 @@ pytestmark = pytest.mark.gpu
 CONFIG1 = dict(sequence_len=64, vocab_size=512, n_layer=2, n_head=2, n_kv_head=2, n_embd=128, head_dim=64,
                kv_dim=128)
 # Whole-model gradients chain ~40 fp32 GEMMs / reductions whose summation
-# order legitimately differs from the oracle's double accumulation.
-GRAD_FP32 = 3e-4
+# order legitimately differs from the oracle's double accumulation.  Observed
+# at BASELINE configs 1, 4 and 5: <= 1.3e-5 (the MARGIN lines each whole-step
+# test prints).
+GRAD_FP32 = 4e-5
+# Where a gradient is ill-conditioned, every fp32 implementation is far from
+# the exact value: the q / k projection gradients of the small head_dim-128
+# models at step 2 sit 1.7e-5 (WIDE) to 4.2e-5 (ODD128) from fp64 autograd in
+# the oracle itself (which accumulates in double).  Tests that run the fp64
+# autograd model bound each gradient by max(GRAD_FP32, COND_K x the oracle's
+# own distance from fp64) for that tensor and step.
+COND_K = 10.0
+# The bf16 counterpart: the fp64 model with every product operand rounded to
+# bf16 (test_oracle_composites._torch_step(bf16=True)) is itself 0.9e-2 to
+# 2.5e-2 from the exact fp64 gradients on those q / k projections; each
+# gradient is bounded by max(TOL_BF16, BF16_K x that distance).  The GPU's bf16
+# step rounds at more points (the q|k|v product before RoPE, the logits) and
+# measured up to 2.6x the emulation's distance.
+BF16_K = 4.0
 # Muon update error: the Polar Express polynomials multiply small singular
 # values by prod(a_i) ~ 990 over five iterations, so fp32 operand rounding
 # (6e-8) reaches a few 1e-4 of the update; bf16 operands a few 1e-2.
@@ -57,12 +73,27 @@ def _copy_into(dst_flat, dst_tensors, src_flat, src_tensors):
         dst_flat[o:o + s] = src_flat[so:so + ss]
 
 
-def _run(cfg, B, T, precision, rope_period, seed0, steps, tok_seed=0, tokens=_tokens):
+def _fp64_grads(cfg, om, B, T, rope_period, x, y, bf16=False):
+    """Gradients of the fp64 autograd restatement of the step (the reference
+    backward's rules, tests/test_oracle_composites.py) at the oracle's
+    current weights; bf16: with every product operand rounded to bf16."""
+    import test_oracle_composites as tc
+    sh = tc._shapes(cfg)
+    p = om.params()
+    W = {n: np.array(p[o:o + s], copy=True).reshape(sh[n]) for n, o, s in om.tensors()}
+    _, _, g = tc._torch_step(cfg, W, x, y, B, T, rope_period, bf16=bf16)
+    return {n: np.asarray(v).ravel() for n, v in g.items()}
+
+
+def _run(cfg, B, T, precision, rope_period, seed0, steps, tok_seed=0, tokens=_tokens, fp64=False):
     """Each stage is compared on identical inputs: forward/backward from the
     same weights, then the optimizer from the same gradients (the GPU's are
     copied into the oracle), then weights are re-synchronised.  AdamW's first
     steps divide g by |g| and Muon normalises, so without this every ulp of
-    gradient noise in a near-zero entry would show up as a weight mismatch."""
+    gradient noise in a near-zero entry would show up as a weight mismatch.
+    fp64: also compute the fp64 autograd gradients (and, for precision 1,
+    those of the bf16-rounding emulation) at every step's weights, for the
+    conditioning-aware gradient bounds of _check."""
     import torch
     from autoresearch_amd.model import GPT, GPTConfig
     from oracle import oracle as orc
@@ -90,6 +121,8 @@ def _run(cfg, B, T, precision, rope_period, seed0, steps, tok_seed=0, tokens=_to
         gflat = gu.host(gm.grads())
         go, gg = _by_name(om.grads().copy(), ot), _by_name(gflat, gt)
         l1 = om.scalar_grad_l1()
+        g64 = _fp64_grads(cfg, om, B, T, rope_period, x, y) if fp64 else None
+        g64b = _fp64_grads(cfg, om, B, T, rope_period, x, y, bf16=True) if fp64 and precision == 1 else None
         tl_o, tl_g = om.token_loss().copy(), gu.host(gm.token_loss())
         # optimizer from identical gradients (and identical pre-step weights)
         _copy_into(om.grads(), ot, gflat, gt)
@@ -98,9 +131,24 @@ def _run(cfg, B, T, precision, rope_period, seed0, steps, tok_seed=0, tokens=_to
         gm.optimizer_step(0.0)
         po, pg = _by_name(om.params().copy(), ot), _by_name(gu.host(gm.params()), gt)
         results.append(dict(loss=(lo, lg), tok=(tl_o, tl_g), grads=(go, gg), params=(po, pg), l1=l1, pre=pre,
-                            shape=cfg))
+                            g64=g64, g64b=g64b))
     gm.close()
     return init_o, init_g, results
+
+
+def _record(obs):
+    """Print the observed error margins of a whole-step test (and append them
+    as one JSON line to $AR_MARGINS_FILE when set), so that each tolerance can
+    be compared with what the configurations actually show."""
+    import json
+    import os
+    name = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    line = {"test": name, **{k: (float(v) if isinstance(v, (float, np.floating)) else v) for k, v in obs.items()}}
+    print("MARGIN " + json.dumps(line), flush=True)
+    path = os.environ.get("AR_MARGINS_FILE")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(line) + "\n")
 
 
 def _check(init_o, init_g, results, tol, grad_tol, upd_tol):
@@ -108,20 +156,28 @@ def _check(init_o, init_g, results, tol, grad_tol, upd_tol):
     upd_tol: relative error allowed on the optimizer's update w_new - w_old.
     Muon's five Polar Express iterations amplify operand rounding (fp32 ~1e-4,
     bf16 operands ~5e-2 of the update); a weight's error is lr x that, so
-    ||w_gpu - w_orc|| <= tol*||w_orc|| + upd_tol*||w_orc - w_old||."""
+    ||w_gpu - w_orc|| <= tol*||w_orc|| + upd_tol*||w_orc - w_old||.
+    The observed maxima of every error class are recorded (_record)."""
+    obs = dict(loss=0.0, token_loss=0.0, grad=0.0, grad_worst="", scalar_grad=0.0, update_muon=0.0,
+               update_adamw=0.0, update_worst="", flips=0, near_zero=0, tol=tol, grad_tol=grad_tol, upd_tol=upd_tol)
     # init is bit-exact for the uniform tensors, within fp32 for the normal ones
     for n in init_o:
         assert rel_err(init_g[n], init_o[n]) <= TOL_FP32, n
     for s, r in enumerate(results):
         lo, lg = r["loss"]
+        obs["loss"] = max(obs["loss"], abs(lg - lo) / abs(lo))
         assert abs(lg - lo) <= tol * abs(lo), (s, lo, lg)
-        assert rel_err(r["tok"][1], r["tok"][0]) <= tol
+        e = rel_err(r["tok"][1], r["tok"][0])
+        obs["token_loss"] = max(obs["token_loss"], e)
+        assert e <= tol
         go, gg = r["grads"]
         # resid_lambdas / x0_lambdas gradients are sums of B*T*C products that
         # cancel to ~1e-3 of their L1 mass at init; fp32 noise in their inputs
         # is then amplified, so they are bounded by the summation error scale:
         # |diff| <= tol * sum_i |g_i x_i| (per layer).
         for n, l1 in (("resid_lambdas", r["l1"][0]), ("x0_lambdas", r["l1"][1])):
+            rel = np.abs(gg[n] - go[n]) / np.maximum(l1, 1e-30)
+            obs["scalar_grad"] = max(obs["scalar_grad"], float(np.max(rel)))
             assert np.all(np.abs(gg[n] - go[n]) <= grad_tol * l1), (s, n, gg[n], go[n], l1)
         for n in go:
             if n in ("resid_lambdas", "x0_lambdas"):
@@ -129,54 +185,93 @@ def _check(init_o, init_g, results, tol, grad_tol, upd_tol):
             if np.linalg.norm(go[n]) == 0.0:
                 assert np.linalg.norm(gg[n]) == 0.0, (s, n)  # step 1: proj weights are zero
                 continue
-            assert rel_err(gg[n], go[n]) <= grad_tol, (s, n, rel_err(gg[n], go[n]))
+            e = rel_err(gg[n], go[n])
+            if e > obs["grad"]:
+                obs["grad"], obs["grad_worst"] = e, f"step{s}:{n}"
+            bound = grad_tol
+            if r["g64b"] is not None:
+                # bf16: how far bf16 operand rounding alone moves this gradient
+                e_b = rel_err(r["g64b"][n], r["g64"][n])
+                obs["bf16_rounding_vs_fp64"] = max(obs.get("bf16_rounding_vs_fp64", 0.0), e_b)
+                obs["ratio_to_bf16_rounding"] = max(obs.get("ratio_to_bf16_rounding", 0.0), e / max(e_b, 1e-30))
+                bound = max(grad_tol, BF16_K * e_b)
+            elif r["g64"] is not None:
+                e_orc = rel_err(go[n], r["g64"][n])
+                obs["oracle_vs_fp64"] = max(obs.get("oracle_vs_fp64", 0.0), e_orc)
+                bound = max(grad_tol, COND_K * e_orc)
+            assert e <= bound, (s, n, e, bound)
         po, pg = r["params"]
         for n in po:
             w_old = r["pre"][n].astype(np.float64)
             diff = pg[n].astype(np.float64) - po[n]
-            dec = _cautious_decay(n, w_old, r["shape"])
-            if dec is not None:
+            lr = _muon_lr(n)
+            if lr is not None:
                 # Muon's cautious update decays p only where X p >= 0
-                # (optimizer.mojo:197-210).  Where X is within rounding of 0
-                # two implementations may take different branches; such an
-                # entry differs by exactly the decay lr wd |p|.  Those are set
-                # aside and the rest meet the bound.  |X| is within the
-                # update's relative noise upd_tol of 0 on about 0.8 upd_tol of
-                # the entries (X is roughly Gaussian), hence the cap 2 upd_tol.
-                flip = (dec > 0) & (np.abs(np.abs(diff) - dec) <= 0.05 * dec)
-                assert flip.sum() <= 2 * upd_tol * diff.size, (s, n, int(flip.sum()))
+                # (optimizer.mojo:197-210).  Where the oracle's X is within
+                # the update noise of 0, two implementations may take
+                # different branches, and such an entry differs by exactly
+                # the decay lr wd |p|.  Only entries that are both near zero
+                # in the oracle's own X (recovered from its step) and off by
+                # the decay are set aside; the rest meet the bound.
+                x_o = _oracle_muon_x(po[n].astype(np.float64), w_old, lr, _MUON_WD)
+                near = np.abs(x_o) <= 2.0 * upd_tol * np.sqrt(np.mean(x_o * x_o))
+                dec = lr * _MUON_WD * np.abs(w_old)
+                flip = near & (dec > 0) & (np.abs(np.abs(diff) - dec) <= 0.05 * dec)
+                obs["flips"] += int(flip.sum())
+                obs["near_zero"] += int(near.sum())
                 diff = np.where(flip, 0.0, diff)
-            bound = tol * np.linalg.norm(po[n]) + upd_tol * np.linalg.norm(po[n] - w_old)
+            upd = np.linalg.norm(po[n] - w_old)
             d = np.linalg.norm(diff)
+            if upd > 0:
+                key = "update_muon" if lr is not None else "update_adamw"
+                if d / upd > obs[key]:
+                    obs[key] = d / upd
+                    if key == "update_muon":
+                        obs["update_worst"] = f"step{s}:{n}"
+            bound = tol * np.linalg.norm(po[n]) + upd_tol * upd
             assert d <= bound, (s, n, d, bound)
+    _record(obs)
+    return obs
 
 
-def _cautious_decay(name, w_old, shape):
-    """lr wd |p| of the Muon matrices at progress 0 (lr multiplier 1, weight
-    decay 0.2, lr 0.04 sqrt(max(1, rows / cols)): train.mojo:272,
-    optimizer.mojo:265-267); None for the AdamW tensors."""
+_MUON_WD = float(np.float32(0.2))  # train.mojo:272
+
+
+def _muon_lr(name):
+    """Muon's lr at progress 0 (lr multiplier 1: 0.04 sqrt(max(1, rows / cols)),
+    optimizer.mojo:265-267) as the fp32 value the step uses; None for the
+    AdamW tensors."""
     part = name.split(".")[-1]
     aspect = {"c_q": 1.0, "c_k": 1.0, "c_v": 1.0, "c_proj": 1.0, "c_fc": 4.0, "mlp_proj": 0.25}.get(part)
     if aspect is None or not name.startswith("h"):
         return None
-    lr = np.float32(0.04 * np.sqrt(max(1.0, aspect)))
-    return float(lr) * float(np.float32(0.2)) * np.abs(w_old)
+    return float(np.float32(0.04 * np.sqrt(max(1.0, aspect))))
+
+
+def _oracle_muon_x(p_new, p_old, lr, wd):
+    """The oracle's orthogonalised update X, recovered from its step
+    p_new = p_old - lr (X + wd p_old [X p_old >= 0]): exactly one branch is
+    consistent with its own mask (X p >= 0 with X = c1, or X p < 0 with
+    X = c0, since c1 p = c0 p - wd p^2), and at p = 0 both agree."""
+    c0 = (p_old - p_new) / lr          # mask false: X = c0
+    c1 = c0 - wd * p_old               # mask true:  X = c1
+    return np.where(c1 * p_old >= 0.0, c1, c0)
 
 
 @pytest.mark.parametrize("seed0", [0, 42])
 def test_config1_fp32_two_steps(seed0):
-    init_o, init_g, res = _run(CONFIG1, 2, 64, 0, 0, seed0, steps=2)
+    init_o, init_g, res = _run(CONFIG1, 2, 64, 0, 0, seed0, steps=2, fp64=True)
     _check(init_o, init_g, res, TOL_FP32, GRAD_FP32, UPD_FP32)
 
 
 def test_config1_bf16_two_steps():
-    init_o, init_g, res = _run(CONFIG1, 2, 64, 1, 0, 0, steps=2)
+    init_o, init_g, res = _run(CONFIG1, 2, 64, 1, 0, 0, steps=2, fp64=True)
     _check(init_o, init_g, res, TOL_BF16, TOL_BF16, UPD_BF16)
 
 
 @pytest.mark.parametrize("precision", [0, 1])
 def test_wide_model(precision):
-    init_o, init_g, res = _run(WIDE, 2, 256, precision, 256, 3, steps=2)
+    init_o, init_g, res = _run(WIDE, 2, 256, precision, 256, 3, steps=2, fp64=True)
     if precision == 0:
         _check(init_o, init_g, res, TOL_FP32, GRAD_FP32, UPD_FP32)
     else:
@@ -193,20 +288,71 @@ def test_odd_length_small_heads(precision):
     head_dim 32 and windows of 50 (three layers) and 100: the attention
     kernels' partial last blocks, rows past T and windows shorter than a tile,
     in the whole step against the oracle."""
-    init_o, init_g, res = _run(ODD, 2, 100, precision, 100, 5, steps=2)
+    init_o, init_g, res = _run(ODD, 2, 100, precision, 100, 5, steps=2, fp64=True)
     if precision == 0:
         _check(init_o, init_g, res, TOL_FP32, GRAD_FP32, UPD_FP32)
     else:
         _check(init_o, init_g, res, TOL_BF16, TOL_BF16, UPD_BF16)
 
 
-@pytest.mark.parametrize("cfg,T", [(WIDE, 256), (ODD, 100)], ids=["wide", "odd"])
+ODD128 = dict(sequence_len=100, vocab_size=512, n_layer=4, n_head=2, n_kv_head=2, n_embd=256, head_dim=128,
+              kv_dim=256)
+
+
+@pytest.mark.parametrize("precision", [0, 1])
+def test_odd_length_head_dim_128(precision):
+    """T = 100 at head_dim 128 (windows 50 and 100): the partial last 32- and
+    64-row blocks of the hd-128 kernels the benchmark runs (the bf16 dK / dV
+    kernel that stores dS and the dQ product from it; the fp32 split dV / dK
+    launches with their tile prefetch) against the oracle.  The step-2 q / k
+    projection gradients of this small model are ill-conditioned: the oracle
+    itself is 4e-5 from fp64 autograd there, and bf16 operand rounding alone
+    moves them by ~1.4e-2 (the bounds of _check scale with both)."""
+    init_o, init_g, res = _run(ODD128, 2, 100, precision, 100, 11, steps=2, fp64=True)
+    if precision == 0:
+        _check(init_o, init_g, res, TOL_FP32, GRAD_FP32, UPD_FP32)
+    else:
+        _check(init_o, init_g, res, TOL_BF16, TOL_BF16, UPD_BF16)
+
+
+def test_bf16_ds_workspace_is_bit_identical():
+    """The bf16 step's dQ from the stored dS blocks and the dQ kernel that
+    recomputes S and dP feed the same bf16 dS values to the same products:
+    every gradient is bit-identical with and without the dS workspace, here
+    at head_dim 128 and T = 100 (partial last blocks, windows 50 / 100)."""
+    import os
+    import gpu_util as gu
+    from autoresearch_amd.model import GPT, GPTConfig
+    x, y = _tokens(4, 2, 100, ODD128["vocab_size"])
+    xd, yd = gu.dev(x), gu.dev(y)
+    grads = []
+    for cap in (None, "0"):
+        if cap is None:
+            os.environ.pop("AR_ATTN_DS_MAX_BYTES", None)
+        else:
+            os.environ["AR_ATTN_DS_MAX_BYTES"] = cap
+        try:
+            gm = GPT(GPTConfig(**ODD128), 2, 100, precision=1, rope_period=100)
+        finally:
+            os.environ.pop("AR_ATTN_DS_MAX_BYTES", None)
+        gm.init_weights(11)
+        gm.train_step(xd, yd, 0.0)   # step 1: c_proj becomes non-zero
+        gm.zero_grads()
+        gm.forward(xd, yd)
+        gm.backward(xd, yd, 1.0)
+        grads.append(gu.host(gm.grads()).copy())
+        gm.close()
+    assert np.any(grads[0] != 0)
+    np.testing.assert_array_equal(grads[0], grads[1])
+
+
+@pytest.mark.parametrize("cfg,T", [(WIDE, 256), (ODD, 100), (ODD128, 100)], ids=["wide", "odd", "odd128"])
 def test_bf16_attention_backward_without_ds_workspace(cfg, T, monkeypatch):
     """The bf16 step's fallback for long sequences: with the dS workspace cap
     at 0 bytes the model keeps the dQ kernel that recomputes S and dP (and D
     from its own kernel); the whole step must still match the oracle."""
     monkeypatch.setenv("AR_ATTN_DS_MAX_BYTES", "0")
-    init_o, init_g, res = _run(cfg, 2, T, 1, T, 3, steps=2)
+    init_o, init_g, res = _run(cfg, 2, T, 1, T, 3, steps=2, fp64=True)
     _check(init_o, init_g, res, TOL_BF16, TOL_BF16, UPD_BF16)
 
 
@@ -237,9 +383,11 @@ def test_config5_dims_two_steps(precision):
         _check(init_o, init_g, res, TOL_BF16, TOL_BF16, UPD_BF16)
 
 
-@pytest.mark.parametrize("cfg,B", [(CONFIG4, 32), (CONFIG5, 64)], ids=["config4", "config5"])
-def test_full_size_step_properties(cfg, B):
-    """The benchmarked workloads at full size (bf16, B = 32 / 64, T 2048),
+@pytest.mark.parametrize("cfg,B,precision", [(CONFIG4, 32, 1), (CONFIG5, 64, 1), (CONFIG4, 32, 0)],
+                         ids=["config4", "config5", "config4_fp32"])
+def test_full_size_step_properties(cfg, B, precision):
+    """The benchmarked workloads at full size (B = 32 / 64, T 2048; config 4
+    in bf16 and at the reference's fp32, config 5 in bf16),
     where the oracle would take minutes, through size-independent properties:
     the first loss is ln V to within 0.01 (lm_head ~ N(0, 0.001) makes the
     logits nearly uniform, test_forward.mojo:114-120), the step is bit-identical
@@ -252,7 +400,7 @@ def test_full_size_step_properties(cfg, B):
     xd, yd = gu.dev(x), gu.dev(y)
     runs = []
     for _ in range(2):
-        gm = GPT(GPTConfig(**cfg), B, T, precision=1, rope_period=T)
+        gm = GPT(GPTConfig(**cfg), B, T, precision=precision, rope_period=T)
         gm.init_weights(42)
         losses = [gm.train_step(xd, yd, 0.0) for _ in range(5)]
         p = gu.host(gm.params())

@@ -126,24 +126,79 @@ def _rope(x, cos, sin):
     return torch.cat([x1 * c + x2 * s, -x1 * s + x2 * c], -1)
 
 
-def _attention(q, k, v, B, T, ws):
+# ---- bf16 operand storage, emulated in fp64 ----
+# A bf16-mode step stores every matrix-product operand as bf16 in both passes:
+# a product's inputs and the gradient that reaches its output (dY), plus the
+# attention probabilities P (for P V) and dS (for dQ, dK).  _round_both rounds
+# a value and the gradient that flows back through it; _round_grad only the
+# gradient; _round_value only the value.  The distance of this model's
+# gradients from the exact fp64 ones measures how far bf16 rounding alone
+# moves each gradient (large where a gradient is a small difference of large
+# terms).
+def _bf(x):
+    return x.to(torch.bfloat16).to(x.dtype)
+
+
+class _RoundBoth(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        return _bf(x)
+
+    @staticmethod
+    def backward(ctx, g):
+        return _bf(g)
+
+
+class _RoundGrad(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        return x.clone()
+
+    @staticmethod
+    def backward(ctx, g):
+        return _bf(g)
+
+
+class _RoundValue(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        return _bf(x)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g
+
+
+def _mm(a, b, bf16):
+    if not bf16:
+        return a @ b
+    return _RoundGrad.apply(_RoundBoth.apply(a) @ _RoundBoth.apply(b))
+
+
+def _attention(q, k, v, B, T, ws, bf16=False):
     """Key kp visible from qp iff kp <= qp and (ws <= 0 or kp >= qp - ws),
     scores scaled by 1/sqrt(hd) (ops.mojo:244-323).  q, k, v: [B*T, H, hd]."""
     H, hd = q.shape[1], q.shape[2]
+    if bf16:
+        q, k, v = _RoundBoth.apply(q), _RoundBoth.apply(k), _RoundBoth.apply(v)
     qt, kt, vt = (x.reshape(B, T, H, hd).permute(0, 2, 1, 3) for x in (q, k, v))
     s = qt @ kt.transpose(-1, -2) / np.sqrt(hd)
+    if bf16:
+        s = _RoundGrad.apply(s)  # dS
     i = torch.arange(T)
     vis = i[None, :] <= i[:, None]
     if ws > 0:
         vis = vis & (i[None, :] >= i[:, None] - ws)
     s = s.masked_fill(~vis, float("-inf"))
-    o = torch.softmax(s, -1) @ vt
+    p = torch.softmax(s, -1)
+    o = (_RoundValue.apply(p) if bf16 else p) @ vt
     return o.permute(0, 2, 1, 3).reshape(B * T, H, hd)
 
 
-def _torch_step(cfg, W, x_ids, y_ids, B, T, rope_period):
+def _torch_step(cfg, W, x_ids, y_ids, B, T, rope_period, bf16=False):
     """Forward of model.mojo:576-772 in fp64; returns (mean loss, per-token
-    loss, {name: gradient}) with the reference backward's rules."""
+    loss, {name: gradient}) with the reference backward's rules.  bf16: every
+    product operand rounded to bf16 as above (the rest stays fp64)."""
     C, V, L, H, hd = cfg["n_embd"], cfg["vocab_size"], cfg["n_layer"], cfg["n_head"], cfg["head_dim"]
     BT = B * T
     P = {n: torch.tensor(a, dtype=D, requires_grad=True) for n, a in W.items()}
@@ -159,9 +214,9 @@ def _torch_step(cfg, W, x_ids, y_ids, B, T, rope_period):
         x = _ScaledAdd.apply(x, x0.detach(), P["resid_lambdas"], P["x0_lambdas"], i)
         x_saved = x
         xn = x / _rms(x)
-        q = (xn @ P[p + "c_q"].T).reshape(BT, H, hd)
-        k = (xn @ P[p + "c_k"].T).reshape(BT, H, hd)
-        v = (xn @ P[p + "c_v"].T).reshape(BT, H, hd)
+        q = _mm(xn, P[p + "c_q"].T, bf16).reshape(BT, H, hd)
+        k = _mm(xn, P[p + "c_k"].T, bf16).reshape(BT, H, hd)
+        v = _mm(xn, P[p + "c_v"].T, bf16).reshape(BT, H, hd)
         if _has_ve(cfg, i):
             ve = P[p + "value_embeds"][ids].reshape(BT, H, hd)
             gate = 2.0 * torch.sigmoid(xn[:, :GATE_CH] @ P[p + "ve_gate"].T)   # [BT, H]
@@ -169,13 +224,13 @@ def _torch_step(cfg, W, x_ids, y_ids, B, T, rope_period):
         q, k = _rope(q, cos, sin), _rope(k, cos, sin)
         q = _straight_through(q, q / _rms(q))                       # Q6
         k = _straight_through(k, k / _rms(k))
-        a = _attention(q, k, v, B, T, _window(cfg, i)).reshape(BT, C)
-        x = x + a @ P[p + "c_proj"].T
+        a = _attention(q, k, v, B, T, _window(cfg, i), bf16).reshape(BT, C)
+        x = x + _mm(a, P[p + "c_proj"].T, bf16)
         xn2 = _MlpNorm.apply(x, x_saved)                            # Q7
-        act = torch.relu(xn2 @ P[p + "c_fc"].T) ** 2
-        x = x + act @ P[p + "mlp_proj"].T
+        act = torch.relu(_mm(xn2, P[p + "c_fc"].T, bf16)) ** 2
+        x = x + _mm(act, P[p + "mlp_proj"].T, bf16)
     xf = x / _rms(x)
-    z = xf @ P["lm_head"].T
+    z = _mm(xf, P["lm_head"].T, bf16)
     zc = _straight_through(z, SOFTCAP * torch.tanh(z / SOFTCAP))    # Q4
     tok = torch.logsumexp(zc, -1) - zc[torch.arange(BT), torch.tensor(y_ids)]
     tok.sum().backward()                                            # Q5
