@@ -70,8 +70,18 @@ using TileL = Tile<256, 256, 2, 4>;
 //   (TC, row stride ldc): relu(h)^2 = a gives h = sqrt(a) where h > 0, so
 //   relu_squared_bwd's 2 h (ops.mojo:1126-1140) comes from the activation,
 //   whose bf16 rounding perturbs sqrt(a) by at most 2^-10 relative.
+// QKV (persistent kernel, head-aligned waves): the q | k | v product's
+//   post-processing of qkv_post (ar_fused.hip) on the fp32 accumulators: q and
+//   k rotated by rope_fwd (ops.mojo:209-238) and scaled by their per-head
+//   RMSNorm (ops.mojo:61-104, model.mojo:680-691), v plus gate x value
+//   embedding (ve_apply_fwd, ops.mojo:544-560), each written as bf16 into its
+//   own [M, C] buffer.
+// DOUT_D (persistent kernel, head-aligned waves): C = acc as bf16 (the
+//   attention-output gradient dO of the c_proj dX product) and
+//   D[row, head] = sum_d bf16(dO)[row, d] O[row, d] (flash_attn_bwd_precompute_d,
+//   ops.mojo:329-346, on the bf16 dO the dP products read).
 enum Epi { EPI_STORE = 0, EPI_ACCUM = 1, EPI_PARTIAL = 2, EPI_ADD = 3, EPI_RELU2 = 4, EPI_SOFTCAP = 5,
-           EPI_RELU2_BWD = 6, EPI_AXPBY = 7 };
+           EPI_RELU2_BWD = 6, EPI_AXPBY = 7, EPI_QKV = 8, EPI_DOUT_D = 9 };
 
 template <bool BF16> struct Mfma;
 
@@ -547,21 +557,43 @@ __device__ __forceinline__ void pk_item(int lin, int items, int tiles_n, int til
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-template <bool AK, bool BKM, typename TC, int EPI>
+// Operands of the head-aligned epilogues (EPI_QKV, EPI_DOUT_D).
+struct PkHead {
+    bf16 *q, *k, *v;               // QKV: outputs, [M, cpart] bf16 each
+    const float *cos_t, *sin_t;    // QKV: rope tables [period, HD / 2]
+    int64_t period;                // QKV: table row = row % period
+    const float* gate;             // QKV: [M, H] value-embedding gate (null: none)
+    const float* table;            // QKV: value-embedding table [V, cpart]
+    const int64_t* idx;            // QKV: token ids [M]
+    const float* o;                // DOUT_D: attention output O, fp32 [M, N]
+    float* d;                      // DOUT_D: D, [M, N / HD]
+    int64_t cpart;                 // QKV: columns per part (C); a part starts on a 256-column tile
+};
+
+// HLD = 0: 8 waves of 128 x 64.  HLD = head_dim (32 / 64 / 128): 8 waves of
+// 64 x 128 (4 x 2), so each wave's 128 output columns hold whole heads, for
+// the head-wise epilogues.
+template <bool AK, bool BKM, typename TC, int EPI, int HLD = 0>
 __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, const bf16* B, int64_t M, int64_t N,
                                                      int64_t lda, int64_t ldb, int64_t ldc, int64_t kps,
                                                      int64_t splits, float* partial, const void* aux, void* aux_out,
-                                                     float cap) {
+                                                     float cap, PkHead hx) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     constexpr int OPB = kPkStage / 2;
+    constexpr bool HL = HLD > 0;
+    constexpr int WTM = HL ? 2 : 4, WTN = HL ? 4 : 2;  // 32 x 32 MFMA blocks per wave (rows, columns)
+    static_assert(!HL || (128 % HLD == 0 && HLD >= 32), "head-aligned waves hold whole heads");
+    static_assert(HL == (EPI == EPI_QKV || EPI == EPI_DOUT_D), "head epilogues run on head-aligned waves");
     const int lane = threadIdx.x % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int wm = wave >> 2, wn = wave & 3;
+    const int wm = HL ? wave >> 1 : wave >> 2, wn = HL ? wave & 1 : wave & 3;
+    const int wrow = wm * 32 * WTM, wcol = wn * 32 * WTN;  // the wave's block within the 256 x 256 tile
     // bf16 outputs whose epilogue is element-wise on the product alone: the
     // MFMA operands are swapped so that each accumulator holds a transposed
     // 32 x 32 block (lane l: row l % 32, four consecutive columns per group of
     // four values), and the epilogue stages bf16 instead of fp32 (see below)
-    constexpr bool SW = std::is_same<TC, bf16>::value && (EPI == EPI_STORE || EPI == EPI_RELU2 || EPI == EPI_SOFTCAP);
+    constexpr bool SW = std::is_same<TC, bf16>::value && (EPI == EPI_STORE || EPI == EPI_RELU2 || EPI == EPI_SOFTCAP ||
+                                                          EPI == EPI_QKV || EPI == EPI_DOUT_D);
     const int tiles_n = (int)(N / 256), tiles_mn = (int)(M / 256) * tiles_n, items = tiles_mn * (int)splits;
     const int grid = (int)gridDim.x, b = (int)blockIdx.x;
     const int nk = (int)(kps / kPkBK);
@@ -604,16 +636,16 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
     int aoff[4], boff[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-        const int ra = wm * 128 + r32, rb = wn * 64 + r32;
+        const int ra = wrow + r32, rb = wcol + r32;
         aoff[ks] = (ra * 8 + ((2 * ks + hi) ^ ((ra >> 1) & 7))) * 16;
         boff[ks] = (rb * 8 + ((2 * ks + hi) ^ ((rb >> 1) & 7))) * 16;
     }
 
-    f32x16 acc[4][2];
+    f32x16 acc[WTM][WTN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < WTM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < WTN; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
@@ -632,27 +664,27 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
         if (g + 1 < G) issue(g + 1);
         const unsigned char* sa = smem_raw + (g & 1) * kPkStage;
         const unsigned char* sb = sa + OPB;
-        auto frags = [&](int ks, bf16x8 (&fa)[4], bf16x8 (&fb)[2]) {
+        auto frags = [&](int ks, bf16x8 (&fa)[WTM], bf16x8 (&fb)[WTN]) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < WTM; ++i) {
                 if constexpr (AK) fa[i] = *reinterpret_cast<const bf16x8*>(sa + aoff[ks] + i * 4096);
-                else fa[i] = tr_frag<256>(reinterpret_cast<const bf16*>(sa), wm * 128 + i * 32, ks, lane);
+                else fa[i] = tr_frag<256>(reinterpret_cast<const bf16*>(sa), wrow + i * 32, ks, lane);
             }
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < WTN; ++j) {
                 if constexpr (BKM) fb[j] = *reinterpret_cast<const bf16x8*>(sb + boff[ks] + j * 4096);
-                else fb[j] = tr_frag<256>(reinterpret_cast<const bf16*>(sb), wn * 64 + j * 32, ks, lane);
+                else fb[j] = tr_frag<256>(reinterpret_cast<const bf16*>(sb), wcol + j * 32, ks, lane);
             }
         };
-        bf16x8 fa[2][4], fb[2][2];
+        bf16x8 fa[2][WTM], fb[2][WTN];
         frags(0, fa[0], fb[0]);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             if (ks < 3) frags(ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < WTM; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < WTN; ++j)
                     acc[i][j] = SW ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks & 1][j], fa[ks & 1][i], acc[i][j], 0, 0, 0)
                                    : __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks & 1][i], fb[ks & 1][j], acc[i][j], 0, 0, 0);
         }
@@ -664,8 +696,8 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
         // strips; lane (t, lane/16, lane%16) owns 4 consecutive columns.
         int z, tm, tn;
         pk_item(it * grid + b, items, tiles_n, tiles_mn, z, tm, tn);
-        const int64_t row0 = (int64_t)tm * 256 + wm * 128, col0 = (int64_t)tn * 256 + wn * 64;
-        // this wave's 128 x 64 block: element (r, c) at base + r * ld + c
+        const int64_t row0 = (int64_t)tm * 256 + wrow, col0 = (int64_t)tn * 256 + wcol;
+        // this wave's block: element (r, c) at base + r * ld + c
         const int64_t cbase = row0 * ldc + col0;
         const int clo = lrow * (int)ldc + lcol;
         if constexpr (SW) {
@@ -682,49 +714,151 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
             unsigned char* const bstrip = smem_raw + 2 * kPkStage + wave * 4096;
             const int m = lane & 31, hh = lane >> 5;
             const int rr = lane >> 3, c16 = lane & 7;
-            TC* const lbase = C + cbase + (int64_t)rr * ldc + c16 * 8;
+            // output rows: C, or for QKV the part (q / k / v) buffer this
+            // tile's columns fall in (row stride cpart)
+            TC* obase = C + cbase;
+            int64_t ldo = ldc;
+            int part = 0;
+            int64_t pcol = col0;  // QKV: first column of the wave within its part
+            if constexpr (EPI == EPI_QKV) {
+                part = (int)(col0 / hx.cpart);
+                pcol = col0 - (int64_t)part * hx.cpart;
+                obase = (part == 0 ? hx.q : part == 1 ? hx.k : hx.v) + row0 * hx.cpart + pcol;
+                ldo = hx.cpart;
+            }
+            TC* const lbase = obase + (int64_t)rr * ldo + c16 * 8;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < WTM; ++i) {
+                if constexpr (HL) {
+                    // the lane's values of row row0 + 32 i + m: column group cg = 4 j + g4
+                    // (columns 8 cg + 4 hh + 0..3 of the wave's 128), acc[i][cg / 4][(cg % 4) * 4 + e]
+                    const int64_t row = row0 + i * 32 + m;
+                    constexpr int NH = 128 / HLD, HALF = HLD / 2;
+                    if constexpr (EPI == EPI_QKV) {
+                        if (part < 2) {
+                            // rope_fwd: (x1, x2) -> (x1 c + x2 s, -x1 s + x2 c) on the head's
+                            // halves (column d and d + HD/2: groups cg and cg + HALF / 8, same
+                            // lane), then the head's RMSNorm over its HD values (half in the
+                            // partner lane hh ^ 1)
+                            const int64_t tok = row % hx.period;
+                            const float* ct = hx.cos_t + tok * HALF;
+                            const float* sn = hx.sin_t + tok * HALF;
+                            float ss[NH];
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                            for (int h = 0; h < NH; ++h) ss[h] = 0.f;
 #pragma unroll
-                    for (int g4 = 0; g4 < 4; ++g4) {
-                        float4 x = make_float4(acc[i][j][g4 * 4], acc[i][j][g4 * 4 + 1], acc[i][j][g4 * 4 + 2],
-                                               acc[i][j][g4 * 4 + 3]);
-                        if constexpr (EPI == EPI_RELU2)
-                            x = make_float4(x.x > 0.f ? x.x * x.x : 0.f, x.y > 0.f ? x.y * x.y : 0.f,
-                                            x.z > 0.f ? x.z * x.z : 0.f, x.w > 0.f ? x.w * x.w : 0.f);
-                        else if constexpr (EPI == EPI_SOFTCAP)
-                            x = softcap4(x, cap);
-                        bf16x4 v;
-                        v[0] = (bf16)x.x;
-                        v[1] = (bf16)x.y;
-                        v[2] = (bf16)x.z;
-                        v[3] = (bf16)x.w;
-                        const int c = j * 8 + g4 * 2 + hh;
-                        const int slot = (((c >> 1) ^ (m & 7)) << 1) + ((c & 1) ^ ((m >> 3) & 1));
-                        *reinterpret_cast<bf16x4*>(bstrip + m * 128 + slot * 8) = v;
+                            for (int cg = 0; cg < 16; ++cg) {
+                                constexpr int GPH = HLD / 8;  // column groups per head
+                                if ((cg % GPH) * 8 >= HALF) continue;
+                                const int cgp = cg + HALF / 8, d = (cg % GPH) * 8 + 4 * hh;
+                                const float4 cv = *reinterpret_cast<const float4*>(ct + d);
+                                const float4 sv = *reinterpret_cast<const float4*>(sn + d);
+                                const float cc[4] = {cv.x, cv.y, cv.z, cv.w}, sc[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) {
+                                    const float x1 = acc[i][cg / 4][(cg % 4) * 4 + e];
+                                    const float x2 = acc[i][cgp / 4][(cgp % 4) * 4 + e];
+                                    const float y1 = x1 * cc[e] + x2 * sc[e];
+                                    const float y2 = x1 * (-sc[e]) + x2 * cc[e];
+                                    acc[i][cg / 4][(cg % 4) * 4 + e] = y1;
+                                    acc[i][cgp / 4][(cgp % 4) * 4 + e] = y2;
+                                    ss[cg / GPH] += y1 * y1 + y2 * y2;
+                                }
+                            }
+                            float inv[NH];
+#pragma unroll
+                            for (int h = 0; h < NH; ++h) {
+                                const float t = ss[h] + __shfl_xor(ss[h], 32, kWave);
+                                inv[h] = 1.0f / sqrtf(t / (float)HLD + 1e-5f);  // ops.mojo:61-104 eps
+                            }
+#pragma unroll
+                            for (int cg = 0; cg < 16; ++cg)
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) acc[i][cg / 4][(cg % 4) * 4 + e] *= inv[cg / (HLD / 8)];
+                        } else if (hx.gate) {
+                            // v + gate[row, head] * value_embeds[idx[row]] (ve_apply_fwd)
+                            const int64_t H = hx.cpart / HLD;
+                            const float* ve = hx.table + hx.idx[row] * hx.cpart + pcol;
+                            float g[NH];
+#pragma unroll
+                            for (int h = 0; h < NH; ++h) g[h] = hx.gate[row * H + pcol / HLD + h];
+#pragma unroll
+                            for (int cg = 0; cg < 16; ++cg) {
+                                const float4 e4 = *reinterpret_cast<const float4*>(ve + cg * 8 + 4 * hh);
+                                const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+                                for (int e = 0; e < 4; ++e)
+                                    acc[i][cg / 4][(cg % 4) * 4 + e] += g[cg / (HLD / 8)] * ev[e];
+                            }
+                        }
+                    } else if constexpr (EPI == EPI_DOUT_D) {
+                        // D[row, head] = sum over the head's columns of bf16(dO) * O
+                        const float* orow = hx.o + row * ldc + col0;
+                        float ds[NH];
+#pragma unroll
+                        for (int h = 0; h < NH; ++h) ds[h] = 0.f;
+#pragma unroll
+                        for (int cg = 0; cg < 16; ++cg) {
+                            const float4 o4 = *reinterpret_cast<const float4*>(orow + cg * 8 + 4 * hh);
+                            const float ov[4] = {o4.x, o4.y, o4.z, o4.w};
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                ds[cg / (HLD / 8)] += (float)(bf16)acc[i][cg / 4][(cg % 4) * 4 + e] * ov[e];
+                        }
+                        const int64_t H = N / HLD;
+#pragma unroll
+                        for (int h = 0; h < NH; ++h) {
+                            const float t = ds[h] + __shfl_xor(ds[h], 32, kWave);
+                            if (hh == 0) hx.d[row * H + col0 / HLD + h] = t;
+                        }
                     }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    const int r = p * 8 + rr;
-                    u32x4 q = *reinterpret_cast<const u32x4*>(bstrip + r * 128 + ((c16 ^ (r & 7)) << 4));
-                    if (p & 1) q = __builtin_shufflevector(q, q, 2, 3, 0, 1);  // r / 8 odd
-                    __builtin_nontemporal_store(q, reinterpret_cast<u32x4*>(lbase + (int64_t)(i * 32 + p * 8) * ldc));
                 }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int jp = 0; jp < WTN / 2; ++jp) {
+#pragma unroll
+                    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                        for (int g4 = 0; g4 < 4; ++g4) {
+                            const int j = 2 * jp + jj;
+                            float4 x = make_float4(acc[i][j][g4 * 4], acc[i][j][g4 * 4 + 1], acc[i][j][g4 * 4 + 2],
+                                                   acc[i][j][g4 * 4 + 3]);
+                            if constexpr (EPI == EPI_RELU2)
+                                x = make_float4(x.x > 0.f ? x.x * x.x : 0.f, x.y > 0.f ? x.y * x.y : 0.f,
+                                                x.z > 0.f ? x.z * x.z : 0.f, x.w > 0.f ? x.w * x.w : 0.f);
+                            else if constexpr (EPI == EPI_SOFTCAP)
+                                x = softcap4(x, cap);
+                            bf16x4 v;
+                            v[0] = (bf16)x.x;
+                            v[1] = (bf16)x.y;
+                            v[2] = (bf16)x.z;
+                            v[3] = (bf16)x.w;
+                            const int c = jj * 8 + g4 * 2 + hh;
+                            const int slot = (((c >> 1) ^ (m & 7)) << 1) + ((c & 1) ^ ((m >> 3) & 1));
+                            *reinterpret_cast<bf16x4*>(bstrip + m * 128 + slot * 8) = v;
+                        }
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        const int r = p * 8 + rr;
+                        u32x4 q = *reinterpret_cast<const u32x4*>(bstrip + r * 128 + ((c16 ^ (r & 7)) << 4));
+                        if (p & 1) q = __builtin_shufflevector(q, q, 2, 3, 0, 1);  // r / 8 odd
+                        __builtin_nontemporal_store(
+                            q, reinterpret_cast<u32x4*>(lbase + (int64_t)(i * 32 + p * 8) * ldo + jp * 64));
+                    }
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                }
+#pragma unroll
+                for (int j = 0; j < WTN; ++j)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
             }
             continue;
         }
+        if constexpr (!HL) {
         constexpr bool PRE = EPI == EPI_ACCUM || EPI == EPI_ADD || EPI == EPI_RELU2_BWD;
         // The operand the epilogue combines with (C, the residual or the
         // pre-activation) is loaded one half strip ahead, into a two-slot
@@ -793,6 +927,7 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
         }
+        }  // !HL
     }
 }
 
@@ -950,7 +1085,7 @@ static int32_t pk_launch(hipStream_t st, TC* C, const bf16* A, const bf16* B, in
     const int64_t kps = gk / splits, items = (gm / 256) * (gn / 256) * splits;
     const int cus = pk_cus();
     const unsigned grid = (unsigned)(items < cus ? items : cus);
-#define AR_PK(E)                                                                                                      do {                                                                                                                  static bool attr_set = false;                                                                                     if (!attr_set) {                                                                                                      if (hipFuncSetAttribute((const void*)gemm_pk<AK, BKM, TC, E>,                                                                              hipFuncAttributeMaxDynamicSharedMemorySize, kPkLds) != hipSuccess)                            return set_error(AR_EHIP, "%s: cannot set the LDS size", nm);                                                 attr_set = true;                                                                                              }                                                                                                                 gemm_pk<AK, BKM, TC, E><<<grid, kPkThreads, kPkLds, st>>>(C, A, B, gm, gn, lda, ldb, ldc, kps, splits,                                                                       partial, aux, aux_out, cap);                         } while (0)
+#define AR_PK(E)                                                                                                      do {                                                                                                                  static bool attr_set = false;                                                                                     if (!attr_set) {                                                                                                      if (hipFuncSetAttribute((const void*)gemm_pk<AK, BKM, TC, E>,                                                                              hipFuncAttributeMaxDynamicSharedMemorySize, kPkLds) != hipSuccess)                            return set_error(AR_EHIP, "%s: cannot set the LDS size", nm);                                                 attr_set = true;                                                                                              }                                                                                                                 gemm_pk<AK, BKM, TC, E><<<grid, kPkThreads, kPkLds, st>>>(C, A, B, gm, gn, lda, ldb, ldc, kps, splits,                                                                       partial, aux, aux_out, cap, PkHead{});                         } while (0)
     if (epi >= 0) {
         if (splits != 1) return set_error(AR_EINVAL, "%s: fused epilogues take no reduction split", nm);
         if constexpr (AK) {  // fused epilogues exist for the NT and NN layouts only
@@ -976,6 +1111,69 @@ static int32_t pk_launch(hipStream_t st, TC* C, const bf16* A, const bf16* B, in
 #undef AR_PK
     splitk_reduce<TC>(st, C, partial, gm, gn, ldc, splits, accumulate, 1, 0);
     return check_launch(nm);
+}
+
+// NT product on the head-aligned persistent kernel with a head epilogue
+// (EPI_QKV / EPI_DOUT_D); hd selects the instance.
+template <int EPI>
+static int32_t pk_head_launch(hipStream_t st, bf16* C, const bf16* A, const bf16* B, int64_t gm, int64_t gn, int64_t gk,
+                              int64_t ldc, const PkHead& hx, int64_t hd, const char* nm) {
+    const int64_t items = (gm / 256) * (gn / 256);
+    const int cus = pk_cus();
+    const unsigned grid = (unsigned)(items < cus ? items : cus);
+#define AR_PKH(HD)                                                                                                   \
+    do {                                                                                                             \
+        static bool attr_set = false;                                                                                \
+        if (!attr_set) {                                                                                             \
+            if (hipFuncSetAttribute((const void*)gemm_pk<true, true, bf16, EPI, HD>,                                 \
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kPkLds) != hipSuccess)               \
+                return set_error(AR_EHIP, "%s: cannot set the LDS size", nm);                                        \
+            attr_set = true;                                                                                         \
+        }                                                                                                            \
+        gemm_pk<true, true, bf16, EPI, HD><<<grid, kPkThreads, kPkLds, st>>>(C, A, B, gm, gn, gk, gk, ldc, gk, 1,     \
+                                                                             nullptr, nullptr, nullptr, 0.f, hx);    \
+    } while (0)
+    if (hd == 128) AR_PKH(128);
+    else if (hd == 64) AR_PKH(64);
+    else return set_error(AR_EUNSUPPORTED, "%s: head_dim %lld", nm, (long long)hd);
+#undef AR_PKH
+    return check_launch(nm);
+}
+
+bool gemm_head_fusable(int64_t M, int64_t C, int64_t hd) {
+    return (hd == 64 || hd == 128) && C % 256 == 0 && pk_shape(M, 3 * C, C) && pk_shape(M, C, C) &&
+           3 * C < (1 << 22);
+}
+
+int32_t gemm_qkv_fused(hipStream_t st, bf16* q, bf16* k, bf16* v, const bf16* xn, const bf16* w, int64_t M, int64_t C,
+                       int64_t hd, const float* cos_t, const float* sin_t, int64_t period, const float* gate,
+                       const float* table, const int64_t* idx) {
+    if (!((hd == 64 || hd == 128) && C % 256 == 0 && period > 0 && pk_ok(M, 3 * C, C, C, C, C, xn, w, q) &&
+          ((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15) == 0))
+        return AR_EUNSUPPORTED;
+    PkHead hx{};
+    hx.q = q;
+    hx.k = k;
+    hx.v = v;
+    hx.cos_t = cos_t;
+    hx.sin_t = sin_t;
+    hx.period = period;
+    hx.gate = gate;
+    hx.table = table;
+    hx.idx = idx;
+    hx.cpart = C;
+    return pk_head_launch<EPI_QKV>(st, q, xn, w, M, 3 * C, C, 3 * C, hx, hd, "linear_fwd (q|k|v, fused post)");
+}
+
+int32_t gemm_dout_d_fused(hipStream_t st, bf16* dout, float* d, const bf16* gy, const bf16* wt, const float* o,
+                          int64_t M, int64_t C, int64_t hd) {
+    if (!((hd == 64 || hd == 128) && pk_ok(M, C, C, C, C, C, gy, wt, dout) &&
+          (reinterpret_cast<uintptr_t>(o) & 15) == 0))
+        return AR_EUNSUPPORTED;
+    PkHead hx{};
+    hx.o = o;
+    hx.d = d;
+    return pk_head_launch<EPI_DOUT_D>(st, dout, gy, wt, M, C, C, C, hx, hd, "linear_bwd_dx (c_proj, fused D)");
 }
 
 // Large tiles when the problem has enough of them to fill the chip, or when

@@ -36,6 +36,23 @@ enum { GEMM_EPI_ADD = 3, GEMM_EPI_RELU2 = 4, GEMM_EPI_SOFTCAP = 5, GEMM_EPI_RELU
 int32_t gemm_epilogue(hipStream_t st, int layout, int epi, void* C, int c_bf16, const void* X, int x_bf16,
                       const void* W, int w_bf16, int64_t M, int64_t N, int64_t K, const void* aux, void* aux_out,
                       float cap);
+// Whether gemm_qkv_fused / gemm_dout_d_fused take this shape.
+bool gemm_head_fusable(int64_t M, int64_t C, int64_t hd);
+// The bf16 step's q|k|v forward product xn [M, C] . Wqkv [3C, C]^T with
+// qkv_post fused into its epilogue (persistent kernel, head-aligned waves):
+// q and k rotated (table row = row % period) and head-normed, v plus
+// gate x table[idx] when gate is set, each as bf16 [M, C].  The rope and the
+// norm act on the fp32 products (qkv_post rounds them to bf16 first).
+// AR_EUNSUPPORTED (nothing launched) when the shape does not fit: head_dim
+// 64 / 128, C % 256 == 0, M % 256 == 0.
+int32_t gemm_qkv_fused(hipStream_t st, bf16* q, bf16* k, bf16* v, const bf16* xn, const bf16* w, int64_t M, int64_t C,
+                       int64_t hd, const float* cos_t, const float* sin_t, int64_t period, const float* gate,
+                       const float* table, const int64_t* idx);
+// The c_proj dX product dO = gy [M, C] . wt [C, C]^T (bf16 out) with
+// D[row, head] = sum_d bf16(dO) O (fp32 O [M, C]) in its epilogue, [M, C / hd].
+// AR_EUNSUPPORTED when the shape does not fit (as gemm_qkv_fused).
+int32_t gemm_dout_d_fused(hipStream_t st, bf16* dout, float* d, const bf16* gy, const bf16* wt, const float* o,
+                          int64_t M, int64_t C, int64_t hd);
 // Batched GEMM-space form: C_b[mo,no] = sum_r A_b(mo,r) B_b(no,r); ak / bk
 // select K-major (r contiguous, row stride lda/ldb) vs MN-major storage.
 // With aux: C_b = alpha * (A_b B_b^T) + beta * aux_b (aux laid out as C).

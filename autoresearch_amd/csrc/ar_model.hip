@@ -90,6 +90,9 @@ struct ar_gpt {
     // bf16 dS tiles of one layer's attention backward (written by the dK / dV
     // kernel, read by the dQ product)
     ar::bf16* ds_buf = nullptr;
+    // qkv_post fused into the q|k|v product and D = rowsum(dO O) into the
+    // c_proj dX product (head-aligned persistent GEMM), when the shape allows
+    bool fuse_heads = false;
     float grad_logits_scale = 0.f;  // loss_scale baked into grad_logits_b
     bool grad_logits_valid = false;
     // step-dependent optimizer scalars in device memory (StepScalars)
@@ -402,6 +405,9 @@ static int32_t gpt_build(ar_gpt* m) {
             if (end == e || *end != '\0' || ds_max < 0)
                 return set_error(AR_EINVAL, "gpt: AR_ATTN_DS_MAX_BYTES='%s' is not a non-negative byte count", e);
         }
+        // AR_FUSE_HEADS=0 keeps the separate qkv_post / D kernels (A/B runs, tests)
+        const char* fh = getenv("AR_FUSE_HEADS");
+        m->fuse_heads = !(fh && strcmp(fh, "0") == 0) && gemm_head_fusable(BT, C, hd);
         const int64_t ds_elems = flash_ds_elems(m->B, m->T, H);
         if (ds_elems * (int64_t)sizeof(bf16) <= ds_max) {
             void* p = nullptr;
@@ -594,10 +600,20 @@ static int32_t forward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* tar
         AR_TRY(resid_norm(st, i == 0 ? 0 : 1, m->x0, b.x, b.rms_attn, b.xn, ve ? b.xg : nullptr,
                           ve ? b.gate : nullptr, m->x, m->x0, P(m, m->i_wte), inputs, P(m, m->i_res), P(m, m->i_x0),
                           i, ve ? P(m, m->i_gate[i]) : nullptr, H, kGateChannels, BT, C));
-        // c_q | c_k | c_v: one [3C, C] weight
-        AR_TRY(gemm_b(m, 0, 0, m->qkv, true, b.xn, true, Wb(m, m->i_q[i]), true, BT, 3 * C, C, false));
-        AR_TRY(qkv_post(st, b.q, b.k, b.v, m->qkv, m->rope_cos, m->rope_sin, m->period, b.gate,
-                        ve ? P(m, m->i_ve[i]) : nullptr, inputs, BT, C, H, hd));
+        // c_q | c_k | c_v: one [3C, C] weight; rope + head norm of q / k and the
+        // value-embedding add of v in its epilogue, or in qkv_post after it
+        if (m->fuse_heads) {
+            const int e = prof_begin(m);
+            const int32_t r = gemm_qkv_fused(st, b.q, b.k, b.v, b.xn, Wb(m, m->i_q[i]), BT, C, hd, m->rope_cos,
+                                             m->rope_sin, m->period, ve ? b.gate : nullptr,
+                                             ve ? P(m, m->i_ve[i]) : nullptr, inputs);
+            prof_end(m, e, 0, 2.0 * BT * 3 * C * C);
+            AR_TRY(r);
+        } else {
+            AR_TRY(gemm_b(m, 0, 0, m->qkv, true, b.xn, true, Wb(m, m->i_q[i]), true, BT, 3 * C, C, false));
+            AR_TRY(qkv_post(st, b.q, b.k, b.v, m->qkv, m->rope_cos, m->rope_sin, m->period, b.gate,
+                            ve ? P(m, m->i_ve[i]) : nullptr, inputs, BT, C, H, hd));
+        }
         FlashOut fo;
         fo.b1 = b.attn_out_b;
         AR_TRY(attention_b(m, AttnOp::FWD, b.attn_out, b.lse, fo, b.q, b.k, b.v, nullptr, nullptr, nullptr,
@@ -653,9 +669,17 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
         AR_TRY(gemm_b(m, 2, 2, G(m, m->i_fc[i]), false, m->grad_h, true, b.xn_mlp, true, BT, F, C, true));
         AR_TRY(norm_bwd(st, 1, m->grad_x, m->grad_xb, nullptr, b.x, b.rms_mlp, nullptr, nullptr, 0, nullptr, nullptr,
                         nullptr, BT, C, m->grad_x_norm_b));  // Q7: saved x of the layer
-        // attention output projection
-        AR_TRY(gemm_b(m, 1, 0, m->grad_attn_out_b, true, m->grad_xb, true, WbT(m, m->i_proj[i]), true, BT, C, C,
-                      false));
+        // attention output projection (with D = rowsum(dO O) in its epilogue when fused)
+        if (m->fuse_heads) {
+            const int e = prof_begin(m);
+            const int32_t r = gemm_dout_d_fused(st, m->grad_attn_out_b, m->d_buf, m->grad_xb, WbT(m, m->i_proj[i]),
+                                                b.attn_out, BT, C, hd);
+            prof_end(m, e, 1, 2.0 * BT * C * C);
+            AR_TRY(r);
+        } else {
+            AR_TRY(gemm_b(m, 1, 0, m->grad_attn_out_b, true, m->grad_xb, true, WbT(m, m->i_proj[i]), true, BT, C, C,
+                          false));
+        }
         AR_TRY(gemm_b(m, 2, 2, G(m, m->i_proj[i]), false, m->grad_xb, true, b.attn_out_b, true, BT, C, C, true));
         const int64_t ws = window_size(c, i);
         // dQ | dK | dV straight into the packed bf16 [BT, 3C] buffer, dQ / dK
@@ -672,7 +696,7 @@ static int32_t backward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* ta
         fo.b1 = m->grad_qkv + C;
         fo.b2 = m->grad_qkv + 2 * C;
         fo.ds = m->ds_buf;
-        AR_TRY(flash_d_bf16(st, m->d_buf, b.attn_out, m->grad_attn_out_b, m->B, m->T, H, hd));
+        if (!m->fuse_heads) AR_TRY(flash_d_bf16(st, m->d_buf, b.attn_out, m->grad_attn_out_b, m->B, m->T, H, hd));
         AR_TRY(attention_b(m, AttnOp::DKV, nullptr, nullptr, fo, b.q, b.k, b.v, m->grad_attn_out_b, b.lse, m->d_buf,
                            ws));
         fo.b1 = m->grad_qkv;

@@ -414,6 +414,40 @@ def test_full_size_step_properties(cfg, B, precision):
     assert runs[0][2] == runs[1][2]
 
 
+def test_fused_head_epilogues_match_separate_kernels(monkeypatch):
+    """The bf16 step with qkv_post fused into the q|k|v product's epilogue and
+    D = rowsum(dO O) into the c_proj dX product's (head-aligned persistent
+    GEMM) against the same step with the separate qkv_post / D kernels
+    (AR_FUSE_HEADS=0), at a shape the fused path takes (B*T and C multiples
+    of 256, head_dim 128, value-embedding layers).  The fused rope / norm act on
+    the fp32 products, qkv_post on their bf16 rounding, so the two agree to
+    bf16 rounding, not bit for bit; both are checked against the oracle by the
+    whole-step tests."""
+    import gpu_util as gu
+    from autoresearch_amd.model import GPT, GPTConfig
+    x, y = _tokens(21, 2, 256, WIDE["vocab_size"])
+    xd, yd = gu.dev(x), gu.dev(y)
+    out = []
+    for fuse in ("0", None):
+        if fuse is None:
+            monkeypatch.delenv("AR_FUSE_HEADS", raising=False)
+        else:
+            monkeypatch.setenv("AR_FUSE_HEADS", fuse)
+        gm = GPT(GPTConfig(**WIDE), 2, 256, precision=1, rope_period=256)
+        gm.init_weights(8)
+        gm.train_step(xd, yd, 0.0)  # step 1 makes c_proj non-zero
+        gm.zero_grads()
+        loss = gm.forward(xd, yd)
+        gm.backward(xd, yd, 1.0)
+        out.append((loss, _by_name(gu.host(gm.grads()).copy(), gm.tensors())))
+        gm.close()
+    (l0, g0), (l1, g1) = out
+    assert abs(l1 - l0) <= 1e-4 * abs(l0), (l0, l1)
+    for n in g0:
+        if np.linalg.norm(g0[n]) > 0:
+            assert rel_err(g1[n], g0[n]) <= TOL_BF16, (n, rel_err(g1[n], g0[n]))
+
+
 def test_step_is_deterministic():
     """Two models from the same seed and batch give bit-identical losses,
     gradients and weights (no float atomics anywhere on the step)."""
