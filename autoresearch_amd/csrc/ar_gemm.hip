@@ -35,6 +35,8 @@
 //     (deterministic; the reference's single-block loop over M is serial).
 #include "ar_internal.hpp"
 
+#include <stdlib.h>
+
 #include <mutex>
 #include <type_traits>
 
@@ -521,8 +523,9 @@ constexpr int kPkLds = 2 * kPkStage + 8 * 16 * 64 * 4;                      // 1
 
 template <int N>
 __device__ __forceinline__ void vm_wait() {
-    static_assert(N >= 0 && N < 16, "vmcnt");
-    __builtin_amdgcn_s_waitcnt(N | 0x0F70);  // vmcnt(N), expcnt / lgkmcnt not waited
+    // vmcnt(N) (6 bits: [3:0] and [15:14] of the encoding); expcnt / lgkmcnt not waited
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
 // Per-lane byte offsets of the 4 DMA wave-instructions that fill one operand

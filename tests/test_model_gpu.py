@@ -419,33 +419,33 @@ def test_fused_head_epilogues_match_separate_kernels(monkeypatch):
     D = rowsum(dO O) into the c_proj dX product's (head-aligned persistent
     GEMM) against the same step with the separate qkv_post / D kernels
     (AR_FUSE_HEADS=0), at a shape the fused path takes (B*T and C multiples
-    of 256, head_dim 128, value-embedding layers).  The fused rope / norm act on
-    the fp32 products, qkv_post on their bf16 rounding, so the two agree to
-    bf16 rounding, not bit for bit; both are checked against the oracle by the
-    whole-step tests."""
-    import gpu_util as gu
-    from autoresearch_amd.model import GPT, GPTConfig
-    x, y = _tokens(21, 2, 256, WIDE["vocab_size"])
-    xd, yd = gu.dev(x), gu.dev(y)
-    out = []
+    of 256, head_dim 128, value-embedding layers).  The fused rope / norm act
+    on the fp32 products and qkv_post on their bf16 rounding, so the two differ
+    by bf16 rounding; each is compared with the oracle, and the fused path
+    must be as close to it as the separate kernels are (every gradient and the
+    post-step weights, two steps)."""
+    errs = []
     for fuse in ("0", None):
         if fuse is None:
             monkeypatch.delenv("AR_FUSE_HEADS", raising=False)
         else:
             monkeypatch.setenv("AR_FUSE_HEADS", fuse)
-        gm = GPT(GPTConfig(**WIDE), 2, 256, precision=1, rope_period=256)
-        gm.init_weights(8)
-        gm.train_step(xd, yd, 0.0)  # step 1 makes c_proj non-zero
-        gm.zero_grads()
-        loss = gm.forward(xd, yd)
-        gm.backward(xd, yd, 1.0)
-        out.append((loss, _by_name(gu.host(gm.grads()).copy(), gm.tensors())))
-        gm.close()
-    (l0, g0), (l1, g1) = out
-    assert abs(l1 - l0) <= 1e-4 * abs(l0), (l0, l1)
-    for n in g0:
-        if np.linalg.norm(g0[n]) > 0:
-            assert rel_err(g1[n], g0[n]) <= TOL_BF16, (n, rel_err(g1[n], g0[n]))
+        _, _, res = _run(WIDE, 2, 256, 1, 256, 8, steps=2)
+        e = {}
+        for st, r in enumerate(res):
+            go, gg = r["grads"]
+            for n in go:
+                if n not in ("resid_lambdas", "x0_lambdas") and np.linalg.norm(go[n]) > 0:
+                    e[f"step{st}:grad:{n}"] = rel_err(gg[n], go[n])
+            po, pg = r["params"]
+            for n in po:
+                e[f"step{st}:param:{n}"] = rel_err(pg[n], po[n])
+        errs.append(e)
+    sep, fused = errs
+    worst = max(sep, key=lambda k: fused[k] / (sep[k] + 1e-30))
+    print(f"MARGIN fused/separate worst {worst}: {fused[worst]:.3e} vs {sep[worst]:.3e}")
+    for k in sep:
+        assert fused[k] <= 1.5 * sep[k] + 1e-4, (k, fused[k], sep[k])
 
 
 def test_step_is_deterministic():
