@@ -934,6 +934,245 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
     }
 }
 
+// ---- row-complete persistent GEMM (512 output columns per row) ----
+// The forward's residual products whose output rows feed an RMSNorm (c_proj
+// and mlp_proj at C = 512): one 512-thread workgroup per CU walks 128-row
+// items, each the whole 128 x 512 output block, so the epilogue holds complete
+// rows and runs the row pass of resid_norm (ar_fused.hip) itself:
+//   x = r + acc (the residual add), or for the next layer's input
+//   x = sa[l] (r + acc) + sb[l] x0 (scaled_add_fwd, ops.mojo:579-594);
+//   x (fp32), rms = sqrt(mean(x^2) + 1e-5) (ops.mojo:61-104), xn = bf16(x / rms),
+//   and on value-embedding layers xg = (x / rms)[:, :32] (fp32) and
+//   gate[h] = 2 sigmoid(sum_c w[h, c] xg[c]) (ve_gate_fwd, ops.mojo:516-541).
+// Same data movement as gemm_pk (direct-to-LDS copies, two stages, the stream
+// of k-tiles running across items): A tile 128 x 64, B tile 512 x 64 (80 KB
+// per stage).  8 waves of 64 x 128 (2 x 4) with transposed accumulators (lane:
+// one row, four consecutive columns per group), so a row's sum of squares is a
+// lane sum, one exchange with lane ^ 32 and a four-wave sum through LDS (the
+// stage the item's last k-tile used) in a fixed order.
+constexpr int kRcBM = 128, kRcN = 512;
+constexpr int kRcOpA = kRcBM * kPkBK * 2, kRcOpB = kRcN * kPkBK * 2, kRcStage = kRcOpA + kRcOpB;
+constexpr int kRcLds = 2 * kRcStage;  // 160 KB
+
+struct RcArgs {
+    const float* r;       // residual, fp32 [M, 512] (may alias x_out)
+    float* x_out;         // fp32 [M, 512]
+    float* rms_out;       // [M]
+    bf16* xn_out;         // bf16 [M, 512]
+    const float* x0;      // scaled form: x0 [M, 512]
+    const float* sa;      // scaled form: sa[layer], sb[layer]
+    const float* sb;
+    int64_t layer;
+    float* xg_out;        // value-embedding gate (gate_out null: none): xg [M, 32]
+    float* gate_out;      // gate [M, nkv]
+    const float* gate_w;  // [nkv, 32]
+    int nkv;
+};
+
+template <bool SCALED>
+__global__ __launch_bounds__(kPkThreads) void gemm_rc(const bf16* A, const bf16* B, int64_t M, int64_t K, int64_t lda,
+                                                     int64_t ldb, RcArgs ra) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    const int lane = threadIdx.x % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int wm = wave >> 2, wn = wave & 3;
+    const int items = (int)(M / kRcBM);
+    const int grid = (int)gridDim.x, b = (int)blockIdx.x;
+    const int nk = (int)(K / kPkBK);
+    const int nmine = (items - b + grid - 1) / grid;
+    const int G = nmine * nk;
+
+    // copies: slot j * 512 + wave * 64 + lane of a tile (A: j < 2, B: j < 8),
+    // K-major layout (unit c of row r at r * 8 + (c ^ ((r >> 1) & 7)))
+    unsigned aoffs[2], boffs[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int slot = j * kPkThreads + wave * 64 + lane;
+        const int r = slot >> 3, c = (slot & 7) ^ ((r >> 1) & 7);
+        if (j < 2) aoffs[j] = (unsigned)(r * lda + c * 8) * 2u;
+        boffs[j] = (unsigned)(r * ldb + c * 8) * 2u;
+    }
+    const unsigned lds0 = lds_addr(smem_raw) + wave * 1024;
+    int di = 0, dkt = 0;
+    const char* pa = reinterpret_cast<const char*>(A);
+    const char* pb = reinterpret_cast<const char*>(B);
+    auto issue = [&](int g) {
+        if (dkt == 0) {
+            pa = reinterpret_cast<const char*>(A) + 2 * (int64_t)(di * grid + b) * kRcBM * lda;
+            pb = reinterpret_cast<const char*>(B);
+        }
+        const unsigned st = lds0 + (g & 1) * kRcStage;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) dma16s(pa, aoffs[j], st + j * 8192);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dma16s(pb, boffs[j], st + kRcOpA + j * 8192);
+        pa += 2 * kPkBK;
+        pb += 2 * kPkBK;
+        if (++dkt == nk) {
+            dkt = 0;
+            ++di;
+        }
+    };
+
+    const int r32 = lane & 31, hi = lane >> 5;
+    int aoff[4], boff[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const int rA = wm * 64 + r32, rB = wn * 128 + r32;
+        aoff[ks] = (rA * 8 + ((2 * ks + hi) ^ ((rA >> 1) & 7))) * 16;
+        boff[ks] = (rB * 8 + ((2 * ks + hi) ^ ((rB >> 1) & 7))) * 16;
+    }
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+    float sa = 0.f, sb = 0.f;
+    if constexpr (SCALED) {
+        sa = ra.sa[ra.layer];
+        sb = ra.sb[ra.layer];
+    }
+
+    if (G > 0) issue(0);
+    int ckt = 0, ci = 0;
+    for (int g = 0; g < G; ++g) {
+        vm_wait<0>();
+        __builtin_amdgcn_s_barrier();
+        if (g + 1 < G) issue(g + 1);
+        const unsigned char* sa_ = smem_raw + (g & 1) * kRcStage;
+        const unsigned char* sb_ = sa_ + kRcOpA;
+        auto frags = [&](int ks, bf16x8 (&fa)[2], bf16x8 (&fb)[4]) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) fa[i] = *reinterpret_cast<const bf16x8*>(sa_ + aoff[ks] + i * 4096);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fb[j] = *reinterpret_cast<const bf16x8*>(sb_ + boff[ks] + j * 4096);
+        };
+        bf16x8 fa[2][2], fb[2][4];
+        frags(0, fa[0], fb[0]);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            if (ks < 3) frags(ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks & 1][j], fa[ks & 1][i], acc[i][j], 0, 0,
+                                                                         0);
+        }
+        if (++ckt != nk) continue;
+        ckt = 0;
+        const int it = ci++;
+
+        // Epilogue.  Lane (m, hh): row row0 + 32 i + m, columns 128 wn +
+        // 8 cg + 4 hh + 0..3 (cg = 4 j + g4) = acc[i][j][4 g4 + 0..3].
+        __syncthreads();  // every wave is done with stage g & 1: it holds the row sums
+        float* const red = reinterpret_cast<float*>(smem_raw + (g & 1) * kRcStage);  // [wm][i][wn][32]
+        const int m = lane & 31, hh = lane >> 5;
+        const int64_t row0 = ((int64_t)it * grid + b) * kRcBM + wm * 64;  // local item it is item it * grid + b
+        const int col0 = wn * 128 + 4 * hh;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int64_t row = row0 + i * 32 + m;
+            const float* rrow = ra.r + row * kRcN + col0;
+            const float* xrow = SCALED ? ra.x0 + row * kRcN + col0 : nullptr;
+            float p = 0.f;
+#pragma unroll
+            for (int cg = 0; cg < 16; ++cg) {
+                const float4 r4 = *reinterpret_cast<const float4*>(rrow + cg * 8);
+                const float rv[4] = {r4.x, r4.y, r4.z, r4.w};
+                float xv[4] = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (SCALED) {
+                    const float4 x4 = *reinterpret_cast<const float4*>(xrow + cg * 8);
+                    xv[0] = x4.x;
+                    xv[1] = x4.y;
+                    xv[2] = x4.z;
+                    xv[3] = x4.w;
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float v = rv[e] + acc[i][cg / 4][(cg % 4) * 4 + e];
+                    if constexpr (SCALED) v = sa * v + sb * xv[e];
+                    acc[i][cg / 4][(cg % 4) * 4 + e] = v;
+                    p += v * v;
+                }
+            }
+            p += __shfl_xor(p, 32, kWave);
+            if (hh == 0) red[((wm * 2 + i) * 4 + wn) * 32 + m] = p;
+        }
+        __syncthreads();
+        // Outputs through a wave-private strip (32 rows x 64 columns, fp32) in
+        // the same stage, read back row-contiguous (lane: row 4 t + lane / 16,
+        // columns 4 (lane % 16)), so that x and xn go out as whole row segments.
+        constexpr int SLD = 68;
+        float* const strip = reinterpret_cast<float*>(smem_raw + (g & 1) * kRcStage + 2048) + wave * 32 * SLD;
+        auto row_rms = [&](int i, int rl) {
+            const float* rp = red + (wm * 2 + i) * 4 * 32 + rl;
+            const float ss = ((rp[0] + rp[32]) + rp[64]) + rp[96];
+            return sqrtf(ss / (float)kRcN + 1e-5f);
+        };
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int64_t rowb = row0 + i * 32;
+            if (wn == 0 && lane < 32) ra.rms_out[rowb + lane] = row_rms(i, lane);
+#pragma unroll
+            for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+                for (int cg = 0; cg < 8; ++cg) {
+                    const int j = (pass * 8 + cg) / 4, v0 = ((pass * 8 + cg) % 4) * 4;
+                    *reinterpret_cast<float4*>(strip + m * SLD + cg * 8 + 4 * hh) =
+                        make_float4(acc[i][j][v0], acc[i][j][v0 + 1], acc[i][j][v0 + 2], acc[i][j][v0 + 3]);
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const int rl = t * 4 + (lane >> 4), c4 = (lane & 15) * 4;
+                    const float4 x4 = *reinterpret_cast<const float4*>(strip + rl * SLD + c4);
+                    const float rms = row_rms(i, rl);
+                    const int64_t o = (rowb + rl) * kRcN + wn * 128 + pass * 64 + c4;
+                    st4nt(ra.x_out + o, x4);
+                    st4nt(ra.xn_out + o, make_float4(x4.x / rms, x4.y / rms, x4.z / rms, x4.w / rms));
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+            if (ra.gate_out && wn == 0) {
+                // channels 0..31: groups cg 0..3 of the wn = 0 waves (this lane:
+                // 8 cg + 4 hh + 0..3), the rest in lane ^ 32; the normalised
+                // values in fp32
+                const int64_t row = rowb + m;
+                const float rms = row_rms(i, m);
+                float nv[16];
+#pragma unroll
+                for (int v = 0; v < 16; ++v) nv[v] = acc[i][0][v] / rms;
+                float* xg = ra.xg_out + row * 32 + 4 * hh;
+#pragma unroll
+                for (int cg = 0; cg < 4; ++cg)
+                    *reinterpret_cast<float4*>(xg + cg * 8) =
+                        make_float4(nv[cg * 4], nv[cg * 4 + 1], nv[cg * 4 + 2], nv[cg * 4 + 3]);
+                for (int h = 0; h < ra.nkv; ++h) {
+                    const float* w = ra.gate_w + h * 32 + 4 * hh;
+                    float q = 0.f;
+#pragma unroll
+                    for (int cg = 0; cg < 4; ++cg)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) q += w[cg * 8 + e] * nv[cg * 4 + e];
+                    q += __shfl_xor(q, 32, kWave);
+                    if (hh == 0) ra.gate_out[row * ra.nkv + h] = 2.0f * (1.0f / (1.0f + __expf(-q)));
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+        }
+    }
+}
+
 // Vector form of splitk_reduce_k (N % 4 == 0, ldc % 4 == 0, 16-byte aligned
 // partial / C): four columns per thread, the split partials' loads issued
 // eight at a time ahead of their in-order adds (same order as the scalar form).
@@ -1141,6 +1380,40 @@ static int32_t pk_head_launch(hipStream_t st, bf16* C, const bf16* A, const bf16
     else return set_error(AR_EUNSUPPORTED, "%s: head_dim %lld", nm, (long long)hd);
 #undef AR_PKH
     return check_launch(nm);
+}
+
+bool gemm_rc_fusable(int64_t M, int64_t C, int64_t K) {
+    return C == kRcN && M > 0 && M % kRcBM == 0 && K > 0 && K % kPkBK == 0 && K < (1 << 20) &&
+           M / kRcBM < (1 << 30) / (K / kPkBK);
+}
+
+int32_t gemm_rc_norm(hipStream_t st, const bf16* A, const bf16* W, int64_t M, int64_t K, const float* r, float* x_out,
+                     float* rms_out, bf16* xn_out, const float* x0, const float* sa, const float* sb, int64_t layer,
+                     float* xg_out, float* gate_out, const float* gate_w, int64_t nkv) {
+    if (!gemm_rc_fusable(M, kRcN, K) || ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(W) |
+                                          reinterpret_cast<uintptr_t>(r) | reinterpret_cast<uintptr_t>(x_out) |
+                                          reinterpret_cast<uintptr_t>(xn_out)) & 15) != 0 ||
+        (gate_out && (nkv <= 0 || nkv > 64 || !xg_out || !gate_w)))
+        return set_error(AR_EINVAL, "gemm_rc_norm: unsupported shape / alignment");
+    RcArgs ra{r, x_out, rms_out, xn_out, x0, sa, sb, layer, xg_out, gate_out, gate_w, (int)nkv};
+    const int64_t items = M / kRcBM;
+    const int cus = pk_cus();
+    const unsigned grid = (unsigned)(items < cus ? items : cus);
+#define AR_RC(SC)                                                                                                    \
+    do {                                                                                                             \
+        static bool attr_set = false;                                                                                \
+        if (!attr_set) {                                                                                             \
+            if (hipFuncSetAttribute((const void*)gemm_rc<SC>, hipFuncAttributeMaxDynamicSharedMemorySize, kRcLds) != \
+                hipSuccess)                                                                                          \
+                return set_error(AR_EHIP, "gemm_rc_norm: cannot set the LDS size");                                  \
+            attr_set = true;                                                                                         \
+        }                                                                                                            \
+        gemm_rc<SC><<<grid, kPkThreads, kRcLds, st>>>(A, W, M, K, K, K, ra);                                         \
+    } while (0)
+    if (x0) AR_RC(true);
+    else AR_RC(false);
+#undef AR_RC
+    return check_launch("gemm_rc_norm");
 }
 
 bool gemm_head_fusable(int64_t M, int64_t C, int64_t hd) {

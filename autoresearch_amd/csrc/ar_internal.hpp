@@ -36,6 +36,16 @@ enum { GEMM_EPI_ADD = 3, GEMM_EPI_RELU2 = 4, GEMM_EPI_SOFTCAP = 5, GEMM_EPI_RELU
 int32_t gemm_epilogue(hipStream_t st, int layout, int epi, void* C, int c_bf16, const void* X, int x_bf16,
                       const void* W, int w_bf16, int64_t M, int64_t N, int64_t K, const void* aux, void* aux_out,
                       float cap);
+// Row-complete NT product for C = 512 output columns with the row pass of
+// resid_norm in its epilogue: x = r + A W^T (x0 null), or
+// x = sa[layer] (r + A W^T) + sb[layer] x0; writes x (fp32, may alias r),
+// rms = sqrt(mean(x^2) + 1e-5), xn = bf16(x / rms), and with gate_out set the
+// value-embedding gate (xg = (x / rms)[:, :32], gate = 2 sigmoid(gate_w xg)).
+// A: bf16 [M, K], W: bf16 [512, K].
+bool gemm_rc_fusable(int64_t M, int64_t C, int64_t K);
+int32_t gemm_rc_norm(hipStream_t st, const bf16* A, const bf16* W, int64_t M, int64_t K, const float* r, float* x_out,
+                     float* rms_out, bf16* xn_out, const float* x0, const float* sa, const float* sb, int64_t layer,
+                     float* xg_out, float* gate_out, const float* gate_w, int64_t nkv);
 // Whether gemm_qkv_fused / gemm_dout_d_fused take this shape.
 bool gemm_head_fusable(int64_t M, int64_t C, int64_t hd);
 // The bf16 step's q|k|v forward product xn [M, C] . Wqkv [3C, C]^T with

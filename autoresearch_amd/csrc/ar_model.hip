@@ -93,6 +93,9 @@ struct ar_gpt {
     // qkv_post fused into the q|k|v product and D = rowsum(dO O) into the
     // c_proj dX product (head-aligned persistent GEMM), when the shape allows
     bool fuse_heads = false;
+    // the forward's residual products (c_proj, mlp_proj) as row-complete
+    // GEMMs that also run the following resid_norm pass (C = 512)
+    bool fuse_rows = false;
     float grad_logits_scale = 0.f;  // loss_scale baked into grad_logits_b
     bool grad_logits_valid = false;
     // step-dependent optimizer scalars in device memory (StepScalars)
@@ -408,6 +411,10 @@ static int32_t gpt_build(ar_gpt* m) {
         // AR_FUSE_HEADS=0 keeps the separate qkv_post / D kernels (A/B runs, tests)
         const char* fh = getenv("AR_FUSE_HEADS");
         m->fuse_heads = !(fh && strcmp(fh, "0") == 0) && gemm_head_fusable(BT, C, hd);
+        // AR_FUSE_ROWS=0 keeps the residual-add GEMMs and separate resid_norm passes
+        const char* fr = getenv("AR_FUSE_ROWS");
+        m->fuse_rows = !(fr && strcmp(fr, "0") == 0) && gemm_rc_fusable(BT, C, C) && gemm_rc_fusable(BT, C, F) &&
+                       kGateChannels == 32;
         const int64_t ds_elems = flash_ds_elems(m->B, m->T, H);
         if (ds_elems * (int64_t)sizeof(bf16) <= ds_max) {
             void* p = nullptr;
@@ -597,9 +604,11 @@ static int32_t forward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* tar
         LayerBufsB& b = m->LB[i];
         const bool ve = has_ve(c, i);
         // layer 0: x0 = norm(wte[idx]) (model.mojo:605-618); x = res*x_in + x0l*x0; xn = norm(x)
-        AR_TRY(resid_norm(st, i == 0 ? 0 : 1, m->x0, b.x, b.rms_attn, b.xn, ve ? b.xg : nullptr,
-                          ve ? b.gate : nullptr, m->x, m->x0, P(m, m->i_wte), inputs, P(m, m->i_res), P(m, m->i_x0),
-                          i, ve ? P(m, m->i_gate[i]) : nullptr, H, kGateChannels, BT, C));
+        // (with fuse_rows the previous layer's mlp_proj product produced layer i's input)
+        if (i == 0 || !m->fuse_rows)
+            AR_TRY(resid_norm(st, i == 0 ? 0 : 1, m->x0, b.x, b.rms_attn, b.xn, ve ? b.xg : nullptr,
+                              ve ? b.gate : nullptr, m->x, m->x0, P(m, m->i_wte), inputs, P(m, m->i_res),
+                              P(m, m->i_x0), i, ve ? P(m, m->i_gate[i]) : nullptr, H, kGateChannels, BT, C));
         // c_q | c_k | c_v: one [3C, C] weight; rope + head norm of q / k and the
         // value-embedding add of v in its epilogue, or in qkv_post after it
         if (m->fuse_heads) {
@@ -618,19 +627,47 @@ static int32_t forward_bf16(ar_gpt* m, const int64_t* inputs, const int64_t* tar
         fo.b1 = b.attn_out_b;
         AR_TRY(attention_b(m, AttnOp::FWD, b.attn_out, b.lse, fo, b.q, b.k, b.v, nullptr, nullptr, nullptr,
                            window_size(c, i)));
-        // x = x_layer + attn_out @ c_proj^T
-        AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_ADD, m->x, false, b.attn_out_b, true, Wb(m, m->i_proj[i]), BT, C, C, b.x,
-                      nullptr, 0.f));
-        AR_TRY(resid_norm(st, 2, nullptr, nullptr, b.rms_mlp, b.xn_mlp, nullptr, nullptr, m->x, nullptr, nullptr,
-                          nullptr, nullptr, nullptr, 0, nullptr, 0, 0, BT, C));
+        // x = x_layer + attn_out @ c_proj^T; rms_mlp, xn_mlp = norm(x)
+        if (m->fuse_rows) {
+            const int e = prof_begin(m);
+            const int32_t r = gemm_rc_norm(st, b.attn_out_b, Wb(m, m->i_proj[i]), BT, C, b.x, m->x, b.rms_mlp,
+                                           b.xn_mlp, nullptr, nullptr, nullptr, 0, nullptr, nullptr, nullptr, 0);
+            prof_end(m, e, 0, 2.0 * BT * C * C);
+            AR_TRY(r);
+        } else {
+            AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_ADD, m->x, false, b.attn_out_b, true, Wb(m, m->i_proj[i]), BT, C, C, b.x,
+                          nullptr, 0.f));
+            AR_TRY(resid_norm(st, 2, nullptr, nullptr, b.rms_mlp, b.xn_mlp, nullptr, nullptr, m->x, nullptr, nullptr,
+                              nullptr, nullptr, nullptr, 0, nullptr, 0, 0, BT, C));
+        }
         // act = relu(xn @ c_fc^T)^2 (the pre-activation is not kept); x += act @ mlp_proj^T
         AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_RELU2, b.act, true, b.xn_mlp, true, Wb(m, m->i_fc[i]), BT, F, C, nullptr,
                       nullptr, 0.f));
-        AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_ADD, m->x, false, b.act, true, Wb(m, m->i_mlpp[i]), BT, C, F, m->x,
-                      nullptr, 0.f));
+        if (m->fuse_rows) {
+            // the next layer's input x = res[i+1] (x + act @ mlp_proj^T) + x0l[i+1] x0 and its
+            // norm (and VE gate); after the last layer the final norm of x
+            const int e = prof_begin(m);
+            int32_t r;
+            if (i + 1 < c.n_layer) {
+                LayerBufsB& nb = m->LB[i + 1];
+                const bool nve = has_ve(c, i + 1);
+                r = gemm_rc_norm(st, b.act, Wb(m, m->i_mlpp[i]), BT, F, m->x, nb.x, nb.rms_attn, nb.xn, m->x0,
+                                 P(m, m->i_res), P(m, m->i_x0), i + 1, nve ? nb.xg : nullptr,
+                                 nve ? nb.gate : nullptr, nve ? P(m, m->i_gate[i + 1]) : nullptr, H);
+            } else {
+                r = gemm_rc_norm(st, b.act, Wb(m, m->i_mlpp[i]), BT, F, m->x, m->x, m->rms_final, m->x_final_b,
+                                 nullptr, nullptr, nullptr, 0, nullptr, nullptr, nullptr, 0);
+            }
+            prof_end(m, e, 0, 2.0 * BT * C * F);
+            AR_TRY(r);
+        } else {
+            AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_ADD, m->x, false, b.act, true, Wb(m, m->i_mlpp[i]), BT, C, F, m->x,
+                          nullptr, 0.f));
+        }
     }
-    AR_TRY(resid_norm(st, 2, nullptr, nullptr, m->rms_final, m->x_final_b, nullptr, nullptr, m->x, nullptr, nullptr,
-                      nullptr, nullptr, nullptr, 0, nullptr, 0, 0, BT, C));
+    if (!m->fuse_rows)
+        AR_TRY(resid_norm(st, 2, nullptr, nullptr, m->rms_final, m->x_final_b, nullptr, nullptr, m->x, nullptr,
+                          nullptr, nullptr, nullptr, nullptr, 0, nullptr, 0, 0, BT, C));
     // softcapped logits stored as bf16 (in the fp32 logits buffer), as a bf16 lm_head's output is
     AR_TRY(gemm_e(m, 0, 0, GEMM_EPI_SOFTCAP, LogitsB(m), true, m->x_final_b, true, Wb(m, m->i_lm), BT, V, C, nullptr,
                   nullptr, kSoftcap));

@@ -414,23 +414,33 @@ def test_full_size_step_properties(cfg, B, precision):
     assert runs[0][2] == runs[1][2]
 
 
-def test_fused_head_epilogues_match_separate_kernels(monkeypatch):
-    """The bf16 step with qkv_post fused into the q|k|v product's epilogue and
-    D = rowsum(dO O) into the c_proj dX product's (head-aligned persistent
-    GEMM) against the same step with the separate qkv_post / D kernels
-    (AR_FUSE_HEADS=0), at a shape the fused path takes (B*T and C multiples
-    of 256, head_dim 128, value-embedding layers).  The fused rope / norm act
-    on the fp32 products and qkv_post on their bf16 rounding, so the two differ
-    by bf16 rounding; each is compared with the oracle, and the fused path
-    must be as close to it as the separate kernels are (every gradient and the
-    post-step weights, two steps)."""
+# C = 512 (the row-complete residual products take it), four layers with two
+# value-embedding layers, head_dim 128
+WIDE512 = dict(sequence_len=256, vocab_size=1024, n_layer=4, n_head=4, n_kv_head=4, n_embd=512, head_dim=128,
+               kv_dim=512)
+
+
+@pytest.mark.parametrize("var,cfg", [("AR_FUSE_HEADS", WIDE), ("AR_FUSE_ROWS", WIDE512)], ids=["heads", "rows"])
+def test_fused_epilogues_match_separate_kernels(var, cfg, monkeypatch):
+    """The bf16 step's fused GEMM epilogues against the same step with the
+    separate kernels (var=0), at a shape the fused path takes:
+      heads: qkv_post in the q|k|v product's epilogue and D = rowsum(dO O) in
+        the c_proj dX product's (head-aligned persistent GEMM);
+      rows: the residual add, the next layer's residual scaling, RMSNorm and
+        value-embedding gate in the c_proj / mlp_proj products' epilogues
+        (row-complete GEMM, C = 512) instead of resid_norm.
+    The fused paths round at other points (e.g. rope / norm on the fp32
+    products, not on their bf16 copy), so the two differ by bf16 rounding;
+    each is compared with the oracle, and the fused path must be as close to
+    it as the separate kernels are (every gradient and the post-step
+    weights, two steps)."""
     errs = []
     for fuse in ("0", None):
         if fuse is None:
-            monkeypatch.delenv("AR_FUSE_HEADS", raising=False)
+            monkeypatch.delenv(var, raising=False)
         else:
-            monkeypatch.setenv("AR_FUSE_HEADS", fuse)
-        _, _, res = _run(WIDE, 2, 256, 1, 256, 8, steps=2)
+            monkeypatch.setenv(var, fuse)
+        _, _, res = _run(cfg, 2, 256, 1, 256, 8, steps=2)
         e = {}
         for st, r in enumerate(res):
             go, gg = r["grads"]
