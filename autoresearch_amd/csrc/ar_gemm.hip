@@ -847,8 +847,12 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
                         const int r = p * 8 + rr;
                         u32x4 q = *reinterpret_cast<const u32x4*>(bstrip + r * 128 + ((c16 ^ (r & 7)) << 4));
                         if (p & 1) q = __builtin_shufflevector(q, q, 2, 3, 0, 1);  // r / 8 odd
-                        __builtin_nontemporal_store(
-                            q, reinterpret_cast<u32x4*>(lbase + (int64_t)(i * 32 + p * 8) * ldo + jp * 64));
+                        u32x4* const qd = reinterpret_cast<u32x4*>(lbase + (int64_t)(i * 32 + p * 8) * ldo + jp * 64);
+                        // q, k, v are plain stores: the attention kernels read each k / v
+                        // row many times, so keeping them in the caches pays; other
+                        // outputs stream past L2 (nontemporal)
+                        if constexpr (EPI == EPI_QKV) *qd = q;
+                        else __builtin_nontemporal_store(q, qd);
                     }
                     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                     __builtin_amdgcn_wave_barrier();
