@@ -684,12 +684,18 @@ __global__ __launch_bounds__(kPkThreads) void gemm_pk(TC* C, const bf16* A, cons
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             if (ks < 3) frags(ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+            // keep the next k-step's fragment reads ahead of this k-step's
+            // MFMAs: left alone, the scheduler sinks each read to just before
+            // its first use and waits for it there (lgkmcnt(0) inside every
+            // k-step), to save the second fragment set's registers
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < WTM; ++i)
 #pragma unroll
                 for (int j = 0; j < WTN; ++j)
                     acc[i][j] = SW ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks & 1][j], fa[ks & 1][i], acc[i][j], 0, 0, 0)
                                    : __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks & 1][i], fb[ks & 1][j], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (++ckt != nk) continue;
         ckt = 0;
@@ -1058,12 +1064,14 @@ __global__ __launch_bounds__(kPkThreads) void gemm_rc(const bf16* A, const bf16*
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             if (ks < 3) frags(ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);  // next k-step's reads ahead of these MFMAs (as in gemm_pk)
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks & 1][j], fa[ks & 1][i], acc[i][j], 0, 0,
                                                                          0);
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (++ckt != nk) continue;
         ckt = 0;
