@@ -235,6 +235,11 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
     // Each iteration's combinations ride on the product before them:
     // Bm = cb A + cc (A A) in the A.A epilogue, and X' = ca X + (B X or X B)
     // in the last product's epilogue, written to the other of X / Y.
+    // A = X^T X (or X X^T) is symmetric bit for bit: entries (i, j) and
+    // (j, i) sum the same products in the same k order.  So is A A, and with
+    // it Bm.  A symmetric operand read as the B side of a product is read
+    // K-major (its own transpose), the GEMM's faster LDS path, with the same
+    // values in the same order.
     float* Xc = X;
     float* Yc = Y;
     ::ar::bf16* Xbc = Xb;
@@ -250,12 +255,12 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
         if (r) return r;
         // only the bf16 copy of Bm is read (as the next product's operand),
         // and the last iteration's X is read in fp32 only (the update)
-        if ((r = gemm_batched_bf16(st, true, false, nullptr, Bmb, Ab, Ab, sm, sm, sm, sm, sm, sm, n, ss, ss, ss, A,
+        if ((r = gemm_batched_bf16(st, true, true, nullptr, Bmb, Ab, Ab, sm, sm, sm, sm, sm, sm, n, ss, ss, ss, A,
                                    cc, cb)))
             return r;
         ::ar::bf16* const Yout = it < 4 ? Ybc : nullptr;
         if (tall)
-            r = gemm_batched_bf16(st, true, false, Yc, Yout, Xbc, Bmb, rows, cols, cols, cols, cols, cols, n, size, ss,
+            r = gemm_batched_bf16(st, true, true, Yc, Yout, Xbc, Bmb, rows, cols, cols, cols, cols, cols, n, size, ss,
                                   size, Xc, 1.0f, ca);
         else
             r = gemm_batched_bf16(st, true, false, Yc, Yout, Bmb, Xbc, rows, cols, rows, rows, cols, cols, n, ss, size,
@@ -278,10 +283,10 @@ int32_t muon_group_step(hipStream_t st, float* const* params, const float* const
                                  ss);
         if (r) return r;
         // Bm = cb A + cc (A @ A)
-        if ((r = gemm_batched_f32(st, bf16, true, false, Bm, A, A, sm, sm, sm, sm, sm, sm, n, ss, ss, ss, A, cc, cb)))
+        if ((r = gemm_batched_f32(st, bf16, true, true, Bm, A, A, sm, sm, sm, sm, sm, sm, n, ss, ss, ss, A, cc, cb)))
             return r;
-        if (tall)  // X' = ca X + X @ B
-            r = gemm_batched_f32(st, bf16, true, false, Yc, Xc, Bm, rows, cols, cols, cols, cols, cols, n, size, ss,
+        if (tall)  // X' = ca X + X @ B (B symmetric: read K-major)
+            r = gemm_batched_f32(st, bf16, true, true, Yc, Xc, Bm, rows, cols, cols, cols, cols, cols, n, size, ss,
                                  size, Xc, 1.0f, ca);
         else  // X' = ca X + B @ X
             r = gemm_batched_f32(st, bf16, true, false, Yc, Bm, Xc, rows, cols, rows, rows, cols, cols, n, ss, size,
