@@ -85,7 +85,8 @@ template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf
 // wait for.  m0 is clobbered: the kernels that use these keep nothing of
 // their own in m0 (their ISA has no other m0 reference), so clang's warning
 // that a reserved register in a clobber list may not be preserved is
-// silenced here.
+// silenced here.  tests/test_isa_m0.py compiles the kernels that use these
+// helpers and fails if any other instruction reads or writes m0.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ unsigned lds_addr(const void* p) {
