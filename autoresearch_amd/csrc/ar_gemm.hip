@@ -1910,7 +1910,9 @@ static char* noalloc_scratch(int32_t* status) {
 
 extern "C" int32_t ar_linear_bwd_dw_bf16_noalloc(ar_stream_t stream, float* grad_weight, const float* grad_output,
                                                  const float* input, int64_t M, int64_t N, int64_t K) {
-    int32_t st = AR_OK;
+    // the arguments first: a bad call is AR_EINVAL before any device query
+    int32_t st = check_gemm_args(grad_weight, grad_output, input, M, N, K, "linear_bwd_dw_bf16_noalloc");
+    if (st) return st;
     char* p = noalloc_scratch(&st);
     if (!p) return st;
     return linear_call(stream, 2, true, grad_weight, grad_output, input, M, N, K, "linear_bwd_dw_bf16_noalloc",

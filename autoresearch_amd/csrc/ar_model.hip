@@ -546,21 +546,23 @@ extern "C" int32_t ar_gpt_destroy(ar_gpt* m) {
     return AR_OK;
 }
 
-extern "C" int64_t ar_gpt_num_tensors(const ar_gpt* m) { return (int64_t)m->t.size(); }
+// The accessors answer 0 / -1 / null for a null model.
+extern "C" int64_t ar_gpt_num_tensors(const ar_gpt* m) { return m ? (int64_t)m->t.size() : 0; }
 extern "C" int64_t ar_gpt_tensor_info(const ar_gpt* m, int64_t i, int64_t* offset, const char** name) {
-    if (i < 0 || i >= (int64_t)m->t.size()) return -1;
+    if (!m || i < 0 || i >= (int64_t)m->t.size()) return -1;
     if (offset) *offset = m->t[i].offset;
     if (name) *name = m->t[i].name.c_str();
     return m->t[i].size;
 }
-extern "C" int64_t ar_gpt_num_params(const ar_gpt* m) { return m->nparams; }
-extern "C" float* ar_gpt_params(ar_gpt* m) { return m->params; }
-extern "C" float* ar_gpt_grads(ar_gpt* m) { return m->grads; }
-extern "C" float* ar_gpt_token_loss(ar_gpt* m) { return m->loss; }
-extern "C" float* ar_gpt_mean_loss(ar_gpt* m) { return m->mean_loss; }
+extern "C" int64_t ar_gpt_num_params(const ar_gpt* m) { return m ? m->nparams : 0; }
+extern "C" float* ar_gpt_params(ar_gpt* m) { return m ? m->params : nullptr; }
+extern "C" float* ar_gpt_grads(ar_gpt* m) { return m ? m->grads : nullptr; }
+extern "C" float* ar_gpt_token_loss(ar_gpt* m) { return m ? m->loss : nullptr; }
+extern "C" float* ar_gpt_mean_loss(ar_gpt* m) { return m ? m->mean_loss : nullptr; }
 
 // model.mojo:337-427
 extern "C" int32_t ar_gpt_init_weights(ar_gpt* m, uint64_t seed0) {
+    AR_CHECK_ARG(m != nullptr, "gpt_init_weights: null model");
     const ar_gpt_config& c = m->c;
     const int64_t C = c.n_embd, V = c.vocab_size, Lr = c.n_layer, kv = c.kv_dim, F = kMlpExpansion * C;
     const float s = (float)(sqrt(3.0) * pow((double)C, -0.5));
@@ -588,7 +590,10 @@ extern "C" int32_t ar_gpt_init_weights(ar_gpt* m, uint64_t seed0) {
 }
 
 // model.mojo:777-814
-extern "C" int32_t ar_gpt_zero_grads(ar_gpt* m) { return ar_zero_buffer(AS(m), m->grads, m->nparams); }
+extern "C" int32_t ar_gpt_zero_grads(ar_gpt* m) {
+    AR_CHECK_ARG(m != nullptr, "gpt_zero_grads: null model");
+    return ar_zero_buffer(AS(m), m->grads, m->nparams);
+}
 
 // ------------------------------------------------------------------------
 // bf16 step: model.mojo:576-772 / 819-1037 with bf16 operand storage
@@ -1065,6 +1070,7 @@ extern "C" int32_t ar_gpt_optimizer_step(ar_gpt* m, double progress) {
 // train.mojo:231-282
 extern "C" int32_t ar_gpt_train_step(ar_gpt* m, const int64_t* inputs, const int64_t* targets, double progress,
                                      float* loss_host) {
+    AR_CHECK_ARG(m && inputs && targets, "gpt_train_step: null pointer");
     AR_TRY(ar_gpt_zero_grads(m));
     AR_TRY(ar_gpt_forward(m, inputs, targets, nullptr));
     AR_TRY(ar_gpt_backward(m, inputs, targets, 1.0f));

@@ -312,7 +312,10 @@ int32_t ar_gpt_destroy(ar_gpt* model);
 int32_t ar_gpt_init_weights(ar_gpt* model, uint64_t seed0);
 /* Flat parameter / gradient arenas, tensor order = train.mojo's optimizer
  * registration order: wte, lm_head, resid_lambdas, x0_lambdas, then per layer
- * c_q, c_k, c_v, c_proj, c_fc, mlp_proj[, value_embeds, ve_gate]. */
+ * c_q, c_k, c_v, c_proj, c_fc, mlp_proj[, value_embeds, ve_gate].  With a
+ * null model the counts are 0, tensor_info is -1 and the pointers are NULL;
+ * the ar_gpt_* entries returning a status answer AR_EINVAL for it
+ * (ar_gpt_destroy: AR_OK, nothing to do). */
 int64_t ar_gpt_num_tensors(const ar_gpt* model);
 int64_t ar_gpt_tensor_info(const ar_gpt* model, int64_t i, int64_t* offset, const char** name);
 int64_t ar_gpt_num_params(const ar_gpt* model);

@@ -70,6 +70,54 @@ def test_error_path_without_gpu():
     assert lib.ar_workspace_destroy(None) == 0
 
 
+_NULL_PROBE = r"""
+import ctypes as ct, json, sys
+sys.path.insert(0, sys.argv[1])
+from autoresearch_amd import _lib
+lib = _lib.load()
+out = {}
+for h in _lib.HEADERS:
+    for name, (res, args) in _lib.parse_header(h).items():
+        vals = [None if a in (ct.c_void_p, ct.c_char_p) else 1.0 if a in (ct.c_float, ct.c_double)
+                else 0 if a is ct.c_int32 else 8 for a in args]
+        if name == "ar_last_error":
+            continue
+        r = getattr(lib, name)(*vals)
+        out[name] = r
+        print(name, r, flush=True)  # names the entry if the next call crashes
+print("RESULT " + json.dumps(out))
+"""
+
+
+def test_every_entry_point_rejects_null_arguments():
+    """Every function of the headers, called with null pointers (and small
+    sizes): the status-returning entry points answer AR_EINVAL (-1) before
+    any device work, the accessors 0 / -1 / NULL, and nothing dereferences a
+    null handle.  Exceptions, each the documented behaviour: ar_version,
+    unbinding (a null workspace) in ar_workspace_bind, which asks HIP for the
+    current device (AR_EHIP without a GPU), and the destroy functions (no-op)."""
+    import json
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _NULL_PROBE, root], capture_output=True, text=True, timeout=300)
+    last = r.stdout.strip().splitlines()[-1:] or [""]
+    assert r.returncode == 0, f"crashed after: {last[0]!r}\n{r.stderr[-2000:]}"
+    res = json.loads(last[0][len("RESULT "):])
+    special = {"ar_version", "ar_workspace_bind", "ar_workspace_destroy", "ar_gpt_destroy", "ar_loader_destroy",
+               "ar_workspace_bytes", "ar_gpt_num_tensors", "ar_gpt_tensor_info", "ar_gpt_num_params",
+               "ar_gpt_params", "ar_gpt_grads", "ar_gpt_token_loss", "ar_gpt_mean_loss"}
+    bad = {n: v for n, v in res.items() if n not in special and v != -1}
+    assert not bad, bad
+    assert res["ar_version"] >= 1
+    assert res["ar_workspace_bind"] in (0, -3)
+    assert res["ar_workspace_destroy"] == res["ar_gpt_destroy"] == res["ar_loader_destroy"] == 0
+    assert res["ar_workspace_bytes"] == res["ar_gpt_num_tensors"] == res["ar_gpt_num_params"] == 0
+    assert res["ar_gpt_tensor_info"] == -1
+    assert all(res[n] is None for n in ("ar_gpt_params", "ar_gpt_grads", "ar_gpt_token_loss", "ar_gpt_mean_loss"))
+    assert len(res) > 70
+
+
 def test_gpt_config_default():
     from autoresearch_amd.model import GPTConfig
     c = GPTConfig.default(8192, 8)  # config.mojo:27-43
