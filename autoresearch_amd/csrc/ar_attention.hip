@@ -740,9 +740,12 @@ __global__ void unpad_rows_k(float* dst, const float* src, int64_t rows, int hd,
 int32_t attn_padded(ar_stream_t stream, bool bf, ar::AttnOp op, float* o1, float* o2, const float* const* in,
                     const float* lse, const float* dbuf, int64_t B, int64_t T, int64_t H, int64_t hd,
                     int64_t window) {
-    if (hd <= 0 || hd > 128)
+    if (hd <= 0 || B < 0 || T < 0 || H < 0)
+        return ar::set_error(AR_EINVAL, "flash attention: bad shape (B %lld, T %lld, H %lld, head_dim %lld)",
+                             (long long)B, (long long)T, (long long)H, (long long)hd);
+    if (hd > 128)
         return ar::set_error(AR_EUNSUPPORTED, "flash attention: head_dim %lld not in [1, 128]", (long long)hd);
-    if (B <= 0 || T <= 0 || H <= 0) return B == 0 || T == 0 ? AR_OK : ar::set_error(AR_EINVAL, "flash attention: bad shape");
+    if (B == 0 || T == 0 || H == 0) return AR_OK;
     const int64_t hdp = padded_hd(hd), rows = B * T * H, n = rows * hdp;
     const int nin = op == ar::AttnOp::FWD ? 3 : 4;
     const int nout = op == ar::AttnOp::DKV ? 2 : 1;
@@ -814,6 +817,7 @@ extern "C" int32_t ar_flash_attn_fwd_bf16(ar_stream_t stream, float* output, flo
     AR_ATTN_PTRS(output, q, k, v);
     AR_CHECK_ARG(lse_out != nullptr, "flash_attn_fwd_bf16: null lse");
     AR_CHECK_ARG(B >= 0 && T >= 0 && num_heads >= 0, "flash_attn_fwd_bf16: bad shape");
+    if (native_hd(head_dim) && (B == 0 || T == 0 || num_heads == 0)) return AR_OK;  // nothing to do
     const float* src[3] = {q, k, v};
     if (!native_hd(head_dim))
         return attn_padded(stream, true, ar::AttnOp::FWD, output, lse_out, src, nullptr, nullptr, B, T, num_heads,
@@ -845,6 +849,7 @@ extern "C" int32_t ar_flash_attn_bwd_dq_bf16(ar_stream_t stream, float* grad_q, 
     AR_ATTN_PTRS(grad_q, q, k, v, grad_output);
     AR_CHECK_ARG(lse && d_buf, "flash_attn_bwd_dq_bf16: null lse / d_buf");
     AR_CHECK_ARG(B >= 0 && T >= 0 && num_heads >= 0, "flash_attn_bwd_dq_bf16: bad shape");
+    if (native_hd(head_dim) && (B == 0 || T == 0 || num_heads == 0)) return AR_OK;  // nothing to do
     const float* src[4] = {q, k, v, grad_output};
     if (!native_hd(head_dim))
         return attn_padded(stream, true, ar::AttnOp::DQ, grad_q, nullptr, src, lse, d_buf, B, T, num_heads, head_dim,
@@ -876,6 +881,7 @@ extern "C" int32_t ar_flash_attn_bwd_dkv_bf16(ar_stream_t stream, float* grad_k,
     AR_ATTN_PTRS(grad_k, grad_v, q, k, v, grad_output);
     AR_CHECK_ARG(lse && d_buf, "flash_attn_bwd_dkv_bf16: null lse / d_buf");
     AR_CHECK_ARG(B >= 0 && T >= 0 && num_heads >= 0, "flash_attn_bwd_dkv_bf16: bad shape");
+    if (native_hd(head_dim) && (B == 0 || T == 0 || num_heads == 0)) return AR_OK;  // nothing to do
     const float* src[4] = {q, k, v, grad_output};
     if (!native_hd(head_dim))
         return attn_padded(stream, true, ar::AttnOp::DKV, grad_k, grad_v, src, lse, d_buf, B, T, num_heads, head_dim,

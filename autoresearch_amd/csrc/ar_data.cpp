@@ -232,6 +232,7 @@ extern "C" int32_t ar_bpb_accumulate(const float* token_loss, const int64_t* tar
                                      int64_t n, int64_t vocab_size, double* nats, double* bytes) {
     if (!token_loss || !targets || !token_bytes || !nats || !bytes)
         return ar::set_error(AR_EINVAL, "bpb_accumulate: null pointer");
+    if (n < 0 || vocab_size < 0) return ar::set_error(AR_EINVAL, "bpb_accumulate: negative count");
     for (int64_t i = 0; i < n; ++i) {
         const int64_t t = targets[i];
         if (t >= 0 && t < vocab_size) {

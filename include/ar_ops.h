@@ -102,7 +102,8 @@ int32_t ar_rope_fwd(ar_stream_t stream, float* output, const float* input, const
  * q,k,v,output: [B*T*num_heads, head_dim]; lse_out: [B*T*num_heads].
  * Key kp visible from qp iff kp <= qp and (window_size <= 0 or kp >= qp - window_size).
  * Any head_dim in [1, 128] (AR_EUNSUPPORTED above, where ops.mojo:267 returns
- * silently).  head_dim 32, 64 and 128 run the tiled kernels directly; any
+ * silently; AR_EINVAL for head_dim <= 0 or a negative B, T or num_heads; an
+ * empty shape is AR_OK).  head_dim 32, 64 and 128 run the tiled kernels directly; any
  * other runs them at the next of those sizes on zero-padded copies of the rows
  * in the workspace (softmax scale 1/sqrt(head_dim)).  The same holds for the
  * dq and dkv entries below. */

@@ -118,6 +118,58 @@ def test_every_entry_point_rejects_null_arguments():
     assert len(res) > 70
 
 
+_NEG_PROBE = r"""
+import ctypes as ct, json, sys
+sys.path.insert(0, sys.argv[1])
+from autoresearch_amd import _lib
+lib = _lib.load()
+# opaque handles (model, loader, workspace) cannot be faked with a buffer
+HANDLE = ("ar_gpt_", "ar_loader_", "ar_workspace_")
+out = {}
+bufs = []
+for h in _lib.HEADERS:
+    for name, (res, args) in _lib.parse_header(h).items():
+        if res is not ct.c_int32 or name.startswith(HANDLE) and name != "ar_gpt_create":
+            continue
+        if not any(a is ct.c_int64 for a in args):
+            continue
+        vals = []
+        for a in args:
+            if a is ct.c_void_p:
+                b = (ct.c_char * (1 << 16))()
+                bufs.append(b)
+                vals.append(ct.addressof(b))
+            elif a is ct.c_char_p:
+                vals.append(b"/nonexistent")
+            elif a in (ct.c_float, ct.c_double):
+                vals.append(1.0)
+            elif a is ct.c_int32:
+                vals.append(0)
+            else:
+                vals.append(-1)
+        print(name, flush=True)
+        out[name] = getattr(lib, name)(*vals)
+print("RESULT " + json.dumps(out))
+"""
+
+
+def test_negative_sizes_are_rejected():
+    """Every status-returning entry point that takes int64 sizes, called with
+    host buffers for its pointers and -1 for every size: AR_EINVAL before
+    any device work (a negative extent must never reach a launch)."""
+    import json
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _NEG_PROBE, root], capture_output=True, text=True, timeout=300)
+    last = r.stdout.strip().splitlines()[-1:] or [""]
+    assert r.returncode == 0, f"crashed in: {last[0]!r}\n{r.stderr[-2000:]}"
+    res = json.loads(last[0][len("RESULT "):])
+    bad = {n: v for n, v in res.items() if v != -1}
+    assert not bad, bad
+    assert len(res) > 50
+
+
 def test_gpt_config_default():
     from autoresearch_amd.model import GPTConfig
     c = GPTConfig.default(8192, 8)  # config.mojo:27-43
