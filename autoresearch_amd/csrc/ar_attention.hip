@@ -404,8 +404,11 @@ __global__ __launch_bounds__(kThreads, 2) void fa_fwd_k(float* out, float* lse, 
 }
 
 // ============================ backward: dQ ============================
+// The next K / V tile is prefetched into registers as in the forward; at hd 128
+// that takes ~380 registers, one wave per SIMD (fp32 step: dQ 21.55 -> 21.33 ms
+// against the 256-register form that loaded each tile when it started).
 template <bool BF16, int HD, typename TIN>
-__global__ __launch_bounds__(kThreads, 2) void fa_bwd_dq_k(float* dq, const TIN* q, const TIN* k, const TIN* v,
+__global__ __launch_bounds__(kThreads, HD <= 64 ? 2 : 1) void fa_bwd_dq_k(float* dq, const TIN* q, const TIN* k, const TIN* v,
                                                         const TIN* dout, const float* lse, const float* dbuf, int B,
                                                         int T, int H, int window, float scale_log2, float scale) {
     using A = AT<BF16>;
@@ -438,15 +441,26 @@ __global__ __launch_bounds__(kThreads, 2) void fa_bwd_dq_k(float* dq, const TIN*
     if (window > 0) kstart = q0 - window > 0 ? q0 - window : 0;
     kstart = (kstart / kTile) * kTile;
     const int kend = (q0 + kOwn < T) ? q0 + kOwn : T;
+    // the next tile's K / V rows are loaded into registers while this tile's
+    // MFMAs run, and written to LDS after the barrier that ends them
+    TileVals<BF16, HD, TIN> nk, nv;
+    if (kstart < kend) {
+        nk.load(k + boff, rs, kstart, T);
+        nv.load(v + boff, rs, kstart, T);
+    }
     for (int kv0 = kstart; kv0 < kend; kv0 += kTile) {
-        load_tile<BF16, HD>(sK, sKT, k + boff, rs, kv0, T, true);
-        load_tile<BF16, HD>(sV, nullptr, v + boff, rs, kv0, T, false);
+        nk.write(sK, kv0, T);
+        nv.write(sV, kv0, T);
         __syncthreads();
+        if (kv0 + kTile < kend) {
+            nk.load(k + boff, rs, kv0 + kTile, T);
+            nv.load(v + boff, rs, kv0 + kTile, T);
+        }
         const bool skip = kv0 > qw + 31 || (window > 0 && kv0 + kTile - 1 < qw - window) || qw >= T;
         if (!skip) {
             // one 32-key half at a time (not unrolled): only one S / dP pair is
-            // live, which keeps the hd-128 kernel within 256 registers beside
-            // the own-row Q and dO fragments and the dQ accumulators
+            // live beside the own-row Q and dO fragments, the dQ accumulators
+            // and the prefetched tile
 #pragma unroll 1
             for (int kb = 0; kb < 2; ++kb) {
                 f32x16 s, dp;
@@ -484,10 +498,15 @@ __global__ __launch_bounds__(kThreads, 2) void fa_bwd_dq_k(float* dq, const TIN*
 }
 
 // ============================ backward: dK, dV ============================
-// MODE 0 forms dK and dV in one pass.  At hd 128 the own K and V fragments and
-// both accumulator sets (4 x 64 registers) leave no room for two workgroups
-// per CU, so dV (MODE 1: S, P, dV) and dK (MODE 2: S, dP, dS, dK) run as two
-// launches that each recompute S, and each fits 256 registers.
+// MODE 0 forms dK and dV in one pass.  At hd 128 the own K and V fragments,
+// both accumulator sets (4 x 64 registers) and the next tile's Q / dO rows
+// take ~440 registers, so that launch runs one wave per SIMD (one workgroup
+// per CU).  That measured faster than splitting it into a dV launch (MODE 1:
+// S, P, dV) and a dK launch (MODE 2: S, dP, dS, dK) of 256 registers each,
+// which recompute S twice and leave the dK launch no room for the prefetch:
+// fp32 step, dK + dV 37.4 -> 28.6 ms.  The dispatcher keeps the split only
+// on its bf16-compute branch, which no entry point instantiates (the library
+// runs these kernels on fp32 operands only).
 template <bool BF16, int HD, typename TIN, int MODE>
 __global__ __launch_bounds__(kThreads, (HD <= 64 || MODE != 0) ? 2 : 1) void fa_bwd_dkv_k(float* dk, float* dv, const TIN* q, const TIN* k,
                                                          const TIN* v, const TIN* dout, const float* lse,
@@ -524,11 +543,11 @@ __global__ __launch_bounds__(kThreads, (HD <= 64 || MODE != 0) ? 2 : 1) void fa_
     const int qstart = (k0 / kTile) * kTile;
     int qend = T;
     if (window > 0 && k0 + kOwn - 1 + window + 1 < T) qend = k0 + kOwn - 1 + window + 1;
-    // Launches with registers to spare (the dV launch at hd 128, every one
-    // below) load the next Q / dO tile and its LSE / D values into registers
-    // while this tile's MFMAs run; the hd-128 dK launch has none and loads each
-    // tile when it starts.
-    constexpr bool PF = MODE == 1 || HD <= 64;
+    // Every launch but the split dK one loads the next Q / dO tile and its
+    // LSE / D values into registers while this tile's MFMAs run; the split dK
+    // launch (256 registers at hd 128) has no room and loads each tile when it
+    // starts.
+    constexpr bool PF = MODE != 2;
     TileVals<BF16, HD, TIN> nq, nd;
     float nl = 0.f, ndl = 0.f;
     auto ld_load = [&](int qt0) {  // LSE / D of query qt0 + tid (row 0 past T: masked)
@@ -667,7 +686,7 @@ static int32_t attn_dispatch_hd(hipStream_t st, AttnOp op, float* o1, float* o2,
         return check_launch("flash_attn_bwd_dq");
     }
     const size_t lds = dkv_lds<BF16, HD>();
-    if (HD == 128) {
+    if (HD == 128 && BF16) {
         fa_bwd_dkv_k<BF16, HD, TIN, 1><<<grid, kThreads, lds, st>>>(o1, o2, q, k, v, dout, lse, dbuf, B, T, H,
                                                                     window, scale_log2, scale);
         fa_bwd_dkv_k<BF16, HD, TIN, 2><<<grid, kThreads, lds, st>>>(o1, o2, q, k, v, dout, lse, dbuf, B, T, H,
