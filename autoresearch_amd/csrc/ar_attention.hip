@@ -114,60 +114,12 @@ template <> struct AT<false> {
     __device__ static Frag accfrag_lo(const f32x16& a, int s) { (void)a; (void)s; return 0.0f; }
 };
 
-// Load rows [row0, row0 + 64) of a [T, rs]-strided operand (columns [0, HD))
-// into LDS: natural [row][HD + PADN] and, for bf16, transposed [HD][LDT].
-// Rows at or beyond T are zero.
-template <bool BF16, int HD, typename TIN>
-__device__ __forceinline__ void load_tile(typename AT<BF16>::LT* nat, typename AT<BF16>::LT* tr, const TIN* base,
-                                          int64_t rs, int row0, int T, bool want_tr) {
-    using A = AT<BF16>;
-    using LT = typename A::LT;
-    constexpr int CW = A::CW, LDN = HD + A::PADN;
-    constexpr int ITEMS = (kTile / 4) * (HD / CW);  // 4 rows x CW columns per item
-    for (int it = threadIdx.x; it < ITEMS; it += kThreads) {
-        const int r4 = it % (kTile / 4), dc = (it / (kTile / 4)) * CW;
-        LT vals[4][CW];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = r4 * 4 + i;
-            if (row0 + r < T) {
-                const TIN* src = base + (int64_t)(row0 + r) * rs + dc;
-                if constexpr (sizeof(TIN) == 4) {
-                    float tmp[CW];
-#pragma unroll
-                    for (int j = 0; j < CW; j += 4) *reinterpret_cast<float4*>(tmp + j) =
-                        *reinterpret_cast<const float4*>(src + j);
-#pragma unroll
-                    for (int j = 0; j < CW; ++j) vals[i][j] = (LT)tmp[j];
-                } else {
-                    static_assert(BF16, "bf16 storage needs bf16 compute");
-                    *reinterpret_cast<uint4*>(vals[i]) = *reinterpret_cast<const uint4*>(src);
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < CW; ++j) vals[i][j] = (LT)0.0f;
-            }
-            if (nat)
-                *reinterpret_cast<uint4*>(nat + (r4 * 4 + i) * LDN + dc) = *reinterpret_cast<const uint4*>(vals[i]);
-        }
-        if constexpr (A::TRANS) {
-            if (want_tr) {
-#pragma unroll
-                for (int j = 0; j < CW; ++j) {
-                    bf16x4 col;
-                    col[0] = vals[0][j]; col[1] = vals[1][j]; col[2] = vals[2][j]; col[3] = vals[3][j];
-                    *reinterpret_cast<bf16x4*>(tr + (dc + j) * A::LDT + r4 * 4) = col;
-                }
-            }
-        }
-    }
-}
-
-// load_tile split in two, so that a tile's global loads can be issued before
-// the MFMAs of the previous tile and written to LDS after them: TileVals holds
-// this thread's items of one tile (fp32 compute: 2 x 4 rows x 4 columns).
-// Rows at or beyond T load row T - 1 and are zeroed by a select, so no load
-// sits in a branch.
+// One 64-row tile of a [T, rs]-strided operand (columns [0, HD)) on its way to
+// LDS (natural [row][HD + PADN] layout), in two halves so that its global
+// loads can be issued before the MFMAs of the previous tile and written to LDS
+// after them: TileVals holds this thread's items of the tile (4 rows x 4
+// columns each).  Rows at or beyond T load row T - 1 and are zeroed by a
+// select, so no load sits in a branch.
 template <bool BF16, int HD, typename TIN>
 struct TileVals {
     using A = AT<BF16>;
@@ -498,17 +450,14 @@ __global__ __launch_bounds__(kThreads, HD <= 64 ? 2 : 1) void fa_bwd_dq_k(float*
 }
 
 // ============================ backward: dK, dV ============================
-// MODE 0 forms dK and dV in one pass.  At hd 128 the own K and V fragments,
-// both accumulator sets (4 x 64 registers) and the next tile's Q / dO rows
-// take ~440 registers, so that launch runs one wave per SIMD (one workgroup
-// per CU).  That measured faster than splitting it into a dV launch (MODE 1:
-// S, P, dV) and a dK launch (MODE 2: S, dP, dS, dK) of 256 registers each,
-// which recompute S twice and leave the dK launch no room for the prefetch:
-// fp32 step, dK + dV 37.4 -> 28.6 ms.  The dispatcher keeps the split only
-// on its bf16-compute branch, which no entry point instantiates (the library
-// runs these kernels on fp32 operands only).
-template <bool BF16, int HD, typename TIN, int MODE>
-__global__ __launch_bounds__(kThreads, (HD <= 64 || MODE != 0) ? 2 : 1) void fa_bwd_dkv_k(float* dk, float* dv, const TIN* q, const TIN* k,
+// dK and dV in one pass from one S / P / dS per tile.  At hd 128 the own K and
+// V fragments, both accumulator sets (4 x 64 registers) and the next tile's
+// Q / dO rows take ~440 registers, so that launch runs one wave per SIMD (one
+// workgroup per CU).  That measured faster than a dV launch and a dK launch of
+// 256 registers each, which recomputed S twice and left the dK launch no room
+// for the prefetch: fp32 step, dK + dV 37.4 -> 28.6 ms.
+template <bool BF16, int HD, typename TIN>
+__global__ __launch_bounds__(kThreads, HD <= 64 ? 2 : 1) void fa_bwd_dkv_k(float* dk, float* dv, const TIN* q, const TIN* k,
                                                          const TIN* v, const TIN* dout, const float* lse,
                                                          const float* dbuf, int B, int T, int H, int window,
                                                          float scale_log2, float scale) {
@@ -529,10 +478,9 @@ __global__ __launch_bounds__(kThreads, (HD <= 64 || MODE != 0) ? 2 : 1) void fa_
     const int64_t rs = (int64_t)H * HD;
     const int64_t boff = (int64_t)b * T * rs + (int64_t)h * HD;
 
-    constexpr bool DOV = MODE != 2, DOK = MODE != 1;
-    typename A::Frag kf[HD / A::KS], vf[DOK ? HD / A::KS : 1];
+    typename A::Frag kf[HD / A::KS], vf[HD / A::KS];
     load_bfrags<BF16, HD>(kf, k + boff, rs, my_k, T, lane);
-    if constexpr (DOK) load_bfrags<BF16, HD>(vf, v + boff, rs, my_k, T, lane);
+    load_bfrags<BF16, HD>(vf, v + boff, rs, my_k, T, lane);
 
     f32x16 dka[HD / 32], dva[HD / 32];
 #pragma unroll
@@ -543,11 +491,8 @@ __global__ __launch_bounds__(kThreads, (HD <= 64 || MODE != 0) ? 2 : 1) void fa_
     const int qstart = (k0 / kTile) * kTile;
     int qend = T;
     if (window > 0 && k0 + kOwn - 1 + window + 1 < T) qend = k0 + kOwn - 1 + window + 1;
-    // Every launch but the split dK one loads the next Q / dO tile and its
-    // LSE / D values into registers while this tile's MFMAs run; the split dK
-    // launch (256 registers at hd 128) has no room and loads each tile when it
-    // starts.
-    constexpr bool PF = MODE != 2;
+    // The next Q / dO tile and its LSE / D values are loaded into registers
+    // while this tile's MFMAs run, and written to LDS after the barrier.
     TileVals<BF16, HD, TIN> nq, nd;
     float nl = 0.f, ndl = 0.f;
     auto ld_load = [&](int qt0) {  // LSE / D of query qt0 + tid (row 0 past T: masked)
@@ -558,38 +503,28 @@ __global__ __launch_bounds__(kThreads, (HD <= 64 || MODE != 0) ? 2 : 1) void fa_
             ndl = dbuf[bth];
         }
     };
-    if constexpr (PF) {
-        if (qstart < qend) {
-            nq.load(q + boff, rs, qstart, T);
-            nd.load(dout + boff, rs, qstart, T);
-            ld_load(qstart);
-        }
+    if (qstart < qend) {
+        nq.load(q + boff, rs, qstart, T);
+        nd.load(dout + boff, rs, qstart, T);
+        ld_load(qstart);
     }
     for (int qt0 = qstart; qt0 < qend; qt0 += kTile) {
-        if constexpr (PF) {
-            nq.write(sQ, qt0, T);
-            nd.write(sD, qt0, T);
-        } else {
-            load_tile<BF16, HD>(sQ, sQT, q + boff, rs, qt0, T, true);
-            load_tile<BF16, HD>(sD, sDT, dout + boff, rs, qt0, T, true);
-            ld_load(qt0);
-        }
+        nq.write(sQ, qt0, T);
+        nd.write(sD, qt0, T);
         if (threadIdx.x < kTile) {
             sL[threadIdx.x] = nl * kLog2e;
             sDl[threadIdx.x] = ndl;
         }
         __syncthreads();
-        if constexpr (PF) {
-            if (qt0 + kTile < qend) {
-                nq.load(q + boff, rs, qt0 + kTile, T);
-                nd.load(dout + boff, rs, qt0 + kTile, T);
-                ld_load(qt0 + kTile);
-            }
+        if (qt0 + kTile < qend) {
+            nq.load(q + boff, rs, qt0 + kTile, T);
+            nd.load(dout + boff, rs, qt0 + kTile, T);
+            ld_load(qt0 + kTile);
         }
         const bool skip = qt0 + kTile - 1 < kw || (window > 0 && qt0 > kw + 31 + window) || kw >= T;
         if (!skip) {
             // the two 32-query halves one after the other (not unrolled: at
-            // hd 128 the dK launch has no registers for two halves in flight)
+            // hd 128 two halves in flight would spill)
 #pragma unroll 1
             for (int qb = 0; qb < 2; ++qb) {
                 f32x16 s, dp;
@@ -600,11 +535,9 @@ __global__ __launch_bounds__(kThreads, (HD <= 64 || MODE != 0) ? 2 : 1) void fa_
 #pragma unroll
                 for (int ks = 0; ks < HD / A::KS; ++ks) {
                     s = A::mma(A::rowfrag(qrow, ks, lane), kf[ks], s);
-                    if constexpr (DOK) dp = A::mma(A::rowfrag(drow, ks, lane), vf[ks], dp);
+                    dp = A::mma(A::rowfrag(drow, ks, lane), vf[ks], dp);
                 }
-                // s, dp: lane holds key my_k, queries qt0 + 32qb + acc_row(e).
-                // MODE 0 keeps P and dS; the split launches each need one of
-                // them and form it in place in s.
+                // s, dp: lane holds key my_k, queries qt0 + 32qb + acc_row(e)
                 f32x16 p, ds;
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
@@ -612,24 +545,18 @@ __global__ __launch_bounds__(kThreads, (HD <= 64 || MODE != 0) ? 2 : 1) void fa_
                     const int qq = qt0 + qr;
                     const bool ok = my_k <= qq && qq < T && my_k < T && (window <= 0 || my_k >= qq - window);
                     const float pv = ok ? exp2_hw(s[e] * scale_log2 - sL[qr]) : 0.f;
-                    if constexpr (MODE == 0) {
-                        p[e] = pv;
-                        ds[e] = pv * (dp[e] - sDl[qr]);
-                    } else if constexpr (MODE == 1) {
-                        s[e] = pv;
-                    } else {
-                        s[e] = pv * (dp[e] - sDl[qr]);
-                    }
+                    p[e] = pv;
+                    ds[e] = pv * (dp[e] - sDl[qr]);
                 }
 #pragma unroll
                 for (int st = 0; st < A::STEPS32; ++st) {
-                    const typename A::Frag pb = A::accfrag(MODE == 0 ? p : s, st);
-                    const typename A::Frag db = A::accfrag(MODE == 0 ? ds : s, st);
+                    const typename A::Frag pb = A::accfrag(p, st);
+                    const typename A::Frag db = A::accfrag(ds, st);
 #pragma unroll
                     for (int dt = 0; dt < HD / 32; ++dt) {
                         const int d = dt * 32 + (lane & 31);
-                        if constexpr (DOV) dva[dt] = A::mma(A::permfrag(sD, LDN, sDT, d, qb, st, lane), pb, dva[dt]);
-                        if constexpr (DOK) dka[dt] = A::mma(A::permfrag(sQ, LDN, sQT, d, qb, st, lane), db, dka[dt]);
+                        dva[dt] = A::mma(A::permfrag(sD, LDN, sDT, d, qb, st, lane), pb, dva[dt]);
+                        dka[dt] = A::mma(A::permfrag(sQ, LDN, sQT, d, qb, st, lane), db, dka[dt]);
                     }
                 }
             }
@@ -637,8 +564,8 @@ __global__ __launch_bounds__(kThreads, (HD <= 64 || MODE != 0) ? 2 : 1) void fa_
         __syncthreads();
     }
     float* scratch = reinterpret_cast<float*>(smem_raw) + wave * 32 * 36;
-    if constexpr (DOK) store_rows_T<HD>(dk + boff, rs, kw, T, dka, scale, scratch, lane);
-    if constexpr (DOV) store_rows_T<HD>(dv + boff, rs, kw, T, dva, 1.0f, scratch, lane);
+    store_rows_T<HD>(dk + boff, rs, kw, T, dka, scale, scratch, lane);
+    store_rows_T<HD>(dv + boff, rs, kw, T, dva, 1.0f, scratch, lane);
 }
 
 template <bool BF16, int HD>
@@ -686,15 +613,8 @@ static int32_t attn_dispatch_hd(hipStream_t st, AttnOp op, float* o1, float* o2,
         return check_launch("flash_attn_bwd_dq");
     }
     const size_t lds = dkv_lds<BF16, HD>();
-    if (HD == 128 && BF16) {
-        fa_bwd_dkv_k<BF16, HD, TIN, 1><<<grid, kThreads, lds, st>>>(o1, o2, q, k, v, dout, lse, dbuf, B, T, H,
-                                                                    window, scale_log2, scale);
-        fa_bwd_dkv_k<BF16, HD, TIN, 2><<<grid, kThreads, lds, st>>>(o1, o2, q, k, v, dout, lse, dbuf, B, T, H,
-                                                                    window, scale_log2, scale);
-    } else {
-        fa_bwd_dkv_k<BF16, HD, TIN, 0><<<grid, kThreads, lds, st>>>(o1, o2, q, k, v, dout, lse, dbuf, B, T, H,
-                                                                    window, scale_log2, scale);
-    }
+    fa_bwd_dkv_k<BF16, HD, TIN><<<grid, kThreads, lds, st>>>(o1, o2, q, k, v, dout, lse, dbuf, B, T, H, window,
+                                                             scale_log2, scale);
     return check_launch("flash_attn_bwd_dkv");
 }
 
